@@ -1,0 +1,244 @@
+"""Benchmark of the grouped MoE combine (forward + backward) on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload gigachat] [--mode det|atomic]
+
+A step is one pass of the hot path over one batch: the public autograd entry point
+``grouped_weighted_scatter_add`` (metadata build, plan build, forward kernel) followed by
+``torch.autograd.grad`` through it (backward kernel: grad of every expert buffer and of the
+gates).  Inputs are synthetic (seeded) and resident in HBM before the timed region.  The default
+workload is BASELINE.json's headline configuration: T=4096 tokens, D=16384, E=256 experts, top-8,
+bf16 expert outputs, fp32 gates (the "gigachat" workload of fastmoe_amd.workloads).
+
+Prints ONE JSON line.  ``value`` = algorithmic (compulsory) bytes of forward + backward per step
+divided by the measured step time, in GB/s (1e9 B/s).  ``roofline`` reports the dominant kernel
+(the backward) from HIP events recorded around its launch inside the timed region, on the stream
+it runs on.  ``cpu_baseline`` times the reference's CPU algorithm (oracle/torch_ref.py) on a
+bounded sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+METRIC = "combine fwd+bwd GB/s & % HBM peak at D=16384,E=256,top-8 bf16; latency ms"
+
+
+class EventTimer:
+    """Brackets each C-ABI launch with HIP events on the current (launch) stream."""
+
+    def __init__(self):
+        import torch
+
+        self.torch = torch
+        self.records = []
+        self.enabled = False
+
+    def span(self, name):
+        timer = self
+
+        class _Span:
+            def __enter__(self_inner):
+                if timer.enabled:
+                    self_inner.a = timer.torch.cuda.Event(enable_timing=True)
+                    self_inner.a.record()
+                return self_inner
+
+            def __exit__(self_inner, *exc):
+                if timer.enabled:
+                    b = timer.torch.cuda.Event(enable_timing=True)
+                    b.record()
+                    timer.records.append((name, self_inner.a, b))
+                return False
+
+        return _Span()
+
+    def summary(self):
+        out = {}
+        for name, a, b in self.records:
+            out.setdefault(name, []).append(a.elapsed_time(b) * 1e3)  # us
+        return {k: {"launches": len(v), "avg_us": statistics.fmean(v),
+                    "median_us": statistics.median(v)} for k, v in out.items()}
+
+
+def _cpu_baseline(wl, sample_tokens: int, reps: int):
+    """The reference's CPU combine (cat/mul/index_add_ + index_select/mul/split + gate dot) on a
+    T=sample_tokens slice of the workload's routing recipe, all host threads."""
+    import torch
+
+    from fastmoe_amd.workloads import algorithmic_bytes, make_experts, make_routing
+    from oracle import torch_ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    idx, w, counts = make_routing(wl, sample_tokens)
+    xs = make_experts(counts, wl.D, wl.dtype, "cpu", wl.seed)
+    go = torch.randn(sample_tokens, wl.D, generator=torch.Generator().manual_seed(1)).to(wl.dtype)
+    N = idx.numel()
+    xb = torch.empty(0, dtype=wl.dtype).element_size()
+    fwd_b, bwd_b = algorithmic_bytes(sample_tokens, wl.D, N, xb, xb)
+    torch_ref.fwd_bwd_step(xs, idx, w, go, sample_tokens)  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        torch_ref.fwd_bwd_step(xs, idx, w, go, sample_tokens)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round((fwd_b + bwd_b) / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{wl.name} routing recipe at T={sample_tokens} tokens (N={N} rows), D={wl.D}, "
+                   f"E={wl.E}, top-{wl.k}, {str(wl.dtype).replace('torch.', '')}; forward+backward "
+                   f"of the reference CPU algorithm (oracle/torch_ref.fwd_bwd_step); median of "
+                   f"{reps} after 1 warm-up; {med * 1e3:.1f} ms per step"),
+        "ms_per_step": round(med * 1e3, 3),
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="gigachat")
+    ap.add_argument("--mode", default="det", choices=["det", "atomic"])
+    ap.add_argument("--fwd-only", action="store_true", help="time the forward alone")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=512)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the combine is rank-local "
+                                   "(each rank combines its own tokens after the expert-parallel "
+                                   "all-to-all); run with --gpus 1",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import torch
+
+    import fastmoe_amd
+    from fastmoe_amd import ops
+    from fastmoe_amd.workloads import WORKLOADS, algorithmic_bytes, make_experts, make_routing
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = WORKLOADS[args.workload]
+    idx, w, counts = make_routing(wl)
+    idx, w = idx.to(dev), w.to(dev)
+    xs = make_experts(counts, wl.D, wl.dtype, dev, wl.seed)
+    backward = not args.fwd_only
+    if backward:
+        xs = [x.requires_grad_(True) for x in xs]
+        w.requires_grad_(True)
+    grad_out = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
+                           generator=torch.Generator(device=dev).manual_seed(1)).to(wl.dtype)
+    xb = xs[0].element_size()
+    fwd_b, bwd_b = algorithmic_bytes(wl.T, wl.D, wl.N, xb, xb)
+    step_bytes = fwd_b + (bwd_b if backward else 0)
+    inputs = [w, *xs]
+
+    def step():
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (wl.T, wl.D), mode=args.mode)
+        if backward:
+            torch.autograd.grad(out, inputs, grad_out)
+        return out
+
+    timer = EventTimer()
+    ops._TIMER = timer
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.enabled = True
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    timer.enabled = False
+    ms = start.elapsed_time(stop) / args.steps
+    kernels = timer.summary()
+
+    dom_name = "bwd" if backward else ("fwd_det" if args.mode == "det" else "fwd_atomic")
+    dom_bytes = bwd_b if backward else fwd_b
+    dom_us = kernels[dom_name]["avg_us"]
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / f"traffic_{wl.name}_{dom_name}.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    value = step_bytes / (ms * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": str(wl.dtype).replace("torch.", "").replace("bfloat16", "bf16"),
+        "data": "synthetic (seeded top-k routing of N(0,1) logits; N(0,1) expert outputs, one "
+                "allocation per expert; fp32 softmax gates; N(0,1) grad_out)",
+        "config": {
+            "workload": wl.name, "tokens": wl.T, "hidden": wl.D, "experts": wl.E, "top_k": wl.k,
+            "rows": wl.N, "mode": args.mode, "backward": backward,
+            "fwd_bytes": fwd_b, "bwd_bytes": bwd_b if backward else 0,
+        },
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "latency_ms": round(ms, 4),
+        "tokens_per_s": round(wl.T / (ms * 1e-3), 1),
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in kernels.items()},
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": dom_bytes,
+            "avg_launch_us": round(dom_us, 3),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = _cpu_baseline(wl, args.cpu_sample_tokens, args.cpu_reps)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

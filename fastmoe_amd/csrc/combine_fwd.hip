@@ -1,0 +1,385 @@
+// Forward combine: out[idx[g], :] += w[g] * X_e[g - off[e], :]
+//
+// Replaces _launch_grouped_kernel + _grouped_weighted_scatter_add_kernel
+// (src/fastmoe/kernels/ops.py:277-310, :57-194).  Two modes:
+//
+// DET (token-major).  A wave owns one (token, column chunk).  It walks the token's plan segment in
+// ascending packed-row order, loads 16 bytes per lane per row straight from each expert's buffer
+// (the record carries the row address), multiplies by the gate in fp32, adds into fp32 registers
+// and writes the output chunk once.  Every output byte is written exactly once and every expert
+// byte read exactly once, so HBM traffic equals the compulsory bytes; no zero-fill is needed and
+// the result is bit-identical run to run (and, in fp32, to the CPU index_add_ path, which adds the
+// rounded products in the same ascending order).
+//
+// ATOMIC (packed-row-major, the reference kernel's order).  A wave owns one (row g, column chunk):
+// binary-searches g's expert in the offsets (ops.py:151-154 does offsets + program id instead),
+// loads the row, scales it and adds it into out[idx[g]] with gfx950 hardware float atomics
+// (global_atomic_add_f32, global_atomic_pk_add_bf16 / _f16 on element pairs).  Needs a zero-filled
+// out and is not reproducible bit for bit.
+#include "common.h"
+
+namespace fmoe {
+
+// Column bookkeeping of one wave unit: lane's first column of each of its U vectors.  In a
+// partial (tail) chunk the load address is clamped into the row so that every load can be issued
+// unconditionally; only the stores are predicated.
+template <int V, int U, bool FULL>
+struct Cols {
+  int64_t col[U];
+  int64_t ld[U];
+  __device__ __forceinline__ Cols(int64_t c0, int64_t D) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      col[u] = c0 + (int64_t)u * kWave * V;
+      ld[u] = FULL ? col[u] : (col[u] < D ? col[u] : D - V);
+    }
+  }
+  __device__ __forceinline__ bool ok(int u, int64_t D) const { return FULL || col[u] < D; }
+};
+
+template <typename TX, typename TO, int V, int U, bool FULL, bool AL>
+__device__ __forceinline__ void fwd_det_body(const int32_t* __restrict__ row_ptr,
+                                             const Rec* __restrict__ rec, TO* __restrict__ out,
+                                             int64_t out_stride, int64_t D, uint32_t t,
+                                             uint32_t chunk, int accumulate) {
+  using raw_t = typename Vec<TX, V>::raw_t;
+  constexpr int CW = kWave * V * U;
+  const int lane = threadIdx.x & (kWave - 1);
+  const Cols<V, U, FULL> c((int64_t)chunk * CW + (int64_t)lane * V, D);
+  const int beg = row_ptr[t];
+  const int end = row_ptr[t + 1];
+  TO* orow = out + (int64_t)t * out_stride;
+
+  float acc[U][V];
+  if (accumulate) {
+    if (beg == end) return;  // nothing routed here: out keeps its contents
+#pragma unroll
+    for (int u = 0; u < U; ++u) ld_cvt_out<TO, V>(orow + c.ld[u], acc[u]);
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[u][v] = 0.f;
+  }
+
+  int j = beg;
+  // Two rows per iteration: 2*U independent 16-byte loads in flight before the first add; the
+  // adds still happen in ascending row order.
+  for (; j + 2 <= end; j += 2) {
+    const Rec r0 = rec[j];
+    const Rec r1 = rec[j + 1];
+    raw_t a[U], b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      a[u] = load_x<TX, V, AL>(r0.src, c.ld[u]);
+      b[u] = load_x<TX, V, AL>(r1.src, c.ld[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float x[V];
+      Vec<TX, V>::cvt(a[u], x);
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * r0.w;
+      Vec<TX, V>::cvt(b[u], x);
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * r1.w;
+    }
+  }
+  if (j < end) {
+    const Rec r0 = rec[j];
+    raw_t a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) a[u] = load_x<TX, V, AL>(r0.src, c.ld[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float x[V];
+      Vec<TX, V>::cvt(a[u], x);
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * r0.w;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (c.ok(u, D)) Vec<TO, V>::st(orow + c.col[u], acc[u]);
+}
+
+template <typename TX, typename TO, int V, int U, bool FULL>
+__global__ __launch_bounds__(kGroup) void k_fwd_det(const int32_t* __restrict__ status,
+                                                    const int32_t* __restrict__ row_ptr,
+                                                    const Rec* __restrict__ rec,
+                                                    TO* __restrict__ out, int64_t out_stride,
+                                                    int64_t D, uint32_t T, uint32_t chunks,
+                                                    int accumulate) {
+  const uint32_t unit = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave);
+  const uint32_t t = unit / chunks;
+  if (t >= T) return;
+  const uint32_t chunk = unit - t * chunks;
+  if (V > 1 && status[kStatusMisaligned] != 0)
+    fwd_det_body<TX, TO, V, U, FULL, false>(row_ptr, rec, out, out_stride, D, t, chunk, accumulate);
+  else
+    fwd_det_body<TX, TO, V, U, FULL, true>(row_ptr, rec, out, out_stride, D, t, chunk, accumulate);
+}
+
+// ---- atomics ---------------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+template <typename TO, int V> struct AtomicVec;
+template <int V> struct AtomicVec<float, V> {
+  static __device__ __forceinline__ void add(float* p, const float* f) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) unsafeAtomicAdd(p + v, f[v]);
+  }
+};
+// 16-bit outputs: packed atomics on element pairs, so the vector path only (V even, rows and
+// pairs 4-byte aligned); the host refuses atomic mode with a 16-bit output otherwise.
+template <int V> struct AtomicVec<bf16_t, V> {
+  static_assert(V % 2 == 0, "packed bf16 atomics need element pairs");
+  static __device__ __forceinline__ void add(bf16_t* p, const float* f) {
+#pragma unroll
+    for (int v = 0; v < V; v += 2) {
+      bf16x2_t x;
+      x.x = (__bf16)f[v];
+      x.y = (__bf16)f[v + 1];
+      __builtin_amdgcn_global_atomic_fadd_v2bf16(reinterpret_cast<bf16x2_t*>(p + v), x);
+    }
+  }
+};
+template <int V> struct AtomicVec<f16_t, V> {
+  static_assert(V % 2 == 0, "packed f16 atomics need element pairs");
+  static __device__ __forceinline__ void add(f16_t* p, const float* f) {
+#pragma unroll
+    for (int v = 0; v < V; v += 2) {
+      f16x2_t x;
+      x.x = (_Float16)f[v];
+      x.y = (_Float16)f[v + 1];
+      __builtin_amdgcn_global_atomic_fadd_v2f16(reinterpret_cast<f16x2_t*>(p + v), x);
+    }
+  }
+};
+
+template <typename TX, typename TO, int V, int U, bool FULL, bool AL>
+__device__ __forceinline__ void fwd_atomic_body(uint64_t src, float wf, TO* __restrict__ orow,
+                                                int64_t D, uint32_t chunk) {
+  using raw_t = typename Vec<TX, V>::raw_t;
+  constexpr int CW = kWave * V * U;
+  const int lane = threadIdx.x & (kWave - 1);
+  const Cols<V, U, FULL> c((int64_t)chunk * CW + (int64_t)lane * V, D);
+  raw_t a[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) a[u] = load_x<TX, V, AL>(src, c.ld[u]);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float x[V];
+    Vec<TX, V>::cvt(a[u], x);
+#pragma unroll
+    for (int v = 0; v < V; ++v) x[v] = x[v] * wf;
+    if (c.ok(u, D)) AtomicVec<TO, V>::add(orow + c.col[u], x);
+  }
+}
+
+template <typename TX, typename TO, int V, int U, bool FULL>
+__global__ __launch_bounds__(kGroup) void k_fwd_atomic(
+    const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
+    const void* __restrict__ idx, int idx_dtype, const void* __restrict__ w, int w_dtype,
+    TO* __restrict__ out, int64_t out_stride, int64_t D, uint32_t N, int64_t T, uint32_t chunks) {
+  const uint32_t unit = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave);
+  const uint32_t g = unit / chunks;
+  if (g >= N) return;
+  const uint32_t chunk = unit - g * chunks;
+  const int64_t t = load_index(idx, idx_dtype, g);
+  if (t < 0 || t >= T) return;  // out-of-range rows are dropped (the plan counts them)
+  const int64_t e = expert_of_row(offsets, E, g);
+  const uint64_t src = (uint64_t)ptr_table[e] + (uint64_t)((g - offsets[e]) * D) * sizeof(TX);
+  const float wf = load_weight(w, w_dtype, g);
+  TO* orow = out + t * out_stride;
+  if (V > 1 && (src & 15) != 0)
+    fwd_atomic_body<TX, TO, V, U, FULL, false>(src, wf, orow, D, chunk);
+  else
+    fwd_atomic_body<TX, TO, V, U, FULL, true>(src, wf, orow, D, chunk);
+}
+
+// ---- host dispatch ---------------------------------------------------------------------------
+static int env_int(const char* name, int dflt) {
+  const char* s = getenv(name);
+  return (s && *s) ? atoi(s) : dflt;
+}
+
+// Vectors per lane per row: several 16-byte loads in flight per row, and preferably a chunk
+// width that divides D (no tail predication), while small D still spreads over many waves.
+static int pick_u(int64_t D, int V, const char* env) {
+  const int forced = env_int(env, 0);
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  for (int u = 4; u >= 1; u >>= 1) {
+    const int64_t cw = (int64_t)kWave * V * u;
+    if (D % cw == 0 && D / cw >= (u == 1 ? 1 : 2)) return u;
+  }
+  if (D >= (int64_t)kWave * V * 4 * 2) return 4;
+  if (D >= (int64_t)kWave * V * 2) return 2;
+  return 1;
+}
+
+static int grid_for(int64_t units, const char* who, unsigned* blocks) {
+  const int64_t b = (units + kWavesPerGroup - 1) / kWavesPerGroup;
+  if (units >= (int64_t(1) << 32) - kWavesPerGroup || b >= (int64_t(1) << 31)) {
+    fmoe_host::set_error("%s: grid too large (%lld wave units)", who, (long long)units);
+    return FMOE_ERANGE;
+  }
+  *blocks = (unsigned)b;
+  return FMOE_OK;
+}
+
+struct FwdArgs {
+  int mode;
+  const int32_t* status;
+  const int32_t* row_ptr;
+  const Rec* rec;
+  const void* idx;
+  int idx_dtype;
+  const void* w;
+  int w_dtype;
+  const int64_t* ptr_table;
+  const int64_t* offsets;
+  int64_t E, N, T, D;
+  void* out;
+  int64_t out_stride;
+  int accumulate;
+  hipStream_t s;
+};
+
+template <typename TX, typename TO, int V, int U, bool FULL>
+static int launch_fwd_k(const FwdArgs& a, int64_t chunks) {
+  unsigned blocks;
+  if (a.mode == FMOE_MODE_DET) {
+    if (int rc = grid_for(a.T * chunks, "fmoe_combine_fwd(det)", &blocks)) return rc;
+    hipLaunchKernelGGL((k_fwd_det<TX, TO, V, U, FULL>), dim3(blocks), dim3(kGroup), 0, a.s,
+                       a.status, a.row_ptr, a.rec, static_cast<TO*>(a.out), a.out_stride, a.D,
+                       (uint32_t)a.T, (uint32_t)chunks, a.accumulate);
+    return fmoe_host::check_launch("fmoe_combine_fwd(det)");
+  }
+  if constexpr (V == 1 && sizeof(TO) == 2) {
+    fmoe_host::set_error(
+        "fmoe_combine_fwd(atomic): a 16-bit output needs D %% %d == 0 and %d-byte aligned output "
+        "rows (packed atomics on element pairs); use the deterministic mode",
+        vec16<TX>(), vec16<TX>() * 2);
+    return FMOE_EINVAL;
+  } else {
+    if (int rc = grid_for(a.N * chunks, "fmoe_combine_fwd(atomic)", &blocks)) return rc;
+    hipLaunchKernelGGL((k_fwd_atomic<TX, TO, V, U, FULL>), dim3(blocks), dim3(kGroup), 0, a.s,
+                       a.ptr_table, a.offsets, a.E, a.idx, a.idx_dtype, a.w, a.w_dtype,
+                       static_cast<TO*>(a.out), a.out_stride, a.D, (uint32_t)a.N, a.T,
+                       (uint32_t)chunks);
+    return fmoe_host::check_launch("fmoe_combine_fwd(atomic)");
+  }
+}
+
+template <typename TX, typename TO, int V, int U>
+static int launch_fwd_u(const FwdArgs& a) {
+  const int64_t CW = (int64_t)kWave * V * U;
+  const int64_t chunks = (a.D + CW - 1) / CW;
+  if constexpr (V > 1) {
+    if (a.D % CW == 0) return launch_fwd_k<TX, TO, V, U, true>(a, chunks);
+  }
+  return launch_fwd_k<TX, TO, V, U, false>(a, chunks);
+}
+
+template <typename TX, typename TO, int V>
+static int launch_fwd_v(const FwdArgs& a) {
+  if constexpr (V == 1) {
+    return launch_fwd_u<TX, TO, 1, 4>(a);
+  } else {
+    const int U = pick_u(a.D, V, a.mode == FMOE_MODE_DET ? "FMOE_FWD_DET_U" : "FMOE_FWD_ATOMIC_U");
+    if (U == 4) return launch_fwd_u<TX, TO, V, 4>(a);
+    if (U == 2) return launch_fwd_u<TX, TO, V, 2>(a);
+    return launch_fwd_u<TX, TO, V, 1>(a);
+  }
+}
+
+template <typename TX, typename TO>
+static int launch_fwd_t(const FwdArgs& a) {
+  constexpr int V = vec16<TX>();
+  const int ob = (int)sizeof(TO) == 4 ? 4 : 2;
+  const int64_t vb = (int64_t)V * ob;  // bytes of one output vector
+  const bool vec_ok = (a.D % V == 0) && ((uintptr_t)a.out % vb == 0) &&
+                      ((a.out_stride * ob) % vb == 0) && env_int("FMOE_FORCE_SCALAR", 0) == 0;
+  if (vec_ok) return launch_fwd_v<TX, TO, V>(a);
+  return launch_fwd_v<TX, TO, 1>(a);
+}
+
+template <typename TX>
+static int launch_fwd_x(const FwdArgs& a, int out_dtype) {
+  switch (out_dtype) {
+    case FMOE_F32: return launch_fwd_t<TX, float>(a);
+    case FMOE_BF16: return launch_fwd_t<TX, bf16_t>(a);
+    case FMOE_F16: return launch_fwd_t<TX, f16_t>(a);
+  }
+  fmoe_host::set_error("fmoe_combine_fwd: bad out dtype %d", out_dtype);
+  return FMOE_EINVAL;
+}
+
+}  // namespace fmoe
+
+extern "C" int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indices, int idx_dtype,
+                                const void* d_weights, int w_dtype, const int64_t* d_ptr_table,
+                                const int64_t* d_offsets, int64_t num_experts, int64_t num_rows,
+                                int64_t num_tokens, int64_t hidden, int x_dtype, void* d_out,
+                                int out_dtype, int64_t out_row_stride, int accumulate,
+                                void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  FMOE_REQUIRE(mode == FMOE_MODE_DET || mode == FMOE_MODE_ATOMIC, "fmoe_combine_fwd: bad mode %d",
+               mode);
+  FMOE_REQUIRE(num_rows >= 0 && num_tokens >= 1 && hidden >= 1,
+               "fmoe_combine_fwd: bad sizes N=%lld T=%lld D=%lld", (long long)num_rows,
+               (long long)num_tokens, (long long)hidden);
+  if (num_rows >= (int64_t(1) << 31) || num_tokens >= (int64_t(1) << 30)) {
+    fmoe_host::set_error("fmoe_combine_fwd: N/T exceed the 32-bit row counters");
+    return FMOE_ERANGE;
+  }
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(x_dtype), "fmoe_combine_fwd: bad x dtype %d", x_dtype);
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(out_dtype), "fmoe_combine_fwd: bad out dtype %d",
+               out_dtype);
+  FMOE_REQUIRE(d_out != nullptr, "fmoe_combine_fwd: null out");
+  FMOE_REQUIRE(out_row_stride >= hidden, "fmoe_combine_fwd: out row stride %lld < D %lld",
+               (long long)out_row_stride, (long long)hidden);
+  FwdArgs a{};
+  a.mode = mode;
+  a.N = num_rows;
+  a.T = num_tokens;
+  a.D = hidden;
+  a.E = num_experts;
+  a.out = d_out;
+  a.out_stride = out_row_stride;
+  a.accumulate = accumulate ? 1 : 0;
+  a.s = static_cast<hipStream_t>(stream);
+  if (mode == FMOE_MODE_DET) {
+    FMOE_REQUIRE(d_plan != nullptr, "fmoe_combine_fwd(det): null plan");
+    FMOE_REQUIRE(((uintptr_t)d_plan & 255) == 0, "fmoe_combine_fwd(det): plan not 256B-aligned");
+    const char* ws = static_cast<const char*>(d_plan);
+    a.status = reinterpret_cast<const int32_t*>(ws + fmoe_plan_status_offset());
+    a.row_ptr = reinterpret_cast<const int32_t*>(ws + fmoe_plan_row_ptr_offset(a.N, a.T));
+    a.rec = reinterpret_cast<const Rec*>(ws + fmoe_plan_records_offset(a.N, a.T));
+  } else {
+    if (num_rows == 0) return FMOE_OK;
+    FMOE_REQUIRE(d_indices && d_weights && d_ptr_table && d_offsets,
+                 "fmoe_combine_fwd(atomic): null index/weight/metadata pointer");
+    FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype), "fmoe_combine_fwd: bad index dtype %d",
+                 idx_dtype);
+    FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_combine_fwd: bad weight dtype %d",
+                 w_dtype);
+    FMOE_REQUIRE(num_experts >= 1, "fmoe_combine_fwd: num_experts must be >= 1");
+    a.idx = d_indices;
+    a.idx_dtype = idx_dtype;
+    a.w = d_weights;
+    a.w_dtype = w_dtype;
+    a.ptr_table = d_ptr_table;
+    a.offsets = d_offsets;
+  }
+  switch (x_dtype) {
+    case FMOE_F32: return launch_fwd_x<float>(a, out_dtype);
+    case FMOE_BF16: return launch_fwd_x<bf16_t>(a, out_dtype);
+    case FMOE_F16: return launch_fwd_x<f16_t>(a, out_dtype);
+  }
+  fmoe_host::set_error("fmoe_combine_fwd: bad x dtype %d", x_dtype);
+  return FMOE_EINVAL;
+}

@@ -1,0 +1,285 @@
+// Plan: the token-major inverse of the scatter index, built on the device.
+//
+// The deterministic forward reduces each output row in ascending packed-row order, and the
+// backward reads grad_out[t] once for all rows routed from token t.  Both walk, per token t, the
+// rows g with idx[g] == t.  This file builds that list as CSR:
+//
+//   row_ptr[T + 2]  : segment b = [row_ptr[b], row_ptr[b + 1]); b == T holds the rows whose index
+//                     is out of range (they are dropped by the forward, zero-filled by the backward)
+//   rec[N]          : 16-byte records {source row address, fp32 gate, g}, ascending g per segment
+//
+// Steps (all on the caller's stream, no host synchronisation):
+//   1. count + scan   one 1024-thread workgroup histograms idx into LDS (T + 1 <= kLdsTokens) and
+//                     scans it; larger T fall back to zero / global-atomic count / one-block scan.
+//   2. fill           one thread per row: claims a slot in its segment with an atomic cursor and
+//                     writes its record (arbitrary order inside the segment).
+//   3. sort           one wave per segment ranks the records by g (segments are top-k sized, so a
+//                     register rank of <= 64 entries; larger segments take an O(c^2/64) path) and
+//                     writes them in order, which makes the whole plan bit-identical run to run.
+#include "common.h"
+
+namespace fmoe {
+
+constexpr int kScanThreads = 1024;
+constexpr int kLdsTokens = 33792;  // 132 KiB of LDS histogram (gfx950: 160 KiB per workgroup)
+
+struct PlanLayout {
+  int64_t status, cursor, row_ptr, rec_tmp, rec, total;
+};
+
+__host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  PlanLayout L;
+  L.status = 0;
+  L.cursor = 256;
+  L.row_ptr = L.cursor + up((T + 1) * 4);
+  L.rec_tmp = L.row_ptr + up((T + 2) * 4);
+  L.rec = L.rec_tmp + up(N * 16);
+  L.total = L.rec + up(N * 16);
+  return L;
+}
+
+// Exclusive scan of one int per thread over a 1024-thread block; *total gets the block sum.
+__device__ int block_exclusive_scan_1024(int v, int* total) {
+  __shared__ int wave_tot[kScanThreads / kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  if (lane == kWave - 1) wave_tot[wv] = incl;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kScanThreads / kWave; ++i) {
+    const int x = wave_tot[i];
+    before += (i < wv) ? x : 0;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + incl - v;
+}
+
+// Histogram + scan in LDS: one block.  bins = T + 1 <= kLdsTokens.
+__global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
+    const void* __restrict__ idx, int idx_dtype, int64_t N, int64_t T, int32_t* __restrict__ cursor,
+    int32_t* __restrict__ row_ptr, int32_t* __restrict__ status) {
+  __shared__ int hist[kLdsTokens];
+  const int nb = (int)T + 1;
+  for (int i = threadIdx.x; i < nb; i += kScanThreads) hist[i] = 0;
+  __syncthreads();
+  if (idx_dtype == FMOE_I64) {
+    const int64_t* p = static_cast<const int64_t*>(idx);
+    for (int64_t g = threadIdx.x; g < N; g += kScanThreads) {
+      const int64_t t = p[g];
+      atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
+    }
+  } else {
+    const int32_t* p = static_cast<const int32_t*>(idx);
+    for (int64_t g = threadIdx.x; g < N; g += kScanThreads) {
+      const int32_t t = p[g];
+      atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
+    }
+  }
+  __syncthreads();
+  const int per = (nb + kScanThreads - 1) / kScanThreads;
+  const int b0 = min(nb, (int)threadIdx.x * per);
+  const int b1 = min(nb, b0 + per);
+  int local = 0;
+  for (int b = b0; b < b1; ++b) local += hist[b];
+  int total;
+  int run = block_exclusive_scan_1024(local, &total);
+  for (int b = b0; b < b1; ++b) {
+    const int c = hist[b];
+    row_ptr[b] = run;
+    cursor[b] = run;
+    run += c;
+  }
+  if (threadIdx.x == 0) {
+    row_ptr[nb] = total;
+    status[kStatusInvalid] = hist[T];
+    status[kStatusMisaligned] = 0;
+  }
+}
+
+// ---- fallback for T + 1 > kLdsTokens ----------------------------------------------------------
+__global__ __launch_bounds__(kGroup) void k_plan_zero(int32_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kGroup + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+__global__ __launch_bounds__(kGroup) void k_plan_count_global(const void* __restrict__ idx,
+                                                              int idx_dtype, int64_t N, int64_t T,
+                                                              int32_t* __restrict__ cnt) {
+  const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
+  if (g >= N) return;
+  const int64_t t = load_index(idx, idx_dtype, g);
+  atomicAdd(&cnt[(t >= 0 && t < T) ? t : T], 1);
+}
+
+// In-place: cnt[b] (counts) becomes the cursor (= row_ptr[b]).
+__global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __restrict__ cnt,
+                                                                   int64_t T,
+                                                                   int32_t* __restrict__ row_ptr,
+                                                                   int32_t* __restrict__ status) {
+  const int64_t nb = T + 1;
+  constexpr int kPer = 16;
+  int carry = 0;
+  if (threadIdx.x == 0) {
+    status[kStatusInvalid] = cnt[T];
+    status[kStatusMisaligned] = 0;
+  }
+  __syncthreads();
+  for (int64_t base = 0; base < nb; base += (int64_t)kScanThreads * kPer) {
+    const int64_t b0 = base + (int64_t)threadIdx.x * kPer;
+    int v[kPer];
+    int local = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      v[i] = (b0 + i < nb) ? cnt[b0 + i] : 0;
+      local += v[i];
+    }
+    int total;
+    int run = carry + block_exclusive_scan_1024(local, &total);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (b0 + i < nb) {
+        row_ptr[b0 + i] = run;
+        cnt[b0 + i] = run;
+      }
+      run += v[i];
+    }
+    carry += total;
+  }
+  if (threadIdx.x == 0) row_ptr[nb] = carry;
+}
+
+// ---- fill -----------------------------------------------------------------------------------
+__global__ __launch_bounds__(kGroup) void k_plan_fill(
+    const void* __restrict__ idx, int idx_dtype, const void* __restrict__ w, int w_dtype, int64_t N,
+    int64_t T, const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets,
+    int64_t E, int64_t row_bytes, int32_t* __restrict__ cursor, Rec* __restrict__ rec_tmp,
+    int32_t* __restrict__ status) {
+  const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
+  if (g >= N) return;
+  const int64_t t = load_index(idx, idx_dtype, g);
+  const int64_t b = (t >= 0 && t < T) ? t : T;
+  const int pos = atomicAdd(&cursor[b], 1);
+  const int64_t e = expert_of_row(offsets, E, g);
+  Rec r;
+  r.src = (uint64_t)ptr_table[e] + (uint64_t)((g - offsets[e]) * row_bytes);
+  r.w = load_weight(w, w_dtype, g);
+  r.g = (int32_t)g;
+  rec_tmp[pos] = r;
+  if (r.src & 15) atomicOr(&status[kStatusMisaligned], 1);
+}
+
+// ---- sort: one wave per segment ---------------------------------------------------------------
+__global__ __launch_bounds__(kGroup) void k_plan_sort(const int32_t* __restrict__ row_ptr,
+                                                      int64_t nb, const Rec* __restrict__ rec_tmp,
+                                                      Rec* __restrict__ rec) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t b = (int64_t)blockIdx.x * kWavesPerGroup + uniform(threadIdx.x / kWave);
+  if (b >= nb) return;
+  const int beg = row_ptr[b];
+  const int c = row_ptr[b + 1] - beg;
+  if (c <= kWave) {
+    Rec r;
+    int key = 0x7fffffff;
+    if (lane < c) {
+      r = rec_tmp[beg + lane];
+      key = r.g;
+    }
+    int rank = 0;
+    for (int m = 0; m < c; ++m) rank += (__shfl(key, m, kWave) < key) ? 1 : 0;
+    if (lane < c) rec[beg + rank] = r;
+    return;
+  }
+  // Large segment (only for non-top-k style indices): rank each record against all others.
+  for (int i = lane; i < c; i += kWave) {
+    const Rec r = rec_tmp[beg + i];
+    int rank = 0;
+    for (int m = 0; m < c; ++m) rank += (rec_tmp[beg + m].g < r.g) ? 1 : 0;
+    rec[beg + rank] = r;
+  }
+}
+
+}  // namespace fmoe
+
+extern "C" int64_t fmoe_plan_workspace_bytes(int64_t num_rows, int64_t num_tokens) {
+  if (num_rows < 0 || num_tokens < 1) return -1;
+  return fmoe::plan_layout(num_rows, num_tokens).total;
+}
+extern "C" int64_t fmoe_plan_status_offset(void) { return 0; }
+extern "C" int64_t fmoe_plan_row_ptr_offset(int64_t num_rows, int64_t num_tokens) {
+  return fmoe::plan_layout(num_rows, num_tokens).row_ptr;
+}
+extern "C" int64_t fmoe_plan_records_offset(int64_t num_rows, int64_t num_tokens) {
+  return fmoe::plan_layout(num_rows, num_tokens).rec;
+}
+
+extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d_weights,
+                               int w_dtype, int64_t num_rows, int64_t num_tokens,
+                               const int64_t* d_ptr_table, const int64_t* d_offsets,
+                               int64_t num_experts, int64_t row_bytes, void* d_workspace,
+                               void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  const int64_t N = num_rows, T = num_tokens, E = num_experts;
+  FMOE_REQUIRE(N >= 0, "fmoe_build_plan: num_rows must be >= 0");
+  FMOE_REQUIRE(T >= 1, "fmoe_build_plan: num_tokens must be >= 1");
+  FMOE_REQUIRE(E >= 1, "fmoe_build_plan: num_experts must be >= 1");
+  if (N >= (int64_t(1) << 31) || T >= (int64_t(1) << 30)) {
+    fmoe_host::set_error("fmoe_build_plan: N=%lld / T=%lld exceed the 32-bit row counters",
+                         (long long)N, (long long)T);
+    return FMOE_ERANGE;
+  }
+  FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype), "fmoe_build_plan: bad index dtype %d",
+               idx_dtype);
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_build_plan: bad weight dtype %d", w_dtype);
+  FMOE_REQUIRE(d_workspace && d_ptr_table && d_offsets, "fmoe_build_plan: null device pointer");
+  FMOE_REQUIRE(N == 0 || (d_indices && d_weights), "fmoe_build_plan: null indices/weights");
+  FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0, "fmoe_build_plan: workspace not 256B-aligned");
+  FMOE_REQUIRE(row_bytes > 0, "fmoe_build_plan: row_bytes must be > 0");
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const PlanLayout L = plan_layout(N, T);
+  char* ws = static_cast<char*>(d_workspace);
+  int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
+  int32_t* cursor = reinterpret_cast<int32_t*>(ws + L.cursor);
+  int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
+  Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
+  Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
+  const int64_t nb = T + 1;
+
+  if (nb <= kLdsTokens) {
+    hipLaunchKernelGGL(k_plan_count_scan_lds, dim3(1), dim3(kScanThreads), 0, s, d_indices,
+                       idx_dtype, N, T, cursor, row_ptr, status);
+    if (int rc = fmoe_host::check_launch("fmoe_build_plan(count_scan)")) return rc;
+  } else {
+    hipLaunchKernelGGL(k_plan_zero, dim3((unsigned)((nb + kGroup - 1) / kGroup)), dim3(kGroup), 0,
+                       s, cursor, nb);
+    if (int rc = fmoe_host::check_launch("fmoe_build_plan(zero)")) return rc;
+    if (N > 0) {
+      hipLaunchKernelGGL(k_plan_count_global, dim3((unsigned)((N + kGroup - 1) / kGroup)),
+                         dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, cursor);
+      if (int rc = fmoe_host::check_launch("fmoe_build_plan(count)")) return rc;
+    }
+    hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, cursor, T, row_ptr,
+                       status);
+    if (int rc = fmoe_host::check_launch("fmoe_build_plan(scan)")) return rc;
+  }
+  if (N == 0) return FMOE_OK;
+  hipLaunchKernelGGL(k_plan_fill, dim3((unsigned)((N + kGroup - 1) / kGroup)), dim3(kGroup), 0, s,
+                     d_indices, idx_dtype, d_weights, w_dtype, N, T, d_ptr_table, d_offsets, E,
+                     row_bytes, cursor, rec_tmp, status);
+  if (int rc = fmoe_host::check_launch("fmoe_build_plan(fill)")) return rc;
+  hipLaunchKernelGGL(k_plan_sort,
+                     dim3((unsigned)((nb + kWavesPerGroup - 1) / kWavesPerGroup)), dim3(kGroup), 0,
+                     s, row_ptr, nb, rec_tmp, rec);
+  return fmoe_host::check_launch("fmoe_build_plan(sort)");
+}

@@ -1,0 +1,421 @@
+"""Grouped pointer-indirection MoE combine: the operator API of fastmoe on gfx950 kernels.
+
+Drop-in for ``fastmoe.kernels.ops`` (src/fastmoe/kernels/ops.py): the same public names,
+argument meaning and return values --
+
+    grouped_weighted_scatter_add(expert_tensors, indices, weights, out_shape, out=None,
+                                 metadata=None)                        (ops.py:365-394)
+    weighted_scatter_add(src, indices, weights, out_shape, out=None)   (ops.py:397-398)
+    prepare_grouped_metadata(expert_tensors, device)                   (ops.py:200-271)
+    GroupedWeightedScatterAdd.apply(indices, weights, out_shape, *expert_tensors)
+                                                                       (ops.py:316-359)
+
+    out[indices[g], :] += weights[g] * cat(expert_tensors)[g, :]
+
+computed without concatenating: a device pointer table addresses every expert's own buffer.  All
+work runs in ``libfastmoe_amd.so`` (HIP, gfx950) through its C ABI on the caller's current
+stream; nothing here computes on the CPU, and there is no fallback: CPU tensors and a missing
+library raise.
+
+Differences from the reference, each deliberate:
+  * CPU tensors raise instead of running torch's ``index_add_`` (ops.py:373-384).  That CPU
+    algorithm lives in ``oracle/`` as the test checker.
+  * The backward also returns the gate gradient when ``weights.requires_grad`` (the reference
+    returns None, ops.py:358-359).
+  * ``mode`` selects the forward kernel: "det" (default; token-major, fixed-order, bit-identical
+    run to run) or "atomic" (hardware float atomics in packed-row order, like the reference's
+    Triton kernel).  The default comes from ``FASTMOE_COMBINE_MODE``.
+  * Scatter indices outside [0, T) are dropped by the forward and get zero gradient instead of
+    faulting; ``validate=True`` (or ``FASTMOE_VALIDATE=1``) raises IndexError for them at the cost
+    of one device->host synchronisation.
+"""
+from __future__ import annotations
+
+import contextlib
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import torch
+
+from . import _abi
+
+__all__ = [
+    "GroupedMetadata",
+    "GroupedWeightedScatterAdd",
+    "build_plan",
+    "grouped_weighted_scatter_add",
+    "prepare_grouped_metadata",
+    "weighted_scatter_add",
+]
+
+# Optional per-launch timer (bench.py installs one): an object with span(name) returning a
+# context manager that brackets the C-ABI launch on the current stream.
+_TIMER = None
+
+
+def _span(name: str):
+    timer = _TIMER
+    return contextlib.nullcontext() if timer is None else timer.span(name)
+
+
+_FLOAT_CODES = {torch.float32: _abi.F32, torch.bfloat16: _abi.BF16, torch.float16: _abi.F16}
+_INDEX_CODES = {torch.int64: _abi.I64, torch.int32: _abi.I32}
+_MODES = {"det": _abi.MODE_DET, "atomic": _abi.MODE_ATOMIC}
+
+
+def _mode_code(mode: Optional[str]) -> int:
+    name = (mode or os.environ.get("FASTMOE_COMBINE_MODE", "det")).lower()
+    if name not in _MODES:
+        raise ValueError(f"fastmoe_amd: unknown combine mode {name!r} (expected 'det' or 'atomic')")
+    return _MODES[name]
+
+
+def _validate_default(validate: Optional[bool]) -> bool:
+    if validate is not None:
+        return bool(validate)
+    return os.environ.get("FASTMOE_VALIDATE", "0") not in ("", "0")
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"fastmoe_amd: {what} is on {t.device}; the combine runs only on the GPU "
+            "(the reference's CPU index_add_ path is the test oracle, not a product path)"
+        )
+
+
+class GroupedMetadata(tuple):
+    """Device metadata of a list of ragged expert buffers.
+
+    Unpacks like the reference's 5-tuple ``(ptr_table, chunk_sizes, expert_offsets, max_rows,
+    num_experts)`` (ops.py:271) so code that passes it back as ``metadata=`` keeps working
+    (run_on_cloud.py:67-81).  It also keeps references to the expert tensors, so the raw addresses
+    in ``ptr_table`` stay valid as long as the metadata lives (a freed-and-reused buffer cannot be
+    read through a stale table).
+    """
+
+    def __new__(cls, ptr_table, chunk_sizes, offsets_full, max_rows, num_experts, **extra):
+        self = super().__new__(
+            cls, (ptr_table, chunk_sizes, offsets_full[:num_experts], max_rows, num_experts)
+        )
+        self.offsets_full = offsets_full  # int64[E + 1], offsets_full[E] == N
+        self.max_rows_device = extra["max_rows_device"]
+        self.tensors = tuple(extra["tensors"])
+        self.sizes = tuple(extra["sizes"])
+        self.ptrs = tuple(extra["ptrs"])
+        self.hidden = extra["hidden"]
+        self.dtype = extra["dtype"]
+        self.device = extra["device"]
+        self.num_rows = sum(self.sizes)
+        return self
+
+    def matches(self, expert_tensors: Sequence[torch.Tensor]) -> bool:
+        """True if this metadata describes exactly these buffers (same addresses and rows)."""
+        if len(expert_tensors) != len(self.ptrs):
+            return False
+        return all(
+            t.shape[0] == n and (t.data_ptr() if n else 0) == p
+            for t, p, n in zip(expert_tensors, self.ptrs, self.sizes)
+        )
+
+
+def _check_experts(expert_tensors: Sequence[torch.Tensor]):
+    if len(expert_tensors) == 0:
+        raise ValueError("fastmoe_amd: expert_tensors is empty")
+    ref = expert_tensors[0]
+    _require_cuda(ref, "expert_tensors[0]")
+    if ref.dtype not in _FLOAT_CODES:
+        raise TypeError(f"fastmoe_amd: unsupported expert dtype {ref.dtype}")
+    if ref.dim() != 2:
+        raise ValueError(f"fastmoe_amd: expert tensors must be 2-D [rows, D], got {tuple(ref.shape)}")
+    hidden = ref.shape[1]
+    for i, t in enumerate(expert_tensors):
+        if t.device != ref.device or t.dtype != ref.dtype:
+            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] differs in device/dtype from [0]")
+        if t.dim() != 2 or t.shape[1] != hidden:
+            raise ValueError(
+                f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(t.shape)}, expected [*, {hidden}]"
+            )
+        if t.shape[0] > 1 and (t.stride(1) != 1 or t.stride(0) != hidden):
+            raise ValueError(
+                f"fastmoe_amd: expert_tensors[{i}] must be row-contiguous (strides {t.stride()})"
+            )
+        if t.shape[0] == 1 and hidden > 1 and t.stride(1) != 1:
+            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] must have unit column stride")
+    return ref.dtype, ref.device, hidden
+
+
+def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None) -> GroupedMetadata:
+    """Pointer table, row counts, exclusive offsets and max_rows of the expert buffers.
+
+    Mirrors prepare_grouped_metadata (src/fastmoe/kernels/ops.py:200-271).  The table is built on
+    the device by one kernel launch whose arguments carry the (address, rows) pairs
+    (``fmoe_build_metadata``): no host staging buffer and no synchronous copy.
+    """
+    dtype, dev, hidden = _check_experts(expert_tensors)
+    if device is not None and torch.device(device).type != "cuda":
+        raise RuntimeError(f"fastmoe_amd: metadata device must be a GPU, got {device}")
+    lib = _abi.lib()
+    E = len(expert_tensors)
+    sizes = [int(t.shape[0]) for t in expert_tensors]
+    ptrs = [int(t.data_ptr()) if n > 0 else 0 for t, n in zip(expert_tensors, sizes)]
+    ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
+    chunk_sizes = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
+    max_rows_dev = torch.empty(1, dtype=torch.int32, device=dev)
+    host_ptrs = (ctypes.c_int64 * E)(*ptrs)
+    host_rows = (ctypes.c_int64 * E)(*sizes)
+    with torch.cuda.device(dev), _span("metadata"):
+        rc = lib.fmoe_build_metadata(
+            host_ptrs, host_rows, E, ptr_table.data_ptr(), chunk_sizes.data_ptr(),
+            offsets.data_ptr(), max_rows_dev.data_ptr(), _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_build_metadata")
+    return GroupedMetadata(
+        ptr_table, chunk_sizes, offsets, max(sizes), E,
+        max_rows_device=max_rows_dev, tensors=expert_tensors, sizes=sizes, ptrs=ptrs,
+        hidden=hidden, dtype=dtype, device=dev,
+    )
+
+
+def _routing_args(indices: torch.Tensor, weights: torch.Tensor, num_rows: int, dev):
+    _require_cuda(indices, "indices")
+    _require_cuda(weights, "weights")
+    if indices.device != dev or weights.device != dev:
+        raise ValueError("fastmoe_amd: indices/weights must be on the experts' device")
+    if indices.dtype not in _INDEX_CODES:
+        raise TypeError(f"fastmoe_amd: indices must be int64 or int32, got {indices.dtype}")
+    if weights.dtype not in _FLOAT_CODES:
+        raise TypeError(f"fastmoe_amd: unsupported weights dtype {weights.dtype}")
+    if indices.numel() != num_rows or weights.numel() != num_rows:
+        raise ValueError(
+            f"fastmoe_amd: len(indices)={indices.numel()} and len(weights)={weights.numel()} must "
+            f"equal the total expert rows {num_rows}"
+        )
+    return indices.reshape(-1).contiguous(), weights.reshape(-1).contiguous()
+
+
+def build_plan(meta: GroupedMetadata, indices: torch.Tensor, weights: torch.Tensor,
+               num_tokens: int, validate: Optional[bool] = None) -> torch.Tensor:
+    """Token-major inverse of ``indices`` (``fmoe_build_plan``) as an opaque uint8 device tensor.
+
+    The deterministic forward and the backward read it.  With ``validate`` it synchronises once
+    and raises IndexError if any index lies outside [0, num_tokens).
+    """
+    lib = _abi.lib()
+    N = meta.num_rows
+    idx, w = _routing_args(indices, weights, N, meta.device)
+    nbytes = lib.fmoe_plan_workspace_bytes(N, num_tokens)
+    if nbytes <= 0:
+        raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=meta.device)
+    with torch.cuda.device(meta.device), _span("plan"):
+        rc = lib.fmoe_build_plan(
+            idx.data_ptr(), _INDEX_CODES[idx.dtype], w.data_ptr(), _FLOAT_CODES[w.dtype], N,
+            num_tokens, meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(), len(meta.sizes),
+            meta.hidden * meta.tensors[0].element_size(), ws.data_ptr(),
+            _stream_handle(meta.device),
+        )
+    _abi.check(rc, "fmoe_build_plan")
+    if _validate_default(validate):
+        bad = int(plan_status(ws)[0])
+        if bad:
+            raise IndexError(
+                f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})"
+            )
+    return ws
+
+
+def plan_status(plan: torch.Tensor) -> torch.Tensor:
+    """The plan's int32 status words [invalid_index_count, misaligned_flag] (a device view)."""
+    off = _abi.lib().fmoe_plan_status_offset()
+    return plan[off: off + 8].view(torch.int32)
+
+
+def _check_out(out: torch.Tensor, num_tokens_hint, hidden: int, dev) -> None:
+    _require_cuda(out, "out")
+    if out.device != dev:
+        raise ValueError("fastmoe_amd: out must be on the experts' device")
+    if out.dtype not in _FLOAT_CODES:
+        raise TypeError(f"fastmoe_amd: unsupported out dtype {out.dtype}")
+    if out.dim() != 2 or out.shape[1] != hidden:
+        raise ValueError(f"fastmoe_amd: out must be [T, {hidden}], got {tuple(out.shape)}")
+    if hidden > 1 and out.stride(1) != 1:
+        raise ValueError("fastmoe_amd: out must have unit column stride")
+    if out.shape[0] > 1 and out.stride(0) < hidden:
+        raise ValueError("fastmoe_amd: out rows overlap")
+
+
+def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
+                idx: Optional[torch.Tensor], w: Optional[torch.Tensor], out: torch.Tensor,
+                accumulate: bool) -> None:
+    lib = _abi.lib()
+    T, D = out.shape
+    with torch.cuda.device(meta.device), _span("fwd_det" if mode == _abi.MODE_DET else "fwd_atomic"):
+        rc = lib.fmoe_combine_fwd(
+            mode,
+            plan.data_ptr() if plan is not None else None,
+            idx.data_ptr() if idx is not None else None,
+            _INDEX_CODES[idx.dtype] if idx is not None else _abi.I64,
+            w.data_ptr() if w is not None else None,
+            _FLOAT_CODES[w.dtype] if w is not None else _abi.F32,
+            meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(), len(meta.sizes),
+            meta.num_rows, T, D, _FLOAT_CODES[meta.dtype], out.data_ptr(),
+            _FLOAT_CODES[out.dtype], out.stride(0) if T > 1 else D, 1 if accumulate else 0,
+            _stream_handle(meta.device),
+        )
+    _abi.check(rc, "fmoe_combine_fwd")
+
+
+def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None, *, mode=None,
+                           validate=None):
+    """In-place combine into ``out`` (accumulates; mirrors ops.py:277-310)."""
+    if metadata is None or not isinstance(metadata, GroupedMetadata) or not metadata.matches(
+        expert_tensors
+    ):
+        metadata = prepare_grouped_metadata(expert_tensors, indices.device)
+    _check_out(out, None, metadata.hidden, metadata.device)
+    idx, w = _routing_args(indices, weights, metadata.num_rows, metadata.device)
+    if metadata.max_rows == 0:  # ops.py:286: nothing to add
+        return out
+    code = _mode_code(mode)
+    T = out.shape[0]
+    if code == _abi.MODE_DET:
+        plan = build_plan(metadata, idx, w, T, validate)
+        _launch_fwd(metadata, code, plan, None, None, out, accumulate=True)
+    else:
+        if _validate_default(validate):
+            build_plan(metadata, idx, w, T, True)
+        _launch_fwd(metadata, code, None, idx, w, out, accumulate=True)
+    return out
+
+
+def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices, weights,
+                     out_shape, expert_tensors):
+    meta = prepare_grouped_metadata(expert_tensors, indices.device)
+    shape = tuple(int(s) for s in out_shape)
+    if len(shape) != 2 or shape[1] != meta.hidden:
+        raise ValueError(f"fastmoe_amd: out_shape {shape} must be [T, {meta.hidden}]")
+    T, D = shape
+    idx, w = _routing_args(indices, weights, meta.num_rows, meta.device)
+    code = _mode_code(mode)
+    plan = build_plan(meta, idx, w, T, validate) if meta.num_rows > 0 else None
+    if plan is None:
+        out = torch.zeros(shape, dtype=meta.dtype, device=meta.device)
+    elif code == _abi.MODE_DET:
+        # Every output row is written exactly once (tokens without rows get zeros): no zero-fill.
+        out = torch.empty(shape, dtype=meta.dtype, device=meta.device)
+        _launch_fwd(meta, _abi.MODE_DET, plan, None, None, out, accumulate=False)
+    else:
+        out = torch.zeros(shape, dtype=meta.dtype, device=meta.device)
+        _launch_fwd(meta, _abi.MODE_ATOMIC, None, idx, w, out, accumulate=True)
+    ctx.save_for_backward(idx, w, *expert_tensors)
+    ctx.plan = plan
+    ctx.sizes = meta.sizes
+    ctx.num_tokens = T
+    ctx.x_dtype = meta.dtype
+    return out
+
+
+def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
+    saved = ctx.saved_tensors
+    idx, w = saved[0], saved[1]
+    experts = saved[2:]
+    need_x = any(needs_x)
+    sizes = ctx.sizes
+    if ctx.plan is None or not (needs_w or need_x):
+        gw = torch.zeros_like(w) if needs_w else None
+        gx = [torch.zeros_like(t) if n else None for t, n in zip(experts, needs_x)]
+        return gw, gx
+    N = sum(sizes)
+    T = ctx.num_tokens
+    D = experts[0].shape[1]
+    go = grad_output
+    if go.dtype != ctx.x_dtype:
+        go = go.to(ctx.x_dtype)
+    if D > 1 and go.stride(1) != 1:
+        go = go.contiguous()
+    dev = go.device
+    gx = torch.empty((N, D), dtype=ctx.x_dtype, device=dev) if need_x else None
+    gw = torch.empty(N, dtype=w.dtype, device=dev) if needs_w else None
+    lib = _abi.lib()
+    with torch.cuda.device(dev), _span("bwd"):
+        rc = lib.fmoe_combine_bwd(
+            ctx.plan.data_ptr(), N, T, D, _FLOAT_CODES[ctx.x_dtype], go.data_ptr(),
+            _FLOAT_CODES[go.dtype], go.stride(0) if T > 1 else D,
+            gx.data_ptr() if gx is not None else None,
+            gw.data_ptr() if gw is not None else None,
+            _FLOAT_CODES[w.dtype], _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_combine_bwd")
+    if need_x:
+        parts = torch.split(gx, list(sizes))
+        grads_x = [p if n else None for p, n in zip(parts, needs_x)]
+    else:
+        grads_x = [None] * len(sizes)
+    return gw, grads_x
+
+
+class GroupedWeightedScatterAdd(torch.autograd.Function):
+    """Autograd bridge (mirrors src/fastmoe/kernels/ops.py:316-359).
+
+    forward : out = zeros(out_shape, dtype=experts[0].dtype) + combine   (ops.py:317-331)
+    backward: grad_X_e = split(grad_out[indices] * weights[:, None])     (ops.py:333-353)
+              plus grad_weights[g] = <grad_out[indices[g]], X[g]>  when weights require grad.
+    Both directions share one plan (token-major inverse of the indices) built in the forward.
+    The forward kernel is chosen by ``FASTMOE_COMBINE_MODE`` ("det" by default).
+    """
+
+    @staticmethod
+    def forward(ctx, indices, weights, out_shape, *expert_tensors):
+        return _combine_forward(ctx, None, None, indices, weights, out_shape, expert_tensors)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        gw, gx = _combine_backward(ctx, grad_output, ctx.needs_input_grad[1],
+                                   ctx.needs_input_grad[3:])
+        return (None, gw, None, *gx)
+
+
+class _GroupedCombineWithOptions(torch.autograd.Function):
+    """Same as GroupedWeightedScatterAdd with an explicit (mode, validate) first argument."""
+
+    @staticmethod
+    def forward(ctx, options, indices, weights, out_shape, *expert_tensors):
+        mode, validate = options
+        return _combine_forward(ctx, mode, validate, indices, weights, out_shape, expert_tensors)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        gw, gx = _combine_backward(ctx, grad_output, ctx.needs_input_grad[2],
+                                   ctx.needs_input_grad[4:])
+        return (None, None, gw, None, *gx)
+
+
+def grouped_weighted_scatter_add(expert_tensors, indices, weights, out_shape, out=None,
+                                 metadata=None, *, mode=None, validate=None):
+    """Public entry point (mirrors src/fastmoe/kernels/ops.py:365-394).
+
+    * ``out`` given: accumulate into it in place, outside autograd (graph-capturable; ops.py:389).
+    * otherwise: autograd path, returns a new ``[T, D]`` tensor in the experts' dtype (ops.py:394).
+    CPU tensors raise (see the module docstring).
+    """
+    _require_cuda(indices, "indices")
+    if out is not None:
+        return _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=metadata,
+                                      mode=mode, validate=validate)
+    if mode is None and validate is None:
+        return GroupedWeightedScatterAdd.apply(indices, weights, out_shape, *expert_tensors)
+    return _GroupedCombineWithOptions.apply((mode, validate), indices, weights, out_shape,
+                                            *expert_tensors)
+
+
+def weighted_scatter_add(src, indices, weights, out_shape, out=None, *, mode=None, validate=None):
+    """Single-tensor form (mirrors src/fastmoe/kernels/ops.py:397-398)."""
+    return grouped_weighted_scatter_add([src], indices, weights, out_shape, out, mode=mode,
+                                        validate=validate)

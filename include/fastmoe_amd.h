@@ -1,0 +1,163 @@
+/*
+ * fastmoe_amd.h -- C ABI of the MI355X (gfx950) grouped pointer-indirection MoE combine.
+ *
+ * The combine adds every routed row g of the ragged per-expert output buffers, scaled by its gate
+ * weight, into the token-ordered output:
+ *
+ *     out[idx[g], :] += w[g] * X_e[g - off[e], :]      for g in [off[e], off[e] + n_e)
+ *
+ * where X_e is expert e's own [n_e, D] buffer (never concatenated), off[] is the exclusive prefix
+ * sum of the row counts n_e, idx[] is the scatter index (token of each packed row) and w[] the gate
+ * weight.  The backward gives grad_X[g, :] = grad_out[idx[g], :] * w[g] and
+ * grad_w[g] = sum_d grad_out[idx[g], d] * X_e[g - off[e], d].
+ *
+ * Conventions
+ *   - Every pointer named d_* is a device pointer; host_* pointers are host memory.
+ *   - Sizes are int64_t.  `stream` is a hipStream_t passed as void* (NULL = null stream).
+ *   - Every entry point only enqueues work on `stream`: none allocates memory, none synchronises,
+ *     so a caller may capture the calls in a HIP graph.
+ *   - Return value: FMOE_OK (0) or a negative fmoe_status; fmoe_last_error() then holds a message
+ *     (thread-local, valid until the next failing call on the same thread).
+ *   - Rows whose scatter index lies outside [0, T) are never read or written through; they are
+ *     counted into the plan's status word (fmoe_plan_status_offset()) and their gradients are
+ *     written as zero.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   fmoe_build_metadata    <- prepare_grouped_metadata        src/fastmoe/kernels/ops.py:200-271
+ *   fmoe_combine_fwd       <- _launch_grouped_kernel + Triton  src/fastmoe/kernels/ops.py:277-310
+ *                             _grouped_weighted_scatter_add_kernel  ops.py:57-194
+ *   fmoe_combine_bwd       <- GroupedWeightedScatterAdd.backward    ops.py:333-359
+ *   fmoe_build_plan        <- no counterpart: the token-major inverse of the scatter index that the
+ *                             deterministic combine and the backward read (ops.py:344 gathers by
+ *                             scatter index on the fly instead)
+ */
+#ifndef FASTMOE_AMD_H
+#define FASTMOE_AMD_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define FMOE_API __attribute__((visibility("default")))
+#else
+#define FMOE_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FMOE_ABI_VERSION 1
+
+/* Element types. */
+enum fmoe_dtype {
+  FMOE_F32 = 0,
+  FMOE_BF16 = 1,
+  FMOE_F16 = 2,
+  FMOE_I64 = 3, /* scatter index only */
+  FMOE_I32 = 4  /* scatter index only */
+};
+
+/* Forward combine modes. */
+enum fmoe_mode {
+  /* Token-major: every output row is reduced in ascending packed-row order in fp32 registers and
+     written once.  Bit-identical run to run; bit-identical to the CPU index_add_ path in fp32. */
+  FMOE_MODE_DET = 0,
+  /* Packed-row-major like the reference kernel: hardware float atomics into `out`
+     (global_atomic_add_f32 / global_atomic_pk_add_bf16 / global_atomic_pk_add_f16). */
+  FMOE_MODE_ATOMIC = 1
+};
+
+enum fmoe_status {
+  FMOE_OK = 0,
+  FMOE_EINVAL = -1,   /* bad argument (null pointer, size, dtype, alignment, layout) */
+  FMOE_EHIP = -2,     /* a HIP runtime call failed */
+  FMOE_ERANGE = -3    /* a size exceeds what the kernels address (e.g. N >= 2^31) */
+};
+
+/* Version of this ABI (FMOE_ABI_VERSION). */
+FMOE_API int fmoe_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+FMOE_API const char* fmoe_last_error(void);
+
+/*
+ * Pointer table and row-count metadata of E ragged expert buffers
+ * (replaces prepare_grouped_metadata, src/fastmoe/kernels/ops.py:200-271).
+ *
+ * host_ptrs[e]  : device address of expert e's [n_e, D] row-contiguous buffer (may be 0 if n_e==0)
+ * host_rows[e]  : n_e
+ * Writes on the device:
+ *   d_ptr_table[E]        int64 addresses             (ops.py:221-224)
+ *   d_chunk_sizes[E]      int32 row counts            (ops.py:233-234)
+ *   d_offsets[E + 1]      int64 exclusive prefix sums, d_offsets[E] = sum n_e   (ops.py:247-256)
+ *   d_max_rows[1]         int32 max n_e               (ops.py:268)
+ * The table travels inside kernel arguments (no host staging buffer, no H2D copy), up to 256
+ * experts per launch.
+ */
+FMOE_API int fmoe_build_metadata(const int64_t* host_ptrs, const int64_t* host_rows, int64_t num_experts,
+                        int64_t* d_ptr_table, int32_t* d_chunk_sizes, int64_t* d_offsets,
+                        int32_t* d_max_rows, void* stream);
+
+/*
+ * Plan: token-major inverse of the scatter index.  For each token t, the packed rows g with
+ * idx[g] == t, in ascending g, each as a 16-byte record {source row address, fp32 gate, g}.
+ * Rows with an out-of-range index form one extra segment (number T) that the backward zero-fills.
+ *
+ * Workspace: fmoe_plan_workspace_bytes(N, T) bytes of device memory, 256-byte aligned, owned by the
+ * caller; no zero-fill is needed.  Layout (byte offsets from the workspace base):
+ *   fmoe_plan_status_offset()     : int32 count of out-of-range scatter indices
+ *   fmoe_plan_row_ptr_offset(N,T) : int32 row_ptr[T + 2] (segment t = [row_ptr[t], row_ptr[t+1]))
+ *   fmoe_plan_records_offset(N,T) : N sorted 16-byte records
+ *
+ * d_indices : [N] scatter index, FMOE_I64 or FMOE_I32
+ * d_weights : [N] gate weights, FMOE_F32 / FMOE_BF16 / FMOE_F16
+ * d_ptr_table, d_offsets : from fmoe_build_metadata
+ * row_bytes : D * sizeof(expert element)
+ */
+FMOE_API int64_t fmoe_plan_workspace_bytes(int64_t num_rows, int64_t num_tokens);
+FMOE_API int64_t fmoe_plan_status_offset(void);
+FMOE_API int64_t fmoe_plan_row_ptr_offset(int64_t num_rows, int64_t num_tokens);
+FMOE_API int64_t fmoe_plan_records_offset(int64_t num_rows, int64_t num_tokens);
+FMOE_API int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d_weights, int w_dtype,
+                    int64_t num_rows, int64_t num_tokens, const int64_t* d_ptr_table,
+                    const int64_t* d_offsets, int64_t num_experts, int64_t row_bytes,
+                    void* d_workspace, void* stream);
+
+/*
+ * Forward combine (replaces _launch_grouped_kernel + _grouped_weighted_scatter_add_kernel,
+ * src/fastmoe/kernels/ops.py:277-310 and :57-194).
+ *
+ * mode == FMOE_MODE_DET    : reads the plan (d_plan from fmoe_build_plan on the same inputs);
+ *                            d_indices/d_weights/d_ptr_table/d_offsets may be NULL.
+ * mode == FMOE_MODE_ATOMIC : reads d_indices/d_weights/d_ptr_table/d_offsets; d_plan may be NULL.
+ * out        : [T, D] with row stride out_row_stride (elements) and unit column stride.
+ * accumulate : 1 = add into the existing contents of out (the reference's in-place contract,
+ *              ops.py:389-390); 0 = overwrite (rows of tokens without routed rows become 0).
+ *              FMOE_MODE_ATOMIC always accumulates: the caller zero-fills out beforehand.
+ * x_dtype    : dtype of every expert buffer; out_dtype: dtype of out.
+ */
+FMOE_API int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indices, int idx_dtype,
+                     const void* d_weights, int w_dtype, const int64_t* d_ptr_table,
+                     const int64_t* d_offsets, int64_t num_experts, int64_t num_rows,
+                     int64_t num_tokens, int64_t hidden, int x_dtype, void* d_out, int out_dtype,
+                     int64_t out_row_stride, int accumulate, void* stream);
+
+/*
+ * Backward combine (replaces GroupedWeightedScatterAdd.backward, src/fastmoe/kernels/ops.py:333-359,
+ * and adds the gate gradient that the reference leaves out at :358-359).
+ *
+ * d_grad_out : [T, D] of gout_dtype, row stride gout_row_stride, unit column stride
+ * d_grad_x   : [N, D] contiguous of x_dtype (packed-row order; split per expert by the caller), or
+ *              NULL to skip it.  grad_X[g] = round_x(f32(grad_out[idx[g]]) * w[g]).
+ * d_grad_w   : [N] of gw_dtype, or NULL to skip it (then the expert buffers are not read).
+ *              grad_w[g] accumulates the D products in fp64 and rounds once.
+ */
+FMOE_API int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t num_tokens, int64_t hidden,
+                     int x_dtype, const void* d_grad_out, int gout_dtype, int64_t gout_row_stride,
+                     void* d_grad_x, void* d_grad_w, int gw_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTMOE_AMD_H */

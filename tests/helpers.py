@@ -1,0 +1,59 @@
+"""Shared helpers of the test-suite: tensor <-> numpy bit patterns and oracle drivers."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import cref
+
+CODE = {torch.float32: cref.F32, torch.bfloat16: cref.BF16, torch.float16: cref.F16}
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    """Host numpy array of a tensor's storage: fp32 as float32, bf16/f16 as uint16 bits."""
+    t = t.detach().contiguous().cpu()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """Raw bit patterns (uint16 / uint32) for exact comparisons."""
+    a = to_np(t)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def oracle_fwd(experts, idx, w, T, out_dtype, acc_init=None):
+    """Expected output bits (storage of out_dtype) and the fp32 accumulator."""
+    D = experts[0].shape[1]
+    xs = [to_np(x) for x in experts]
+    acc, bad = cref.combine_fwd(xs, to_np(idx.long()), to_np(w.float()), T, D,
+                                CODE[experts[0].dtype], acc=acc_init)
+    return cref.round_to(acc, CODE[out_dtype]), acc, bad
+
+
+def oracle_bwd(experts, idx, w, T, grad_out):
+    D = experts[0].shape[1]
+    xs = [to_np(x) for x in experts]
+    return cref.combine_bwd(xs, to_np(idx.long()), to_np(w.float()), T, D, to_np(grad_out),
+                            CODE[experts[0].dtype])
+
+
+def abs_dot(experts, idx, grad_out, T):
+    """sum_d |grad_out[idx[g], d] * X[g, d]| per row (the scale of grad_w's rounding error)."""
+    x = torch.cat([e.detach().float().cpu() for e in experts], 0).abs().double()
+    go = grad_out.detach().float().cpu().abs().double()
+    i = idx.cpu().long()
+    valid = (i >= 0) & (i < T)
+    rows = go[i.clamp(0, T - 1)]
+    return ((rows * x).sum(-1) * valid.double()).numpy()
+
+
+def abs_sum(experts, idx, w, T):
+    """sum_g |w[g] * X[g, d]| per output element (scale of reordering error of a fp32 sum)."""
+    D = experts[0].shape[1]
+    xs = [to_np(x) for x in experts]
+    code = CODE[experts[0].dtype]
+    xs_abs = [np.abs(cref.widen(x, code)) for x in xs]
+    acc, _ = cref.combine_fwd(xs_abs, to_np(idx.long()), np.abs(to_np(w.float())), T, D, cref.F32)
+    return acc

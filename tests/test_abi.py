@@ -1,0 +1,121 @@
+"""The C-ABI library loads, exports exactly what include/fastmoe_amd.h declares, and rejects bad
+arguments before touching the GPU (CPU only: no kernel is launched here)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from fastmoe_amd import _abi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fastmoe_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return set(re.findall(r"^FMOE_API\s+[\w\s\*]+?\b(fmoe_\w+)\s*\(", text, re.M))
+
+
+def test_header_declares_the_binding_table():
+    names = _declared()
+    assert names == set(_abi.SIGNATURES), names ^ set(_abi.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _abi.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.fmoe_abi_version() == _abi.ABI_VERSION
+
+
+def test_no_other_symbols_exported():
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_abi.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    assert {n for n in exported if n.startswith("fmoe_")} == _declared()
+    assert not [n for n in exported if n.startswith("_ZN4fmoe")]
+
+
+def test_plan_layout_functions():
+    lib = _abi.lib()
+    N, T = 32768, 4096
+    total = lib.fmoe_plan_workspace_bytes(N, T)
+    rp = lib.fmoe_plan_row_ptr_offset(N, T)
+    rec = lib.fmoe_plan_records_offset(N, T)
+    assert lib.fmoe_plan_status_offset() == 0
+    assert rp % 256 == 0 and rec % 256 == 0
+    assert rp >= 256 + 4 * (T + 1)
+    assert rec >= rp + 4 * (T + 2) + 16 * N
+    assert total >= rec + 16 * N
+    assert lib.fmoe_plan_workspace_bytes(-1, T) < 0
+    assert lib.fmoe_plan_workspace_bytes(N, 0) < 0
+
+
+@pytest.mark.parametrize("case", ["zero_experts", "null_table", "negative_rows", "null_ptr_rows"])
+def test_build_metadata_rejects_bad_arguments(case):
+    lib = _abi.lib()
+    ptrs = (ctypes.c_int64 * 2)(0x1000, 0x2000)
+    rows = (ctypes.c_int64 * 2)(3, 4)
+    dev = 0x10000  # never dereferenced: validation fails before any launch
+    if case == "zero_experts":
+        rc = lib.fmoe_build_metadata(ptrs, rows, 0, dev, dev, dev, dev, None)
+    elif case == "null_table":
+        rc = lib.fmoe_build_metadata(ptrs, rows, 2, None, dev, dev, dev, None)
+    elif case == "negative_rows":
+        rows[1] = -1
+        rc = lib.fmoe_build_metadata(ptrs, rows, 2, dev, dev, dev, dev, None)
+    else:
+        ptrs[0] = 0
+        rc = lib.fmoe_build_metadata(ptrs, rows, 2, dev, dev, dev, dev, None)
+    assert rc == _abi.EINVAL
+    assert lib.fmoe_last_error().decode()
+
+
+def test_combine_entry_points_reject_bad_arguments():
+    lib = _abi.lib()
+    dev = 0x10000
+    # bad mode
+    rc = lib.fmoe_combine_fwd(7, dev, None, _abi.I64, None, _abi.F32, None, None, 1, 4, 4, 8,
+                              _abi.F32, dev, _abi.F32, 8, 0, None)
+    assert rc == _abi.EINVAL and b"mode" in lib.fmoe_last_error()
+    # det without plan
+    rc = lib.fmoe_combine_fwd(_abi.MODE_DET, None, None, _abi.I64, None, _abi.F32, None, None, 1,
+                              4, 4, 8, _abi.F32, dev, _abi.F32, 8, 0, None)
+    assert rc == _abi.EINVAL
+    # out stride smaller than D
+    rc = lib.fmoe_combine_fwd(_abi.MODE_DET, dev * 256, None, _abi.I64, None, _abi.F32, None, None,
+                              1, 4, 4, 8, _abi.F32, dev, _abi.F32, 4, 0, None)
+    assert rc == _abi.EINVAL
+    # too many rows for the 32-bit counters
+    rc = lib.fmoe_combine_fwd(_abi.MODE_DET, dev * 256, None, _abi.I64, None, _abi.F32, None, None,
+                              1, 1 << 31, 4, 8, _abi.F32, dev, _abi.F32, 8, 0, None)
+    assert rc == _abi.ERANGE
+    # backward: grad_out dtype must equal the expert dtype
+    rc = lib.fmoe_combine_bwd(dev * 256, 4, 4, 8, _abi.BF16, dev, _abi.F32, 8, dev, None,
+                              _abi.F32, None)
+    assert rc == _abi.EINVAL
+    # plan: bad index dtype, unaligned workspace
+    rc = lib.fmoe_build_plan(dev, _abi.F32, dev, _abi.F32, 4, 4, dev, dev, 1, 32, dev * 256, None)
+    assert rc == _abi.EINVAL
+    rc = lib.fmoe_build_plan(dev, _abi.I64, dev, _abi.F32, 4, 4, dev, dev, 1, 32, dev + 8, None)
+    assert rc == _abi.EINVAL
+
+
+def test_check_raises_with_library_message():
+    lib = _abi.lib()
+    rc = lib.fmoe_build_metadata(None, None, 0, None, None, None, None, None)
+    with pytest.raises(ValueError, match="num_experts"):
+        _abi.check(rc, "fmoe_build_metadata")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_abi, "_LIB", None)
+    monkeypatch.setenv("FASTMOE_AMD_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(_abi.FastMoEError, match="no non-HIP fallback"):
+        _abi.lib()
+    monkeypatch.setattr(_abi, "_LIB", None)

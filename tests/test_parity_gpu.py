@@ -1,0 +1,464 @@
+"""GPU parity of the HIP combine against the C oracle (oracle/combine_ref.c).
+
+Bars:
+  * deterministic forward: bit-identical to the oracle, which adds the fp32-rounded products in
+    ascending packed-row order like torch's CPU index_add_ (ops.py:373-384), then rounds once to
+    the output dtype -- i.e. 0 ulp in fp32 and "<= 1 ulp after fp32 accumulation" in bf16/f16;
+  * atomic forward: fp32 within (k-1) * 2^-24 * sum|terms| (reordering only); 16-bit outputs with
+    packed 16-bit atomics round after every add, so within k * 2^-8 (bf16) / k * 2^-11 (f16) of
+    sum|terms|;
+  * grad_X: bit-identical (one fp32 product, one rounding, as ops.py:344-353 + autograd's cast);
+  * grad_w: within 1e-6 * sum_d |grad_out * X| of the fp64 oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import fastmoe_amd
+from fastmoe_amd import ops
+from fastmoe_amd.workloads import WORKLOADS, Workload, make_experts, make_routing
+from tests.helpers import abs_dot, abs_sum, bits, oracle_bwd, oracle_fwd, to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+# BASELINE configurations at sizes the CPU oracle finishes in about a second.
+SCALED = {
+    "plumbing": 256,    # full size
+    "mid": 512,
+    "gigachat": 256,
+    "skewed": 1024,
+    "detatomic": 1024,
+    "published": 512,
+}
+
+
+def _inputs(name: str, T: int | None = None, dtype=None):
+    wl = WORKLOADS[name]
+    T = SCALED[name] if T is None else T
+    idx, w, counts = make_routing(wl, T)
+    experts = make_experts(counts, wl.D, dtype or wl.dtype, "cpu", wl.seed)
+    return wl, T, idx, w, experts
+
+
+def _to_dev(experts, idx, w):
+    return [x.to(DEV) for x in experts], idx.to(DEV), w.to(DEV)
+
+
+@pytest.mark.parametrize("name", list(SCALED))
+def test_fwd_det_bitexact(name):
+    wl, T, idx, w, experts = _inputs(name)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), mode="det")
+    torch.cuda.synchronize()
+    assert out.dtype == wl.dtype and out.shape == (T, wl.D)
+    want, _, bad = oracle_fwd(experts, idx, w, T, wl.dtype)
+    assert bad == 0
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
+
+
+@pytest.mark.parametrize("name", list(SCALED))
+def test_fwd_atomic_within_reordering(name):
+    wl, T, idx, w, experts = _inputs(name)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), mode="atomic")
+    torch.cuda.synchronize()
+    _, acc, _ = oracle_fwd(experts, idx, w, T, torch.float32)
+    scale = abs_sum(experts, idx, w, T)
+    got = out.float().cpu().numpy()
+    k = max(2, int(np.bincount(idx.numpy(), minlength=T).max()))
+    if wl.dtype == torch.float32:
+        tol = (k - 1) * 2.0 ** -24 * scale + 1e-30
+    else:
+        tol = k * 2.0 ** -8 * scale + 2.0 ** -126
+    assert np.all(np.abs(got - acc) <= tol)
+
+
+def test_fwd_fp32_atomic_vs_det_on_published_shape():
+    """The reference's own bench shape (randint indices, fp32): det is bit-exact, atomic close."""
+    wl, T, idx, w, experts = _inputs("published")
+    xd, idd, wd = _to_dev(experts, idx, w)
+    det = torch.zeros(T, wl.D, device=DEV)
+    atom = torch.zeros(T, wl.D, device=DEV)
+    fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), out=det, mode="det")
+    fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), out=atom, mode="atomic")
+    want, acc, _ = oracle_fwd(experts, idx, w, T, torch.float32)
+    np.testing.assert_array_equal(bits(det), want.view(np.uint32))
+    rel = np.abs(atom.cpu().numpy() - acc) / (abs_sum(experts, idx, w, T) + 1e-30)
+    assert rel.max() <= 1e-6
+
+
+@pytest.mark.parametrize("name", ["plumbing", "gigachat", "skewed"])
+def test_bwd_grad_x_bitexact_grad_w_close(name):
+    wl, T, idx, w, experts = _inputs(name)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    xd = [x.requires_grad_(True) for x in xd]
+    wd.requires_grad_(True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D))
+    gen = torch.Generator().manual_seed(wl.seed + 7)
+    grad_out = torch.randn(T, wl.D, generator=gen).to(wl.dtype)
+    grads = torch.autograd.grad(out, [wd, *xd], grad_out.to(DEV))
+    gw, gxs = grads[0], grads[1:]
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, grad_out)
+    got_gx = np.concatenate([to_np(g) for g in gxs], 0)
+    np.testing.assert_array_equal(got_gx.view(np.uint32) if got_gx.dtype == np.float32 else got_gx,
+                                  want_gx.view(np.uint32) if want_gx.dtype == np.float32 else want_gx)
+    scale = abs_dot(experts, idx, grad_out, T)
+    err = np.abs(gw.double().cpu().numpy() - want_gw)
+    assert np.all(err <= 1e-6 * scale + 1e-30)
+    assert gw.dtype == wd.dtype
+
+
+def test_bwd_without_gate_grad_and_without_expert_grad():
+    wl, T, idx, w, experts = _inputs("plumbing")
+    xd, idd, wd = _to_dev(experts, idx, w)
+    grad_out = torch.randn(T, wl.D)
+    # only experts
+    xg = [x.clone().requires_grad_(True) for x in xd]
+    out = fastmoe_amd.grouped_weighted_scatter_add(xg, idd, wd, (T, wl.D))
+    gxs = torch.autograd.grad(out, xg, grad_out.to(DEV))
+    want_gx, _ = oracle_bwd(experts, idx, w, T, grad_out)
+    np.testing.assert_array_equal(np.concatenate([to_np(g) for g in gxs]).view(np.uint32),
+                                  want_gx.view(np.uint32))
+    # only the gate
+    wg = wd.clone().requires_grad_(True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wg, (T, wl.D))
+    (gw,) = torch.autograd.grad(out, [wg], grad_out.to(DEV))
+    _, want_gw = oracle_bwd(experts, idx, w, T, grad_out)
+    scale = abs_dot(experts, idx, grad_out, T)
+    assert np.all(np.abs(gw.double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
+def test_inplace_accumulates_into_out():
+    """ops.py:389-390 contract: the kernel adds into the given out (here non-zero)."""
+    wl, T, idx, w, experts = _inputs("mid", T=256)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    init = torch.randn(T, wl.D, generator=torch.Generator().manual_seed(9))
+    for mode in ("det", "atomic"):
+        out = init.to(DEV).clone()
+        meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
+        ret = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), out=out,
+                                                        metadata=meta, mode=mode)
+        assert ret is out
+        want, acc, _ = oracle_fwd(experts, idx, w, T, torch.float32, acc_init=init.numpy())
+        if mode == "det":
+            np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+        else:
+            scale = abs_sum(experts, idx, w, T) + np.abs(init.numpy())
+            assert np.all(np.abs(out.cpu().numpy() - acc) <= 8 * 2.0 ** -24 * scale + 1e-30)
+
+
+def test_det_repeatable_10x():
+    wl, T, idx, w, experts = _inputs("detatomic", T=2048)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    first = None
+    for _ in range(10):
+        out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), mode="det")
+        b = bits(out)
+        if first is None:
+            first = b
+        else:
+            np.testing.assert_array_equal(b, first)
+
+
+def test_grouping_invariance():
+    """Any split of the packed rows into expert buffers gives the same bits (det)."""
+    wl, T, idx, w, experts = _inputs("mid", T=128)
+    cat = torch.cat(experts, 0)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    a = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), mode="det")
+    one = fastmoe_amd.weighted_scatter_add(cat.to(DEV), idd, wd, (T, wl.D), mode="det")
+    parts = list(torch.split(cat, [1, 7, 0, 100, cat.shape[0] - 108]))
+    b = fastmoe_amd.grouped_weighted_scatter_add([p.contiguous().to(DEV) for p in parts], idd, wd,
+                                                 (T, wl.D), mode="det")
+    np.testing.assert_array_equal(bits(a), bits(one))
+    np.testing.assert_array_equal(bits(a), bits(b))
+
+
+def test_linearity_in_w():
+    wl, T, idx, w, experts = _inputs("plumbing")
+    xd, idd, wd = _to_dev(experts, idx, w)
+    a = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D))
+    b = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd * 2, (T, wl.D))
+    np.testing.assert_array_equal(bits(a * 2), bits(b))
+
+
+def test_edge_empty_experts_and_tokens():
+    D = 64
+    T = 10
+    sizes = [0, 3, 0, 0, 5, 0]
+    gen = torch.Generator().manual_seed(3)
+    experts = [torch.randn(n, D, generator=gen) for n in sizes]
+    idx = torch.tensor([0, 2, 2, 9, 4, 0, 2, 7])
+    w = torch.rand(8, generator=gen)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
+    want, _, _ = oracle_fwd(experts, idx, w, T, torch.float32)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+    assert torch.all(out[[1, 3, 5, 6, 8]] == 0)
+
+
+def test_edge_all_experts_empty():
+    D = 16
+    experts = [torch.empty(0, D, device=DEV) for _ in range(4)]
+    idx = torch.empty(0, dtype=torch.long, device=DEV)
+    w = torch.empty(0, device=DEV, requires_grad=True)
+    xs = [x.requires_grad_(True) for x in experts]
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (5, D))
+    assert out.shape == (5, D) and torch.all(out == 0)
+    o2 = torch.ones(5, D, device=DEV)
+    fastmoe_amd.grouped_weighted_scatter_add(experts, idx, w.detach(), (5, D), out=o2)
+    assert torch.all(o2 == 1)
+    g = torch.autograd.grad(out, [w, *xs], torch.ones(5, D, device=DEV))
+    assert g[0].shape == (0,)
+
+
+def test_edge_large_segments_randint():
+    """Many rows per token (segments > 64) take the plan's large-segment sort."""
+    D, T, N = 40, 3, 700
+    gen = torch.Generator().manual_seed(11)
+    experts = [torch.randn(n, D, generator=gen) for n in (300, 0, 400)]
+    idx = torch.randint(0, T, (N,), generator=gen)
+    w = torch.rand(N, generator=gen)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), mode="det")
+    want, _, _ = oracle_fwd(experts, idx, w, T, torch.float32)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+    xg = [x.clone().requires_grad_(True) for x in xd]
+    wg = wd.clone().requires_grad_(True)
+    go = torch.randn(T, D, generator=gen)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xg, idd, wg, (T, D))
+    g = torch.autograd.grad(out, [wg, *xg], go.to(DEV))
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, go)
+    got_gx = np.concatenate([to_np(t) for t in g[1:] if t is not None])
+    np.testing.assert_array_equal(got_gx.view(np.uint32), want_gx.view(np.uint32))
+    scale = abs_dot(experts, idx, go, T)
+    assert np.all(np.abs(g[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
+def test_edge_invalid_indices_dropped_and_flagged():
+    D, T = 32, 6
+    gen = torch.Generator().manual_seed(5)
+    experts = [torch.randn(4, D, generator=gen), torch.randn(3, D, generator=gen)]
+    idx = torch.tensor([0, -1, 5, 6, 2, 100, 2])
+    w = torch.rand(7, generator=gen)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    for mode in ("det", "atomic"):
+        out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), mode=mode)
+        want, acc, bad = oracle_fwd(experts, idx, w, T, torch.float32)
+        assert bad == 3
+        if mode == "det":
+            np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+        else:
+            np.testing.assert_allclose(out.cpu().numpy(), acc, rtol=1e-6, atol=1e-6)
+    meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
+    plan = fastmoe_amd.build_plan(meta, idd, wd, T)
+    assert int(ops.plan_status(plan)[0]) == 3
+    with pytest.raises(IndexError):
+        fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), validate=True)
+    xg = [x.clone().requires_grad_(True) for x in xd]
+    wg = wd.clone().requires_grad_(True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xg, idd, wg, (T, D))
+    go = torch.randn(T, D, generator=gen)
+    g = torch.autograd.grad(out, [wg, *xg], go.to(DEV))
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, go)
+    got = np.concatenate([to_np(t) for t in g[1:]])
+    np.testing.assert_array_equal(got.view(np.uint32), want_gx.view(np.uint32))
+    assert np.all(g[0].cpu().numpy()[[1, 3, 5]] == 0)
+
+
+@pytest.mark.parametrize("D", [100, 8, 1, 4096 + 8])
+def test_edge_odd_hidden_sizes(D):
+    """D not a multiple of the 16-byte vector (scalar path) and partial column chunks."""
+    T = 33
+    gen = torch.Generator().manual_seed(D)
+    sizes = [5, 17, 0, 11]
+    for dtype in (torch.float32, torch.bfloat16):
+        experts = [torch.randn(n, D, generator=gen).to(dtype) for n in sizes]
+        idx = torch.randint(0, T, (sum(sizes),), generator=gen)
+        w = torch.rand(sum(sizes), generator=gen)
+        xd, idd, wd = _to_dev(experts, idx, w)
+        out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), mode="det")
+        want, _, _ = oracle_fwd(experts, idx, w, T, dtype)
+        np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
+        xg = [x.clone().requires_grad_(True) for x in xd]
+        wg = wd.clone().requires_grad_(True)
+        out = fastmoe_amd.grouped_weighted_scatter_add(xg, idd, wg, (T, D))
+        go = torch.randn(T, D, generator=gen).to(dtype)
+        g = torch.autograd.grad(out, [wg, *xg], go.to(DEV))
+        want_gx, want_gw = oracle_bwd(experts, idx, w, T, go)
+        got = np.concatenate([to_np(t) for t in g[1:] if t is not None])
+        np.testing.assert_array_equal(got, want_gx)
+        scale = abs_dot(experts, idx, go, T)
+        assert np.all(np.abs(g[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
+def test_edge_misaligned_expert_buffers():
+    """Expert buffers that start 2 bytes off a 16-byte boundary (views into a larger buffer)."""
+    D, T = 64, 20
+    gen = torch.Generator().manual_seed(21)
+    sizes = [6, 9, 5]
+    experts, views = [], []
+    for n in sizes:
+        big = torch.randn(n * D + 1, generator=gen).to(torch.bfloat16).to(DEV)
+        v = big[1:].view(n, D)
+        assert v.data_ptr() % 16 != 0
+        views.append(v)
+        experts.append(v.cpu())
+    idx = torch.randint(0, T, (sum(sizes),), generator=gen)
+    w = torch.rand(sum(sizes), generator=gen)
+    idd, wd = idx.to(DEV), w.to(DEV)
+    out = fastmoe_amd.grouped_weighted_scatter_add(views, idd, wd, (T, D), mode="det")
+    want, _, _ = oracle_fwd(experts, idx, w, T, torch.bfloat16)
+    np.testing.assert_array_equal(bits(out), want)
+    meta = fastmoe_amd.prepare_grouped_metadata(views, DEV)
+    plan = fastmoe_amd.build_plan(meta, idd, wd, T)
+    assert int(ops.plan_status(plan)[1]) != 0
+    atom = fastmoe_amd.grouped_weighted_scatter_add(views, idd, wd, (T, D), mode="atomic")
+    _, acc, _ = oracle_fwd(experts, idx, w, T, torch.float32)
+    scale = abs_sum(experts, idx, w, T)
+    assert np.all(np.abs(atom.float().cpu().numpy() - acc) <= 8 * 2.0 ** -8 * scale + 1e-30)
+    wg = wd.clone().requires_grad_(True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(views, idd, wg, (T, D))
+    go = torch.randn(T, D, generator=gen).to(torch.bfloat16)
+    (gw,) = torch.autograd.grad(out, [wg], go.to(DEV))
+    _, want_gw = oracle_bwd(experts, idx, w, T, go)
+    scale = abs_dot(experts, idx, go, T)
+    assert np.all(np.abs(gw.double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
+@pytest.mark.parametrize("xdt,wdt,idt,odt", [
+    (torch.float16, torch.float32, torch.int64, torch.float16),
+    (torch.bfloat16, torch.bfloat16, torch.int32, torch.bfloat16),
+    (torch.bfloat16, torch.float32, torch.int64, torch.float32),
+    (torch.float32, torch.float32, torch.int32, torch.bfloat16),
+])
+def test_dtype_combinations(xdt, wdt, idt, odt):
+    D, T = 256, 64
+    gen = torch.Generator().manual_seed(2)
+    sizes = [20, 0, 44, 64]
+    experts = [torch.randn(n, D, generator=gen).to(xdt) for n in sizes]
+    idx = torch.randint(0, T, (sum(sizes),), generator=gen)
+    w = torch.rand(sum(sizes), generator=gen).to(wdt)
+    xd = [x.to(DEV) for x in experts]
+    out = torch.zeros(T, D, dtype=odt, device=DEV)
+    fastmoe_amd.grouped_weighted_scatter_add(xd, idx.to(idt).to(DEV), w.to(DEV), (T, D), out=out,
+                                             mode="det")
+    want, _, _ = oracle_fwd(experts, idx, w, T, odt)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
+
+
+def test_plan_matches_oracle():
+    from oracle import cref
+
+    wl, T, idx, w, experts = _inputs("skewed", T=512)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
+    plan = fastmoe_amd.build_plan(meta, idd, wd, T)
+    lib = fastmoe_amd._abi.lib()
+    N = idx.numel()
+    rp_off = lib.fmoe_plan_row_ptr_offset(N, T)
+    rec_off = lib.fmoe_plan_records_offset(N, T)
+    row_ptr = plan[rp_off: rp_off + 4 * (T + 2)].view(torch.int32).cpu().numpy()
+    rec = plan[rec_off: rec_off + 16 * N].view(torch.int64).view(N, 2).cpu()
+    want_rp, want_g = cref.plan(idx.numpy(), T)
+    np.testing.assert_array_equal(row_ptr, want_rp)
+    g = (rec[:, 1] >> 32).numpy().astype(np.int32)
+    np.testing.assert_array_equal(g, want_g)
+    wbits = (rec[:, 1] & 0xFFFFFFFF).numpy().astype(np.uint32)
+    np.testing.assert_array_equal(wbits, w.numpy()[want_g].view(np.uint32))
+    off, _ = cref.metadata(meta.sizes)
+    e_of = np.searchsorted(off, want_g, side="right") - 1
+    src = np.array([meta.ptrs[e] for e in e_of], dtype=np.int64) + (want_g - off[e_of]) * wl.D * 2
+    np.testing.assert_array_equal(rec[:, 0].numpy(), src)
+
+
+def test_metadata_matches_closed_forms():
+    gen = torch.Generator().manual_seed(8)
+    for E in (1, 7, 256, 300, 600):
+        sizes = torch.randint(0, 5, (E,), generator=gen).tolist()
+        sizes[E // 2] = 9
+        experts = [torch.zeros(n, 8, device=DEV) for n in sizes]
+        meta = fastmoe_amd.prepare_grouped_metadata(experts, DEV)
+        ptr_table, chunk_sizes, expert_offsets, max_rows, num_experts = meta
+        assert num_experts == E and max_rows == max(sizes)
+        assert chunk_sizes.cpu().tolist() == sizes
+        want_off = np.concatenate([[0], np.cumsum(sizes)])
+        np.testing.assert_array_equal(meta.offsets_full.cpu().numpy(), want_off)
+        np.testing.assert_array_equal(expert_offsets.cpu().numpy(), want_off[:E])
+        got_ptr = ptr_table.cpu().tolist()
+        assert got_ptr == [x.data_ptr() if n else 0 for x, n in zip(experts, sizes)]
+        assert int(meta.max_rows_device.item()) == max(sizes)
+
+
+def test_large_token_count_uses_global_plan_path():
+    """T + 1 above the LDS histogram capacity (33792 bins): zero / count / scan in global memory."""
+    D, T, k = 16, 40000, 2
+    wl = Workload("bigT", T, D, 16, k, torch.float32, 13, False)
+    idx, w, counts = make_routing(wl)
+    experts = make_experts(counts, D, torch.float32, "cpu", 13)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
+    want, _, _ = oracle_fwd(experts, idx, w, T, torch.float32)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+
+
+def test_graph_capture_replays():
+    """In-place launch with precomputed metadata captured in a graph (run_on_cloud.py:66-92)."""
+    wl, T, idx, w, experts = _inputs("gigachat", T=128)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
+    out_static = torch.zeros(T, wl.D, dtype=torch.float32, device=DEV)
+    fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), out=out_static, metadata=meta)
+    torch.cuda.synchronize()
+    eager = out_static.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        out_static.zero_()
+        with torch.cuda.graph(g, stream=s):
+            fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), out=out_static,
+                                                     metadata=meta)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(4):
+        out_static.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(out_static), bits(eager))
+        _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum().item()
+
+
+@pytest.mark.parametrize("name", ["gigachat"])
+def test_full_size_fwd_bwd_parity(name):
+    """The BASELINE headline config at its full size: forward bit-exact, grad_X bit-exact,
+    grad_w within 1e-6 of sum|terms|, against the C oracle."""
+    wl = WORKLOADS[name]
+    idx, w, counts = make_routing(wl)
+    xd = make_experts(counts, wl.D, wl.dtype, DEV, wl.seed)
+    idd, wd = idx.to(DEV), w.to(DEV).requires_grad_(True)
+    xg = [x.requires_grad_(True) for x in xd]
+    out = fastmoe_amd.grouped_weighted_scatter_add(xg, idd, wd, (wl.T, wl.D))
+    go = torch.randn(wl.T, wl.D, device=DEV, generator=torch.Generator(device=DEV).manual_seed(1)).to(wl.dtype)
+    grads = torch.autograd.grad(out, [wd, *xg], go)
+    experts = [x.detach().cpu() for x in xd]
+    want, _, _ = oracle_fwd(experts, idx, w, wl.T, wl.dtype)
+    np.testing.assert_array_equal(bits(out), want)
+    del want
+    want_gx, want_gw = oracle_bwd(experts, idx, w, wl.T, go.cpu())
+    got_gx = np.concatenate([to_np(g) for g in grads[1:]])
+    np.testing.assert_array_equal(got_gx, want_gx)
+    scale = abs_dot(experts, idx, go.cpu(), wl.T)
+    assert np.all(np.abs(grads[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
+def test_atomic_mode_refuses_16bit_output_without_vector_layout():
+    D, T = 100, 8
+    x = torch.randn(6, D).to(torch.bfloat16).to(DEV)
+    idx = torch.randint(0, T, (6,)).to(DEV)
+    w = torch.rand(6).to(DEV)
+    with pytest.raises(ValueError, match="deterministic"):
+        fastmoe_amd.weighted_scatter_add(x, idx, w, (T, D), mode="atomic")
