@@ -5,7 +5,11 @@
 A step is one pass of the hot path over one batch: the public autograd entry point
 ``grouped_weighted_scatter_add`` (metadata build, plan build, forward kernel) followed by
 ``torch.autograd.grad`` through it (backward kernel: grad of every expert buffer and of the
-gates).  Inputs are synthetic (seeded) and resident in HBM before the timed region.  The default
+gates).  Inputs are synthetic (seeded) and resident in HBM before the timed region.  The timed
+region replays that step captured once as a HIP graph (all of its kernels run on every replay;
+the host-side Python/autograd cost of E=256 tensors is excluded), as the reference's own kernel
+benchmark does with CUDA graphs; the eager, host-inclusive step time is reported beside it
+(``eager_ms_per_step``).  The default
 workload is BASELINE.json's headline configuration: T=4096 tokens, D=16384, E=256 experts, top-8,
 bf16 expert outputs, fp32 gates (the "gigachat" workload of fastmoe_amd.workloads).
 
@@ -124,6 +128,10 @@ def main() -> int:
     ap.add_argument("--mode", default="det", choices=["det", "atomic"])
     ap.add_argument("--fwd-only", action="store_true", help="time the forward alone")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager steps instead of graph replays")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="K",
+                    help="also run K plain 1 GiB device copies (a reference kernel of known bytes "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=512)
     ap.add_argument("--cpu-reps", type=int, default=3)
     args = ap.parse_args()
@@ -167,24 +175,84 @@ def main() -> int:
             torch.autograd.grad(out, inputs, grad_out)
         return out
 
+    if args.copy_probe:
+        a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(args.copy_probe):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
     timer = EventTimer()
     ops._TIMER = timer
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+
+    def timed(fn, n):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(n):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / n, (time.perf_counter() - t0) * 1e3 / n
+
+    # Eager steps through the public autograd API (host-inclusive: Python + autograd over E
+    # expert tensors is part of this number).
+    eager_ms, eager_wall_ms = timed(step, args.steps)
+
+    # Per-kernel durations: HIP events around every C-ABI launch, on the launch stream.  A sleep
+    # kernel first gives the GPU a backlog so that the host has enqueued each event-kernel-event
+    # triple before the GPU reaches it (the events then bracket the kernel, not host gaps).
+    timer.records.clear()
     timer.enabled = True
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record()
+    try:
+        torch.cuda._sleep(int(args.steps * 3e-3 * 2.4e9))
+        backlog = True
+    except Exception:
+        backlog = False
     for _ in range(args.steps):
         step()
-    stop.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     timer.enabled = False
-    ms = start.elapsed_time(stop) / args.steps
     kernels = timer.summary()
+    timer.records.clear()
+
+    graph_error = None
+    graph = None
+    if not args.eager:
+        # The same step captured once as a HIP graph (metadata upload, plan, forward, backward)
+        # and replayed: the timed region is pure device work, the convention of the reference's
+        # own kernel benchmark (run_on_cloud.py:66-92).
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            for _ in range(args.warmup):
+                graph.replay()
+            torch.cuda.synchronize()
+        except Exception as exc:  # capture unsupported: report eager numbers only
+            graph_error = f"{type(exc).__name__}: {exc}"
+            graph = None
+
+    if graph is not None:
+        ms, wall_ms = timed(graph.replay, args.steps)
+        timing = "hip-graph replay of one captured step"
+    else:
+        ms, wall_ms = eager_ms, eager_wall_ms
+        timing = "eager steps"
+    wall = wall_ms * args.steps / 1e3
 
     dom_name = "bwd" if backward else ("fwd_det" if args.mode == "det" else "fwd_atomic")
     dom_bytes = bwd_b if backward else fwd_b
@@ -219,6 +287,13 @@ def main() -> int:
         "latency_ms": round(ms, 4),
         "tokens_per_s": round(wl.T / (ms * 1e-3), 1),
         "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "timing": timing,
+        "eager_ms_per_step": round(eager_ms, 4),
+        "eager_value": round(step_bytes / (eager_ms * 1e-3) / 1e9, 2),
+        "eager_wall_ms_per_step": round(eager_wall_ms, 4),
+        "graph_error": graph_error,
+        "kernel_timing": "HIP events around each launch in eager steps queued behind a sleep kernel"
+                         if backlog else "HIP events around each launch in eager steps",
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in kernels.items()},
         "roofline": {

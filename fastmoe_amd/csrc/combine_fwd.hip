@@ -4,7 +4,8 @@
 // (src/fastmoe/kernels/ops.py:277-310, :57-194).  Two modes:
 //
 // DET (token-major).  A wave owns one (token, column chunk).  It walks the token's plan segment in
-// ascending packed-row order, loads 16 bytes per lane per row straight from each expert's buffer
+// ascending packed-row order (ordering a short segment in registers first), loads 16 bytes per
+// lane per row straight from each expert's buffer
 // (the record carries the row address), multiplies by the gate in fp32, adds into fp32 registers
 // and writes the output chunk once.  Every output byte is written exactly once and every expert
 // byte read exactly once, so HBM traffic equals the compulsory bytes; no zero-fill is needed and
@@ -20,41 +21,38 @@
 
 namespace fmoe {
 
-// Column bookkeeping of one wave unit: lane's first column of each of its U vectors.  In a
-// partial (tail) chunk the load address is clamped into the row so that every load can be issued
-// unconditionally; only the stores are predicated.
-template <int V, int U, bool FULL>
-struct Cols {
-  int64_t col[U];
-  int64_t ld[U];
-  __device__ __forceinline__ Cols(int64_t c0, int64_t D) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      col[u] = c0 + (int64_t)u * kWave * V;
-      ld[u] = FULL ? col[u] : (col[u] < D ? col[u] : D - V);
-    }
-  }
-  __device__ __forceinline__ bool ok(int u, int64_t D) const { return FULL || col[u] < D; }
-};
-
-template <typename TX, typename TO, int V, int U, bool FULL, bool AL>
+// Tile of one wave unit: U 16-byte vectors per lane per row (64 * V * U columns) and batches of
+// R rows, so R * U independent loads per lane are in flight before the first use.
+template <typename TX, typename TO, int V, int U, int RB, bool AL>
 __device__ __forceinline__ void fwd_det_body(const int32_t* __restrict__ row_ptr,
                                              const Rec* __restrict__ rec, TO* __restrict__ out,
-                                             int64_t out_stride, int64_t D, uint32_t t,
+                                             int64_t out_stride, uint32_t D, uint32_t t,
                                              uint32_t chunk, int accumulate) {
-  using raw_t = typename Vec<TX, V>::raw_t;
+  using VX = Vec<TX, V>;
+  using VO = Vec<TO, V>;
+  using raw_t = typename VX::raw_t;
   constexpr int CW = kWave * V * U;
+  // The misaligned-row path (element loads) takes one row at a time so that it does not set the
+  // register budget of the kernel.
+  constexpr int R = AL ? RB : 1;
   const int lane = threadIdx.x & (kWave - 1);
-  const Cols<V, U, FULL> c((int64_t)chunk * CW + (int64_t)lane * V, D);
+  const uint32_t col0 = chunk * CW + (uint32_t)lane * V;
+  uint32_t xoff[U], ooff[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    xoff[u] = (col0 + (uint32_t)u * kWave * V) * (uint32_t)sizeof(TX);
+    ooff[u] = (col0 + (uint32_t)u * kWave * V) * (uint32_t)sizeof(TO);
+  }
+  const uint32_t xrow_bytes = D * (uint32_t)sizeof(TX);
   const int beg = row_ptr[t];
   const int end = row_ptr[t + 1];
-  TO* orow = out + (int64_t)t * out_stride;
+  const rsrc_t ro = make_rsrc(out + (int64_t)t * out_stride, D * (uint32_t)sizeof(TO));
 
   float acc[U][V];
   if (accumulate) {
     if (beg == end) return;  // nothing routed here: out keeps its contents
 #pragma unroll
-    for (int u = 0; u < U; ++u) ld_cvt_out<TO, V>(orow + c.ld[u], acc[u]);
+    for (int u = 0; u < U; ++u) VO::cvt(VO::ld(ro, ooff[u]), acc[u]);
   } else {
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -62,62 +60,65 @@ __device__ __forceinline__ void fwd_det_body(const int32_t* __restrict__ row_ptr
       for (int v = 0; v < V; ++v) acc[u][v] = 0.f;
   }
 
-  int j = beg;
-  // Two rows per iteration: 2*U independent 16-byte loads in flight before the first add; the
-  // adds still happen in ascending row order.
-  for (; j + 2 <= end; j += 2) {
-    const Rec r0 = rec[j];
-    const Rec r1 = rec[j + 1];
-    raw_t a[U], b[U];
+  for (int jb = beg; jb < end; jb += kWave) {
+    const int cnt = min(end - jb, kWave);
+    LaneRecs lr;
+    lr.load(rec, jb, cnt, lane);
+    // A segment of up to 64 rows comes unordered from the plan: order it by g here.  Longer
+    // segments are already in ascending g.
+    if (end - beg <= kWave) lr.sort_by_row(cnt, lane);
+    for (int i = 0; i < cnt; i += R) {
+      // Batch of R rows; a partial batch repeats its last row for the loads (never accumulated),
+      // so every load is issued unconditionally.
+      raw_t a[R][U];
+      float wr[R];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      a[u] = load_x<TX, V, AL>(r0.src, c.ld[u]);
-      b[u] = load_x<TX, V, AL>(r1.src, c.ld[u]);
-    }
+      for (int r = 0; r < R; ++r) {
+        const int ir = min(i + r, cnt - 1);
+        const rsrc_t rx = make_rsrc(lr.src(ir), xrow_bytes);
+        wr[r] = lr.w(ir);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float x[V];
-      Vec<TX, V>::cvt(a[u], x);
+        for (int u = 0; u < U; ++u) a[r][u] = load_x<TX, V, AL>(rx, xoff[u]);
+      }
+      // Adds in ascending row order (the order of the plan segment).
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * r0.w;
-      Vec<TX, V>::cvt(b[u], x);
+      for (int r = 0; r < R; ++r) {
+        if (i + r < cnt) {
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * r1.w;
+          for (int u = 0; u < U; ++u) {
+            float x[V];
+            VX::cvt(a[r][u], x);
+#pragma unroll
+            for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * wr[r];
+          }
+        }
+      }
     }
   }
-  if (j < end) {
-    const Rec r0 = rec[j];
-    raw_t a[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = load_x<TX, V, AL>(r0.src, c.ld[u]);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float x[V];
-      Vec<TX, V>::cvt(a[u], x);
-#pragma unroll
-      for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * r0.w;
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (c.ok(u, D)) Vec<TO, V>::st(orow + c.col[u], acc[u]);
+  for (int u = 0; u < U; ++u) VO::st(ro, ooff[u], acc[u]);  // columns >= D: dropped by range check
 }
 
-template <typename TX, typename TO, int V, int U, bool FULL>
+template <typename TX, typename TO, int V, int U, int RB>
 __global__ __launch_bounds__(kGroup) void k_fwd_det(const int32_t* __restrict__ status,
                                                     const int32_t* __restrict__ row_ptr,
                                                     const Rec* __restrict__ rec,
                                                     TO* __restrict__ out, int64_t out_stride,
-                                                    int64_t D, uint32_t T, uint32_t chunks,
+                                                    uint32_t D, uint32_t T, uint32_t chunks,
                                                     int accumulate) {
-  const uint32_t unit = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave);
-  const uint32_t t = unit / chunks;
-  if (t >= T) return;
-  const uint32_t chunk = unit - t * chunks;
-  if (V > 1 && status[kStatusMisaligned] != 0)
-    fwd_det_body<TX, TO, V, U, FULL, false>(row_ptr, rec, out, out_stride, D, t, chunk, accumulate);
-  else
-    fwd_det_body<TX, TO, V, U, FULL, true>(row_ptr, rec, out, out_stride, D, t, chunk, accumulate);
+  const bool al = !(V > 1 && status[kStatusMisaligned] != 0);
+  const uint32_t units = T * chunks;
+  // Wave units (token, column chunk); a grid smaller than units / 4 strides over them.
+  for (uint32_t unit = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave);
+       unit < units; unit += gridDim.x * kWavesPerGroup) {
+    const uint32_t t = unit / chunks;
+    const uint32_t chunk = unit - t * chunks;
+    if (al)
+      fwd_det_body<TX, TO, V, U, RB, true>(row_ptr, rec, out, out_stride, D, t, chunk, accumulate);
+    else
+      fwd_det_body<TX, TO, V, U, RB, false>(row_ptr, rec, out, out_stride, D, t, chunk,
+                                            accumulate);
+  }
 }
 
 // ---- atomics ---------------------------------------------------------------------------------
@@ -158,31 +159,35 @@ template <int V> struct AtomicVec<f16_t, V> {
   }
 };
 
-template <typename TX, typename TO, int V, int U, bool FULL, bool AL>
+template <typename TX, typename TO, int V, int U, bool AL>
 __device__ __forceinline__ void fwd_atomic_body(uint64_t src, float wf, TO* __restrict__ orow,
-                                                int64_t D, uint32_t chunk) {
-  using raw_t = typename Vec<TX, V>::raw_t;
+                                                uint32_t D, uint32_t chunk) {
+  using VX = Vec<TX, V>;
+  using raw_t = typename VX::raw_t;
   constexpr int CW = kWave * V * U;
   const int lane = threadIdx.x & (kWave - 1);
-  const Cols<V, U, FULL> c((int64_t)chunk * CW + (int64_t)lane * V, D);
+  const uint32_t col0 = chunk * CW + (uint32_t)lane * V;
+  const rsrc_t rx = make_rsrc(src, D * (uint32_t)sizeof(TX));
   raw_t a[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) a[u] = load_x<TX, V, AL>(src, c.ld[u]);
+  for (int u = 0; u < U; ++u)
+    a[u] = load_x<TX, V, AL>(rx, (col0 + (uint32_t)u * kWave * V) * (uint32_t)sizeof(TX));
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    const uint32_t col = col0 + (uint32_t)u * kWave * V;
     float x[V];
-    Vec<TX, V>::cvt(a[u], x);
+    VX::cvt(a[u], x);
 #pragma unroll
     for (int v = 0; v < V; ++v) x[v] = x[v] * wf;
-    if (c.ok(u, D)) AtomicVec<TO, V>::add(orow + c.col[u], x);
+    if (col < D) AtomicVec<TO, V>::add(orow + col, x);
   }
 }
 
-template <typename TX, typename TO, int V, int U, bool FULL>
+template <typename TX, typename TO, int V, int U>
 __global__ __launch_bounds__(kGroup) void k_fwd_atomic(
     const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
     const void* __restrict__ idx, int idx_dtype, const void* __restrict__ w, int w_dtype,
-    TO* __restrict__ out, int64_t out_stride, int64_t D, uint32_t N, int64_t T, uint32_t chunks) {
+    TO* __restrict__ out, int64_t out_stride, uint32_t D, uint32_t N, int64_t T, uint32_t chunks) {
   const uint32_t unit = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave);
   const uint32_t g = unit / chunks;
   if (g >= N) return;
@@ -190,13 +195,14 @@ __global__ __launch_bounds__(kGroup) void k_fwd_atomic(
   const int64_t t = load_index(idx, idx_dtype, g);
   if (t < 0 || t >= T) return;  // out-of-range rows are dropped (the plan counts them)
   const int64_t e = expert_of_row(offsets, E, g);
-  const uint64_t src = (uint64_t)ptr_table[e] + (uint64_t)((g - offsets[e]) * D) * sizeof(TX);
+  const uint64_t src =
+      (uint64_t)ptr_table[e] + (uint64_t)((g - offsets[e]) * (int64_t)D) * sizeof(TX);
   const float wf = load_weight(w, w_dtype, g);
   TO* orow = out + t * out_stride;
   if (V > 1 && (src & 15) != 0)
-    fwd_atomic_body<TX, TO, V, U, FULL, false>(src, wf, orow, D, chunk);
+    fwd_atomic_body<TX, TO, V, U, false>(src, wf, orow, D, chunk);
   else
-    fwd_atomic_body<TX, TO, V, U, FULL, true>(src, wf, orow, D, chunk);
+    fwd_atomic_body<TX, TO, V, U, true>(src, wf, orow, D, chunk);
 }
 
 // ---- host dispatch ---------------------------------------------------------------------------
@@ -247,13 +253,15 @@ struct FwdArgs {
   hipStream_t s;
 };
 
-template <typename TX, typename TO, int V, int U, bool FULL>
+template <typename TX, typename TO, int V, int U, int RB>
 static int launch_fwd_k(const FwdArgs& a, int64_t chunks) {
   unsigned blocks;
   if (a.mode == FMOE_MODE_DET) {
     if (int rc = grid_for(a.T * chunks, "fmoe_combine_fwd(det)", &blocks)) return rc;
-    hipLaunchKernelGGL((k_fwd_det<TX, TO, V, U, FULL>), dim3(blocks), dim3(kGroup), 0, a.s,
-                       a.status, a.row_ptr, a.rec, static_cast<TO*>(a.out), a.out_stride, a.D,
+    const int persist = env_int("FMOE_FWD_GRID", 0);  // workgroups; 0 = one wave per unit
+    if (persist > 0 && (unsigned)persist < blocks) blocks = (unsigned)persist;
+    hipLaunchKernelGGL((k_fwd_det<TX, TO, V, U, RB>), dim3(blocks), dim3(kGroup), 0, a.s, a.status,
+                       a.row_ptr, a.rec, static_cast<TO*>(a.out), a.out_stride, (uint32_t)a.D,
                        (uint32_t)a.T, (uint32_t)chunks, a.accumulate);
     return fmoe_host::check_launch("fmoe_combine_fwd(det)");
   }
@@ -265,33 +273,38 @@ static int launch_fwd_k(const FwdArgs& a, int64_t chunks) {
     return FMOE_EINVAL;
   } else {
     if (int rc = grid_for(a.N * chunks, "fmoe_combine_fwd(atomic)", &blocks)) return rc;
-    hipLaunchKernelGGL((k_fwd_atomic<TX, TO, V, U, FULL>), dim3(blocks), dim3(kGroup), 0, a.s,
+    hipLaunchKernelGGL((k_fwd_atomic<TX, TO, V, U>), dim3(blocks), dim3(kGroup), 0, a.s,
                        a.ptr_table, a.offsets, a.E, a.idx, a.idx_dtype, a.w, a.w_dtype,
-                       static_cast<TO*>(a.out), a.out_stride, a.D, (uint32_t)a.N, a.T,
+                       static_cast<TO*>(a.out), a.out_stride, (uint32_t)a.D, (uint32_t)a.N, a.T,
                        (uint32_t)chunks);
     return fmoe_host::check_launch("fmoe_combine_fwd(atomic)");
   }
 }
 
-template <typename TX, typename TO, int V, int U>
+template <typename TX, typename TO, int V, int U, int RB>
 static int launch_fwd_u(const FwdArgs& a) {
   const int64_t CW = (int64_t)kWave * V * U;
   const int64_t chunks = (a.D + CW - 1) / CW;
-  if constexpr (V > 1) {
-    if (a.D % CW == 0) return launch_fwd_k<TX, TO, V, U, true>(a, chunks);
-  }
-  return launch_fwd_k<TX, TO, V, U, false>(a, chunks);
+  return launch_fwd_k<TX, TO, V, U, RB>(a, chunks);
 }
 
+// Tile shapes (U vectors per lane per row, R rows per batch).  FMOE_FWD_TILE=<U><R> (e.g. "44")
+// overrides the choice for tuning.
 template <typename TX, typename TO, int V>
 static int launch_fwd_v(const FwdArgs& a) {
   if constexpr (V == 1) {
-    return launch_fwd_u<TX, TO, 1, 4>(a);
+    return launch_fwd_u<TX, TO, 1, 4, 4>(a);
   } else {
-    const int U = pick_u(a.D, V, a.mode == FMOE_MODE_DET ? "FMOE_FWD_DET_U" : "FMOE_FWD_ATOMIC_U");
-    if (U == 4) return launch_fwd_u<TX, TO, V, 4>(a);
-    if (U == 2) return launch_fwd_u<TX, TO, V, 2>(a);
-    return launch_fwd_u<TX, TO, V, 1>(a);
+    const int tile = env_int(a.mode == FMOE_MODE_DET ? "FMOE_FWD_TILE" : "FMOE_FWD_ATOMIC_TILE", 0);
+    int U = tile / 10, R = tile % 10;
+    if (!((U == 4 && R == 4) || (U == 2 && (R == 8 || R == 4)) || (U == 1 && R == 8))) {
+      U = pick_u(a.D, V, "FMOE_FWD_DET_U");
+      R = U >= 4 ? 4 : 8;
+    }
+    if (U == 4) return launch_fwd_u<TX, TO, V, 4, 4>(a);
+    if (U == 2 && R == 4) return launch_fwd_u<TX, TO, V, 2, 4>(a);
+    if (U == 2) return launch_fwd_u<TX, TO, V, 2, 8>(a);
+    return launch_fwd_u<TX, TO, V, 1, 8>(a);
   }
 }
 
@@ -342,6 +355,10 @@ extern "C" int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indi
   FMOE_REQUIRE(d_out != nullptr, "fmoe_combine_fwd: null out");
   FMOE_REQUIRE(out_row_stride >= hidden, "fmoe_combine_fwd: out row stride %lld < D %lld",
                (long long)out_row_stride, (long long)hidden);
+  if (hidden * 4 >= (int64_t(1) << 31)) {
+    fmoe_host::set_error("fmoe_combine_fwd: D=%lld exceeds the 2 GiB row limit", (long long)hidden);
+    return FMOE_ERANGE;
+  }
   FwdArgs a{};
   a.mode = mode;
   a.N = num_rows;

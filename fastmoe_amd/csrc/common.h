@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "../../include/fastmoe_amd.h"
 
@@ -84,168 +85,223 @@ template <> __device__ __forceinline__ void st1<f16_t>(f16_t* p, float v) {
   p->bits = f32_to_f16_bits(v);
 }
 
-// ---- vector access: V elements starting at p ------------------------------------------------
-// ld() issues one global load of the raw storage (16 bytes per lane for V == 16/sizeof(T)),
-// cvt() widens it to fp32 later, so that many loads can be in flight before the first use.
-// V == 1 is the unaligned scalar path.
-#define FMOE_GLOBAL __attribute__((address_space(1)))
-
-// Native clang vector types: they load/store through address-space-1 pointers directly.
+// Native clang vector types.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+#define FMOE_GLOBAL __attribute__((address_space(1)))
 
-template <typename R, typename T>
-__device__ __forceinline__ R gload(const T* p) {
-  return *(const FMOE_GLOBAL R*)(p);
+// ---- row access through buffer descriptors ---------------------------------------------------
+// Every streamed row (an expert row, a grad_out / out / grad_X row) is addressed through a buffer
+// resource whose base is the row start and whose num_records is the row length in bytes.  Lanes
+// then use 32-bit byte offsets, the cache policy is an instruction immediate (non-temporal "nt"
+// for streaming data: on MI355X ~7.1 TB/s reads and ~6.2 TB/s copies against ~6.4 / ~5.7 TB/s
+// for the default policy), and the hardware range check makes tail columns free: loads beyond
+// the row return 0 and stores beyond it are dropped, so no lane ever touches memory outside the
+// row it was given.
+#ifndef FMOE_NT
+#define FMOE_NT 1
+#endif
+constexpr int kCPol = FMOE_NT ? 2 : 0;  // gfx950 cache-policy bit 1 = nt
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcWord3);
 }
-template <typename R, typename T>
-__device__ __forceinline__ void gstore(T* p, R v) {
-  *(FMOE_GLOBAL R*)(p) = v;
-}
-
-template <typename T, int V> struct Vec;
-
-template <> struct Vec<float, 1> {
-  using raw_t = float;
-  static __device__ __forceinline__ raw_t ld(const float* p) { return gload<float>(p); }
-  static __device__ __forceinline__ void cvt(raw_t r, float* f) { f[0] = r; }
-  static __device__ __forceinline__ void st(float* p, const float* f) { gstore<float>(p, f[0]); }
-};
-template <> struct Vec<bf16_t, 1> {
-  using raw_t = uint16_t;
-  static __device__ __forceinline__ raw_t ld(const bf16_t* p) { return gload<uint16_t>(p); }
-  static __device__ __forceinline__ void cvt(raw_t r, float* f) {
-    f[0] = __uint_as_float((uint32_t)r << 16);
-  }
-  static __device__ __forceinline__ void st(bf16_t* p, const float* f) {
-    gstore<uint16_t>(p, f32_to_bf16_bits(f[0]));
-  }
-};
-template <> struct Vec<f16_t, 1> {
-  using raw_t = uint16_t;
-  static __device__ __forceinline__ raw_t ld(const f16_t* p) { return gload<uint16_t>(p); }
-  static __device__ __forceinline__ void cvt(raw_t r, float* f) {
-    f[0] = (float)__builtin_bit_cast(_Float16, r);
-  }
-  static __device__ __forceinline__ void st(f16_t* p, const float* f) {
-    gstore<uint16_t>(p, f32_to_f16_bits(f[0]));
-  }
-};
-
-template <> struct Vec<float, 4> {
-  using raw_t = f32x4;
-  static __device__ __forceinline__ raw_t ld(const float* p) { return gload<f32x4>(p); }
-  static __device__ __forceinline__ void cvt(const raw_t& v, float* f) {
-    f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
-  }
-  static __device__ __forceinline__ void st(float* p, const float* f) {
-    gstore<f32x4>(p, f32x4{f[0], f[1], f[2], f[3]});
-  }
-};
-template <> struct Vec<float, 8> {  // output side only (8 fp32 results of one 16-bit input vector)
-  static __device__ __forceinline__ void ld_cvt(const float* p, float* f) {
-    Vec<float, 4>::cvt(Vec<float, 4>::ld(p), f);
-    Vec<float, 4>::cvt(Vec<float, 4>::ld(p + 4), f + 4);
-  }
-  static __device__ __forceinline__ void st(float* p, const float* f) {
-    Vec<float, 4>::st(p, f);
-    Vec<float, 4>::st(p + 4, f + 4);
-  }
-};
-template <> struct Vec<bf16_t, 8> {
-  using raw_t = u32x4;
-  static __device__ __forceinline__ raw_t ld(const bf16_t* p) { return gload<u32x4>(p); }
-  static __device__ __forceinline__ void cvt(const raw_t& v, float* f) {
-    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-    f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
-  }
-  static __device__ __forceinline__ void st(bf16_t* p, const float* f) {
-    u32x4 v;
-    v.x = pack_bf16x2(f[0], f[1]); v.y = pack_bf16x2(f[2], f[3]);
-    v.z = pack_bf16x2(f[4], f[5]); v.w = pack_bf16x2(f[6], f[7]);
-    gstore<u32x4>(p, v);
-  }
-};
-template <> struct Vec<bf16_t, 4> {  // output side of a 4-wide fp32 input vector
-  static __device__ __forceinline__ void ld_cvt(const bf16_t* p, float* f) {
-    const u32x2 v = gload<u32x2>(p);
-    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-  }
-  static __device__ __forceinline__ void st(bf16_t* p, const float* f) {
-    u32x2 v;
-    v.x = pack_bf16x2(f[0], f[1]); v.y = pack_bf16x2(f[2], f[3]);
-    gstore<u32x2>(p, v);
-  }
-};
-template <> struct Vec<f16_t, 8> {
-  using raw_t = u32x4;
-  static __device__ __forceinline__ raw_t ld(const f16_t* p) { return gload<u32x4>(p); }
-  static __device__ __forceinline__ void cvt(const raw_t& v, float* f) {
-    f[0] = f16_lo(v.x); f[1] = f16_hi(v.x); f[2] = f16_lo(v.y); f[3] = f16_hi(v.y);
-    f[4] = f16_lo(v.z); f[5] = f16_hi(v.z); f[6] = f16_lo(v.w); f[7] = f16_hi(v.w);
-  }
-  static __device__ __forceinline__ void st(f16_t* p, const float* f) {
-    u32x4 v;
-    v.x = pack_f16x2(f[0], f[1]); v.y = pack_f16x2(f[2], f[3]);
-    v.z = pack_f16x2(f[4], f[5]); v.w = pack_f16x2(f[6], f[7]);
-    gstore<u32x4>(p, v);
-  }
-};
-template <> struct Vec<f16_t, 4> {
-  static __device__ __forceinline__ void ld_cvt(const f16_t* p, float* f) {
-    const u32x2 v = gload<u32x2>(p);
-    f[0] = f16_lo(v.x); f[1] = f16_hi(v.x); f[2] = f16_lo(v.y); f[3] = f16_hi(v.y);
-  }
-  static __device__ __forceinline__ void st(f16_t* p, const float* f) {
-    u32x2 v;
-    v.x = pack_f16x2(f[0], f[1]); v.y = pack_f16x2(f[2], f[3]);
-    gstore<u32x2>(p, v);
-  }
-};
-
-// Output-side load of V elements widened to fp32 (for accumulate-into-out).
-template <typename T, int V>
-__device__ __forceinline__ void ld_cvt_out(const T* p, float* f) {
-  if constexpr (V == 1 || (V == 4 && sizeof(T) == 4) || (V == 8 && sizeof(T) == 2)) {
-    Vec<T, V>::cvt(Vec<T, V>::ld(p), f);
-  } else {
-    Vec<T, V>::ld_cvt(p, f);
-  }
+__device__ __forceinline__ rsrc_t make_rsrc(uint64_t base, uint32_t bytes) {
+  return make_rsrc(reinterpret_cast<const void*>(base), bytes);
 }
 
-// Raw load of V elements of an expert row.  AL: the row address is 16-byte aligned (vector
-// load); otherwise V element loads packed into the same raw layout, so cvt() serves both.
+constexpr int kCPolCached = 0;  // default policy: keep in L2 / Infinity Cache (re-read data)
+
+template <int BYTES> struct Raw;
+template <> struct Raw<32> {  // two 16-byte accesses (8 fp32 results of one 16-bit input vector)
+  using type = u32x8;
+  template <int CP = kCPol>
+  static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
+    const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CP));
+    const u32x4 b =
+        __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off + 16, 0, CP));
+    return type{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  }
+  static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[0], v[1], v[2], v[3]}, r, (int)off, 0, kCPol);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[4], v[5], v[6], v[7]}, r, (int)off + 16, 0, kCPol);
+  }
+  static __device__ __forceinline__ uint32_t word(const type& v, int i) { return v[i]; }
+};
+template <> struct Raw<16> {
+  using type = u32x4;
+  template <int CP = kCPol>
+  static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(type, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CP));
+  }
+  static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kCPol);
+  }
+  static __device__ __forceinline__ uint32_t word(const type& v, int i) { return v[i]; }
+};
+template <> struct Raw<8> {
+  using type = u32x2;
+  template <int CP = kCPol>
+  static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(type, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, CP));
+  }
+  static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, kCPol);
+  }
+  static __device__ __forceinline__ uint32_t word(const type& v, int i) { return v[i]; }
+};
+template <> struct Raw<4> {
+  using type = uint32_t;
+  template <int CP = kCPol>
+  static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, CP);
+  }
+  static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, kCPol);
+  }
+  static __device__ __forceinline__ uint32_t word(const type& v, int) { return v; }
+};
+template <> struct Raw<2> {
+  using type = uint16_t;
+  template <int CP = kCPol>
+  static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, CP);
+  }
+  static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)off, 0, kCPol);
+  }
+  static __device__ __forceinline__ uint32_t word(const type& v, int) { return v; }
+};
+
+// V consecutive elements of T: one buffer access of V * sizeof(T) bytes, widened to fp32 by cvt().
+template <typename T, int V> struct Vec {
+  static constexpr int kBytes = V * ElemInfo<T>::kBytes;
+  using R = Raw<kBytes>;
+  using raw_t = typename R::type;
+  template <int CP = kCPol>
+  static __device__ __forceinline__ raw_t ld(rsrc_t r, uint32_t off) {
+    return R::template ld<CP>(r, off);
+  }
+  static __device__ __forceinline__ void cvt(const raw_t& raw, float* f) {
+    if constexpr (ElemInfo<T>::kBytes == 4) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) f[v] = __uint_as_float(R::word(raw, v));
+    } else if constexpr (V == 1) {
+      f[0] = std::is_same<T, bf16_t>::value ? __uint_as_float((uint32_t)raw << 16)
+                                            : (float)__builtin_bit_cast(_Float16, (uint16_t)raw);
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; v += 2) {
+        const uint32_t w = R::word(raw, v / 2);
+        if constexpr (std::is_same<T, bf16_t>::value) {
+          f[v] = bf16_lo(w);
+          f[v + 1] = bf16_hi(w);
+        } else {
+          f[v] = f16_lo(w);
+          f[v + 1] = f16_hi(w);
+        }
+      }
+    }
+  }
+  static __device__ __forceinline__ raw_t pack(const float* f) {
+    raw_t raw;
+    if constexpr (ElemInfo<T>::kBytes == 4) {
+      if constexpr (V == 1) {
+        raw = __float_as_uint(f[0]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) raw[v] = __float_as_uint(f[v]);
+      }
+    } else if constexpr (V == 1) {
+      raw = std::is_same<T, bf16_t>::value ? f32_to_bf16_bits(f[0]) : f32_to_f16_bits(f[0]);
+    } else if constexpr (V == 2) {
+      raw = std::is_same<T, bf16_t>::value ? pack_bf16x2(f[0], f[1]) : pack_f16x2(f[0], f[1]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; v += 2)
+        raw[v / 2] = std::is_same<T, bf16_t>::value ? pack_bf16x2(f[v], f[v + 1])
+                                                    : pack_f16x2(f[v], f[v + 1]);
+    }
+    return raw;
+  }
+  static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, const float* f) {
+    R::st(r, off, pack(f));
+  }
+};
+
+// Elements per 16-byte load of T.
+template <typename T> constexpr int vec16() { return 16 / ElemInfo<T>::kBytes; }
+
+// Load of V elements of an expert row.  AL: the row start is 16-byte aligned (one vector
+// access); otherwise V element accesses assembled into the same raw layout, so cvt() serves both.
 template <typename TX, int V, bool AL>
-__device__ __forceinline__ typename Vec<TX, V>::raw_t load_x(uint64_t src, int64_t col) {
-  const TX* p = reinterpret_cast<const TX*>(src) + col;
+__device__ __forceinline__ typename Vec<TX, V>::raw_t load_x(rsrc_t r, uint32_t off) {
+  using VX = Vec<TX, V>;
   if constexpr (AL || V == 1) {
-    return Vec<TX, V>::ld(p);
-  } else if constexpr (sizeof(TX) == 4) {
-    f32x4 r;
-    r.x = gload<float>(p); r.y = gload<float>(p + 1);
-    r.z = gload<float>(p + 2); r.w = gload<float>(p + 3);
-    return r;
+    return VX::ld(r, off);
+  } else if constexpr (ElemInfo<TX>::kBytes == 4) {
+    typename VX::raw_t raw;
+#pragma unroll
+    for (int v = 0; v < V; ++v) raw[v] = Raw<4>::ld(r, off + 4 * v);
+    return raw;
   } else {
-    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
-    u32x4 r;
-    r.x = (uint32_t)gload<uint16_t>(q + 0) | ((uint32_t)gload<uint16_t>(q + 1) << 16);
-    r.y = (uint32_t)gload<uint16_t>(q + 2) | ((uint32_t)gload<uint16_t>(q + 3) << 16);
-    r.z = (uint32_t)gload<uint16_t>(q + 4) | ((uint32_t)gload<uint16_t>(q + 5) << 16);
-    r.w = (uint32_t)gload<uint16_t>(q + 6) | ((uint32_t)gload<uint16_t>(q + 7) << 16);
-    return r;
+    typename VX::raw_t raw;
+#pragma unroll
+    for (int v = 0; v < V; v += 2)
+      raw[v / 2] = (uint32_t)Raw<2>::ld(r, off + 2 * v) |
+                   ((uint32_t)Raw<2>::ld(r, off + 2 * v + 2) << 16);
+    return raw;
   }
 }
 
 // Plan status words (int32, at the start of the plan workspace).
 constexpr int kStatusInvalid = 0;    // rows whose scatter index is outside [0, T)
 constexpr int kStatusMisaligned = 1; // nonzero if any source row is not 16-byte aligned
+constexpr int kStatusLongest = 2;    // rows of the longest token segment
 
-// Elements per 16-byte load of T.
-template <typename T> constexpr int vec16() { return 16 / ElemInfo<T>::kBytes; }
 
 // Wave-uniform value: forces an SGPR so that dependent loads become scalar loads.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// A batch of up to 64 plan records held one per lane; row i of the batch is read back as
+// wave-uniform (SGPR) values with readlane, so the per-row metadata costs no memory latency.
+struct LaneRecs {
+  uint32_t src_lo, src_hi, w_bits;
+  int32_t g;
+  __device__ __forceinline__ void load(const Rec* __restrict__ rec, int first, int count, int lane) {
+    if (lane < count) {
+      const u32x4 v = *(const FMOE_GLOBAL u32x4*)(rec + first + lane);
+      src_lo = v.x; src_hi = v.y; w_bits = v.z; g = (int32_t)v.w;
+    } else {
+      src_lo = src_hi = w_bits = 0; g = 0;
+    }
+  }
+  __device__ __forceinline__ uint64_t src(int i) const {
+    return (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)src_lo, i) |
+           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)src_hi, i) << 32);
+  }
+  __device__ __forceinline__ float w(int i) const {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)w_bits, i));
+  }
+  __device__ __forceinline__ int32_t row(int i) const { return __builtin_amdgcn_readlane(g, i); }
+  // Reorder the `count` records to ascending g: each lane ranks its key against all others
+  // (readlane broadcasts) and pushes its record to lane `rank` (ds_permute).  Keys are distinct.
+  __device__ __forceinline__ void sort_by_row(int count, int lane) {
+    const int key = lane < count ? g : 0x7fffffff;
+    int rank = 0;
+    for (int m = 0; m < count; ++m) rank += (__builtin_amdgcn_readlane(key, m) < key) ? 1 : 0;
+    const int addr = rank * 4;  // lanes >= count all push to lane `count`, which is never read
+    src_lo = (uint32_t)__builtin_amdgcn_ds_permute(addr, (int)src_lo);
+    src_hi = (uint32_t)__builtin_amdgcn_ds_permute(addr, (int)src_hi);
+    w_bits = (uint32_t)__builtin_amdgcn_ds_permute(addr, (int)w_bits);
+    g = __builtin_amdgcn_ds_permute(addr, g);
+  }
+};
 
 // Runtime-typed loads of the small per-row arrays (wave-uniform dtype switch).
 __device__ __forceinline__ float load_weight(const void* w, int dtype, int64_t i) {

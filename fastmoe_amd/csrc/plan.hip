@@ -6,16 +6,23 @@
 //
 //   row_ptr[T + 2]  : segment b = [row_ptr[b], row_ptr[b + 1]); b == T holds the rows whose index
 //                     is out of range (they are dropped by the forward, zero-filled by the backward)
-//   rec[N]          : 16-byte records {source row address, fp32 gate, g}, ascending g per segment
+//   rec[N]          : 16-byte records {source row address, fp32 gate, g}; a segment of up to 64
+//                     rows is unordered (consumers that need the order rank it in registers),
+//                     a longer one is in ascending g
+//   row_rec[N]      : the same per packed row g, in g order, with the token in place of g (-1 for
+//                     an out-of-range index) -- read by the packed-row-major backward
 //
 // Steps (all on the caller's stream, no host synchronisation):
 //   1. count + scan   one 1024-thread workgroup histograms idx into LDS (T + 1 <= kLdsTokens) and
 //                     scans it; larger T fall back to zero / global-atomic count / one-block scan.
 //   2. fill           one thread per row: claims a slot in its segment with an atomic cursor and
-//                     writes its record (arbitrary order inside the segment).
-//   3. sort           one wave per segment ranks the records by g (segments are top-k sized, so a
-//                     register rank of <= 64 entries; larger segments take an O(c^2/64) path) and
-//                     writes them in order, which makes the whole plan bit-identical run to run.
+//                     writes its record (arbitrary order inside the segment) plus its g-ordered
+//                     row record.
+//   3. order          segments longer than 64 rows only (never for top-k routing; the kernel
+//                     exits at once otherwise): one wave per segment ranks its records by g and
+//                     writes them in order.
+//                     Shorter segments are ordered by the consumer in registers, so every result
+//                     is bit-identical run to run even though the fill order is not.
 #include "common.h"
 
 namespace fmoe {
@@ -24,7 +31,7 @@ constexpr int kScanThreads = 1024;
 constexpr int kLdsTokens = 33792;  // 132 KiB of LDS histogram (gfx950: 160 KiB per workgroup)
 
 struct PlanLayout {
-  int64_t status, cursor, row_ptr, rec_tmp, rec, total;
+  int64_t status, cursor, row_ptr, rec_tmp, rec, row_rec, total;
 };
 
 __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
@@ -35,7 +42,8 @@ __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
   L.row_ptr = L.cursor + up((T + 1) * 4);
   L.rec_tmp = L.row_ptr + up((T + 2) * 4);
   L.rec = L.rec_tmp + up(N * 16);
-  L.total = L.rec + up(N * 16);
+  L.row_rec = L.rec + up(N * 16);
+  L.total = L.row_rec + up(N * 16);
   return L;
 }
 
@@ -64,33 +72,57 @@ __device__ int block_exclusive_scan_1024(int v, int* total) {
   return before + incl - v;
 }
 
-// Histogram + scan in LDS: one block.  bins = T + 1 <= kLdsTokens.
+// Max of one int per thread over a 1024-thread block (all threads get it).
+__device__ int block_max_1024(int v) {
+  __shared__ int wave_max[kScanThreads / kWave];
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) v = max(v, __shfl_xor(v, d, kWave));
+  if ((threadIdx.x & (kWave - 1)) == 0) wave_max[threadIdx.x / kWave] = v;
+  __syncthreads();
+  int m = 0;
+#pragma unroll
+  for (int i = 0; i < kScanThreads / kWave; ++i) m = max(m, wave_max[i]);
+  __syncthreads();
+  return m;
+}
+
+// Histogram + scan in LDS: one block.  bins = T + 1 <= kLdsTokens.  Index loads go through a
+// buffer descriptor sized to the array, so a batch of loads is issued unconditionally (lanes past
+// N read 0 and are masked at the atomic) and stays in flight together.
+template <typename TI>
 __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
-    const void* __restrict__ idx, int idx_dtype, int64_t N, int64_t T, int32_t* __restrict__ cursor,
+    const TI* __restrict__ idx, int64_t N, int64_t T, int32_t* __restrict__ cursor,
     int32_t* __restrict__ row_ptr, int32_t* __restrict__ status) {
   __shared__ int hist[kLdsTokens];
   const int nb = (int)T + 1;
   for (int i = threadIdx.x; i < nb; i += kScanThreads) hist[i] = 0;
   __syncthreads();
-  if (idx_dtype == FMOE_I64) {
-    const int64_t* p = static_cast<const int64_t*>(idx);
-    for (int64_t g = threadIdx.x; g < N; g += kScanThreads) {
-      const int64_t t = p[g];
-      atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
+  const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));
+  constexpr int kBatch = 16;
+  for (int64_t base = 0; base < N; base += (int64_t)kScanThreads * kBatch) {
+    TI v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const uint32_t g = (uint32_t)(base + (int64_t)i * kScanThreads + threadIdx.x);
+      v[i] = __builtin_bit_cast(
+          TI, Raw<sizeof(TI)>::template ld<kCPolCached>(ri, g * (uint32_t)sizeof(TI)));
     }
-  } else {
-    const int32_t* p = static_cast<const int32_t*>(idx);
-    for (int64_t g = threadIdx.x; g < N; g += kScanThreads) {
-      const int32_t t = p[g];
-      atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t g = base + (int64_t)i * kScanThreads + threadIdx.x;
+      const int64_t t = (int64_t)v[i];
+      if (g < N) atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
     }
   }
   __syncthreads();
   const int per = (nb + kScanThreads - 1) / kScanThreads;
   const int b0 = min(nb, (int)threadIdx.x * per);
   const int b1 = min(nb, b0 + per);
-  int local = 0;
-  for (int b = b0; b < b1; ++b) local += hist[b];
+  int local = 0, longest = 0;
+  for (int b = b0; b < b1; ++b) {
+    local += hist[b];
+    if (b < nb - 1) longest = max(longest, hist[b]);
+  }
   int total;
   int run = block_exclusive_scan_1024(local, &total);
   for (int b = b0; b < b1; ++b) {
@@ -99,10 +131,13 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
     cursor[b] = run;
     run += c;
   }
+  // longest token segment (the out-of-range segment T is never ordered)
+  longest = block_max_1024(longest);
   if (threadIdx.x == 0) {
     row_ptr[nb] = total;
     status[kStatusInvalid] = hist[T];
     status[kStatusMisaligned] = 0;
+    status[kStatusLongest] = longest;
   }
 }
 
@@ -134,6 +169,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __re
     status[kStatusMisaligned] = 0;
   }
   __syncthreads();
+  int longest = 0;
   for (int64_t base = 0; base < nb; base += (int64_t)kScanThreads * kPer) {
     const int64_t b0 = base + (int64_t)threadIdx.x * kPer;
     int v[kPer];
@@ -142,6 +178,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __re
     for (int i = 0; i < kPer; ++i) {
       v[i] = (b0 + i < nb) ? cnt[b0 + i] : 0;
       local += v[i];
+      if (b0 + i < T) longest = max(longest, v[i]);
     }
     int total;
     int run = carry + block_exclusive_scan_1024(local, &total);
@@ -155,55 +192,64 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __re
     }
     carry += total;
   }
-  if (threadIdx.x == 0) row_ptr[nb] = carry;
+  longest = block_max_1024(longest);
+  if (threadIdx.x == 0) {
+    row_ptr[nb] = carry;
+    status[kStatusLongest] = longest;
+  }
 }
 
 // ---- fill -----------------------------------------------------------------------------------
+constexpr int kLdsExperts = 4096;  // expert offsets staged in LDS for the row -> expert search
+
+template <typename TI, typename TW>
 __global__ __launch_bounds__(kGroup) void k_plan_fill(
-    const void* __restrict__ idx, int idx_dtype, const void* __restrict__ w, int w_dtype, int64_t N,
-    int64_t T, const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets,
-    int64_t E, int64_t row_bytes, int32_t* __restrict__ cursor, Rec* __restrict__ rec_tmp,
+    const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T,
+    const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
+    int64_t row_bytes, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ cursor,
+    Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, Rec* __restrict__ row_rec,
     int32_t* __restrict__ status) {
+  __shared__ int64_t off_lds[kLdsExperts + 1];
+  const bool lds_off = E <= kLdsExperts;
+  if (lds_off)
+    for (int i = threadIdx.x; i <= E; i += kGroup) off_lds[i] = offsets[i];
+  __syncthreads();
   const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
-  if (g >= N) return;
-  const int64_t t = load_index(idx, idx_dtype, g);
-  const int64_t b = (t >= 0 && t < T) ? t : T;
-  const int pos = atomicAdd(&cursor[b], 1);
-  const int64_t e = expert_of_row(offsets, E, g);
-  Rec r;
-  r.src = (uint64_t)ptr_table[e] + (uint64_t)((g - offsets[e]) * row_bytes);
-  r.w = load_weight(w, w_dtype, g);
-  r.g = (int32_t)g;
-  rec_tmp[pos] = r;
-  if (r.src & 15) atomicOr(&status[kStatusMisaligned], 1);
+  if (g < N) {
+    const int64_t t = (int64_t)idx[g];
+    const int64_t b = (t >= 0 && t < T) ? t : T;
+    const int pos = atomicAdd(&cursor[b], 1);
+    const bool long_seg = b < T && row_ptr[b + 1] - row_ptr[b] > kWave;
+    const int64_t e = expert_of_row(lds_off ? off_lds : offsets, E, g);
+    Rec r;
+    r.src = (uint64_t)ptr_table[e] + (uint64_t)((g - (lds_off ? off_lds[e] : offsets[e])) * row_bytes);
+    r.w = ld1(w + g);
+    r.g = (int32_t)g;
+    (long_seg ? rec_tmp : rec)[pos] = r;
+    r.g = (b == T) ? -1 : (int32_t)t;
+    row_rec[g] = r;
+    if (r.src & 15) atomicOr(&status[kStatusMisaligned], 1);
+  }
 }
 
-// ---- sort: one wave per segment ---------------------------------------------------------------
-__global__ __launch_bounds__(kGroup) void k_plan_sort(const int32_t* __restrict__ row_ptr,
-                                                      int64_t nb, const Rec* __restrict__ rec_tmp,
-                                                      Rec* __restrict__ rec) {
+// One wave per token segment, launched after the fill; it exits at once unless some segment is
+// longer than one wave (never for top-k routing: the scan recorded the longest segment).
+__global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __restrict__ row_ptr,
+                                                           int64_t T,
+                                                           const int32_t* __restrict__ status,
+                                                           const Rec* __restrict__ scratch,
+                                                           Rec* __restrict__ rec) {
+  if (status[kStatusLongest] <= kWave) return;
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t b = (int64_t)blockIdx.x * kWavesPerGroup + uniform(threadIdx.x / kWave);
-  if (b >= nb) return;
+  if (b >= T) return;
   const int beg = row_ptr[b];
   const int c = row_ptr[b + 1] - beg;
-  if (c <= kWave) {
-    Rec r;
-    int key = 0x7fffffff;
-    if (lane < c) {
-      r = rec_tmp[beg + lane];
-      key = r.g;
-    }
-    int rank = 0;
-    for (int m = 0; m < c; ++m) rank += (__shfl(key, m, kWave) < key) ? 1 : 0;
-    if (lane < c) rec[beg + rank] = r;
-    return;
-  }
-  // Large segment (only for non-top-k style indices): rank each record against all others.
+  if (c <= kWave) return;
   for (int i = lane; i < c; i += kWave) {
-    const Rec r = rec_tmp[beg + i];
+    const Rec r = scratch[beg + i];
     int rank = 0;
-    for (int m = 0; m < c; ++m) rank += (rec_tmp[beg + m].g < r.g) ? 1 : 0;
+    for (int m = 0; m < c; ++m) rank += (scratch[beg + m].g < r.g) ? 1 : 0;
     rec[beg + rank] = r;
   }
 }
@@ -221,6 +267,11 @@ extern "C" int64_t fmoe_plan_row_ptr_offset(int64_t num_rows, int64_t num_tokens
 extern "C" int64_t fmoe_plan_records_offset(int64_t num_rows, int64_t num_tokens) {
   return fmoe::plan_layout(num_rows, num_tokens).rec;
 }
+namespace fmoe {
+int64_t plan_row_records_offset(int64_t num_rows, int64_t num_tokens) {
+  return plan_layout(num_rows, num_tokens).row_rec;
+}
+}  // namespace fmoe
 
 extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d_weights,
                                int w_dtype, int64_t num_rows, int64_t num_tokens,
@@ -254,11 +305,16 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
   Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
+  Rec* row_rec = reinterpret_cast<Rec*>(ws + L.row_rec);
   const int64_t nb = T + 1;
 
-  if (nb <= kLdsTokens) {
-    hipLaunchKernelGGL(k_plan_count_scan_lds, dim3(1), dim3(kScanThreads), 0, s, d_indices,
-                       idx_dtype, N, T, cursor, row_ptr, status);
+  if (nb <= kLdsTokens && N < (int64_t(1) << 27)) {
+    if (idx_dtype == FMOE_I64)
+      hipLaunchKernelGGL(k_plan_count_scan_lds<int64_t>, dim3(1), dim3(kScanThreads), 0, s,
+                         static_cast<const int64_t*>(d_indices), N, T, cursor, row_ptr, status);
+    else
+      hipLaunchKernelGGL(k_plan_count_scan_lds<int32_t>, dim3(1), dim3(kScanThreads), 0, s,
+                         static_cast<const int32_t*>(d_indices), N, T, cursor, row_ptr, status);
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(count_scan)")) return rc;
   } else {
     hipLaunchKernelGGL(k_plan_zero, dim3((unsigned)((nb + kGroup - 1) / kGroup)), dim3(kGroup), 0,
@@ -274,12 +330,24 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(scan)")) return rc;
   }
   if (N == 0) return FMOE_OK;
-  hipLaunchKernelGGL(k_plan_fill, dim3((unsigned)((N + kGroup - 1) / kGroup)), dim3(kGroup), 0, s,
-                     d_indices, idx_dtype, d_weights, w_dtype, N, T, d_ptr_table, d_offsets, E,
-                     row_bytes, cursor, rec_tmp, status);
+  const dim3 grid((unsigned)((N + kGroup - 1) / kGroup));
+#define FMOE_FILL(TI, TW)                                                                          \
+  hipLaunchKernelGGL((k_plan_fill<TI, TW>), grid, dim3(kGroup), 0, s,                              \
+                     static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
+                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, cursor, rec_tmp, rec, row_rec, \
+                     status)
+  if (idx_dtype == FMOE_I64) {
+    if (w_dtype == FMOE_F32) FMOE_FILL(int64_t, float);
+    else if (w_dtype == FMOE_BF16) FMOE_FILL(int64_t, bf16_t);
+    else FMOE_FILL(int64_t, f16_t);
+  } else {
+    if (w_dtype == FMOE_F32) FMOE_FILL(int32_t, float);
+    else if (w_dtype == FMOE_BF16) FMOE_FILL(int32_t, bf16_t);
+    else FMOE_FILL(int32_t, f16_t);
+  }
+#undef FMOE_FILL
   if (int rc = fmoe_host::check_launch("fmoe_build_plan(fill)")) return rc;
-  hipLaunchKernelGGL(k_plan_sort,
-                     dim3((unsigned)((nb + kWavesPerGroup - 1) / kWavesPerGroup)), dim3(kGroup), 0,
-                     s, row_ptr, nb, rec_tmp, rec);
+  hipLaunchKernelGGL(k_plan_sort_long, dim3((unsigned)((T + kWavesPerGroup - 1) / kWavesPerGroup)),
+                     dim3(kGroup), 0, s, row_ptr, T, status, rec_tmp, rec);
   return fmoe_host::check_launch("fmoe_build_plan(sort)");
 }

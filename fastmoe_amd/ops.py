@@ -81,7 +81,15 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _require_cuda(t: torch.Tensor, what: str) -> None:
+class _DeviceProbe:
+    """Duck-types the ``is_cuda``/``device`` of a tensor for a bare device argument."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.is_cuda = self.device.type == "cuda"
+
+
+def _require_cuda(t, what: str) -> None:
     if not t.is_cuda:
         raise RuntimeError(
             f"fastmoe_amd: {what} is on {t.device}; the combine runs only on the GPU "
@@ -113,6 +121,13 @@ class GroupedMetadata(tuple):
         self.device = extra["device"]
         self.num_rows = sum(self.sizes)
         return self
+
+    # the reference tuple's fields by name
+    ptr_table = property(lambda self: self[0])
+    chunk_sizes = property(lambda self: self[1])
+    expert_offsets = property(lambda self: self[2])
+    max_rows = property(lambda self: self[3])
+    num_experts = property(lambda self: self[4])
 
     def matches(self, expert_tensors: Sequence[torch.Tensor]) -> bool:
         """True if this metadata describes exactly these buffers (same addresses and rows)."""
@@ -158,8 +173,8 @@ def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None
     (``fmoe_build_metadata``): no host staging buffer and no synchronous copy.
     """
     dtype, dev, hidden = _check_experts(expert_tensors)
-    if device is not None and torch.device(device).type != "cuda":
-        raise RuntimeError(f"fastmoe_amd: metadata device must be a GPU, got {device}")
+    if device is not None:
+        _require_cuda(_DeviceProbe(device), "device")
     lib = _abi.lib()
     E = len(expert_tensors)
     sizes = [int(t.shape[0]) for t in expert_tensors]

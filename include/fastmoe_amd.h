@@ -100,14 +100,16 @@ FMOE_API int fmoe_build_metadata(const int64_t* host_ptrs, const int64_t* host_r
 
 /*
  * Plan: token-major inverse of the scatter index.  For each token t, the packed rows g with
- * idx[g] == t, in ascending g, each as a 16-byte record {source row address, fp32 gate, g}.
- * Rows with an out-of-range index form one extra segment (number T) that the backward zero-fills.
+ * idx[g] == t, each as a 16-byte record {source row address, fp32 gate, g}; a segment of up to
+ * 64 rows is stored in no particular order (the deterministic forward orders it by g in
+ * registers), a longer one in ascending g.  Rows with an out-of-range index form one extra
+ * segment (number T).  The plan also holds the same records indexed by g for the backward.
  *
  * Workspace: fmoe_plan_workspace_bytes(N, T) bytes of device memory, 256-byte aligned, owned by the
  * caller; no zero-fill is needed.  Layout (byte offsets from the workspace base):
  *   fmoe_plan_status_offset()     : int32 count of out-of-range scatter indices
  *   fmoe_plan_row_ptr_offset(N,T) : int32 row_ptr[T + 2] (segment t = [row_ptr[t], row_ptr[t+1]))
- *   fmoe_plan_records_offset(N,T) : N sorted 16-byte records
+ *   fmoe_plan_records_offset(N,T) : N 16-byte records, grouped by segment
  *
  * d_indices : [N] scatter index, FMOE_I64 or FMOE_I32
  * d_weights : [N] gate weights, FMOE_F32 / FMOE_BF16 / FMOE_F16

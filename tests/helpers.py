@@ -41,12 +41,16 @@ def oracle_bwd(experts, idx, w, T, grad_out):
 
 def abs_dot(experts, idx, grad_out, T):
     """sum_d |grad_out[idx[g], d] * X[g, d]| per row (the scale of grad_w's rounding error)."""
-    x = torch.cat([e.detach().float().cpu() for e in experts], 0).abs().double()
-    go = grad_out.detach().float().cpu().abs().double()
+    x = torch.cat([e.detach().float().cpu() for e in experts], 0).abs()
+    go = grad_out.detach().float().cpu().abs()
     i = idx.cpu().long()
     valid = (i >= 0) & (i < T)
-    rows = go[i.clamp(0, T - 1)]
-    return ((rows * x).sum(-1) * valid.double()).numpy()
+    out = torch.empty(x.shape[0], dtype=torch.float64)
+    step = 2048  # bounded temporaries at full workload sizes
+    for a in range(0, x.shape[0], step):
+        rows = go[i[a: a + step].clamp(0, T - 1)].double()
+        out[a: a + step] = (rows * x[a: a + step].double()).sum(-1) * valid[a: a + step].double()
+    return out.numpy()
 
 
 def abs_sum(experts, idx, w, T):

@@ -1,0 +1,171 @@
+"""The Python host path end to end on the CPU, against a recording stand-in for the C library.
+
+No kernel runs here: the stand-in checks and records the arguments every C-ABI entry point
+receives (sizes, dtype codes, strides, pointer/None choices) so that marshalling mistakes in
+fastmoe_amd/ops.py show up without a GPU.  Numerics are covered by the GPU parity tests.
+"""
+from __future__ import annotations
+
+import contextlib
+
+import pytest
+import torch
+
+import fastmoe_amd
+from fastmoe_amd import _abi, ops
+
+
+class FakeLib:
+    def __init__(self):
+        self.calls = []
+        self.real = _abi.lib()
+
+    def fmoe_abi_version(self):
+        return _abi.ABI_VERSION
+
+    def fmoe_last_error(self):
+        return b"fake"
+
+    def fmoe_build_metadata(self, host_ptrs, host_rows, E, ptr_table, chunk, offsets, max_rows,
+                            stream):
+        assert isinstance(E, int) and E >= 1
+        assert len(host_ptrs) == E and len(host_rows) == E
+        assert all(isinstance(p, int) for p in (ptr_table, chunk, offsets, max_rows))
+        self.calls.append(("metadata", E, list(host_rows)))
+        return 0
+
+    def fmoe_plan_workspace_bytes(self, N, T):
+        return self.real.fmoe_plan_workspace_bytes(N, T)
+
+    def fmoe_plan_status_offset(self):
+        return 0
+
+    def fmoe_plan_row_ptr_offset(self, N, T):
+        return self.real.fmoe_plan_row_ptr_offset(N, T)
+
+    def fmoe_plan_records_offset(self, N, T):
+        return self.real.fmoe_plan_records_offset(N, T)
+
+    def fmoe_build_plan(self, idx, idt, w, wdt, N, T, ptr_table, offsets, E, row_bytes, ws, stream):
+        assert idt in (_abi.I64, _abi.I32) and wdt in (_abi.F32, _abi.BF16, _abi.F16)
+        assert all(isinstance(p, int) for p in (idx, w, ptr_table, offsets, ws))
+        self.calls.append(("plan", N, T, E, row_bytes, idt, wdt))
+        return 0
+
+    def fmoe_combine_fwd(self, mode, plan, idx, idt, w, wdt, ptr_table, offsets, E, N, T, D, xdt,
+                         out, odt, ostride, acc, stream):
+        if mode == _abi.MODE_DET:
+            assert isinstance(plan, int)
+        else:
+            assert isinstance(idx, int) and isinstance(w, int)
+        self.calls.append(("fwd", mode, N, T, D, xdt, odt, ostride, acc))
+        return 0
+
+    def fmoe_combine_bwd(self, plan, N, T, D, xdt, gout, gdt, gstride, gx, gw, gwdt, stream):
+        assert isinstance(plan, int) and isinstance(gout, int) and gdt == xdt
+        self.calls.append(("bwd", N, T, D, xdt, gstride, gx is not None, gw is not None, gwdt))
+        return 0
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    f = FakeLib()
+    monkeypatch.setattr(_abi, "lib", lambda: f)
+    monkeypatch.setattr(ops, "_require_cuda", lambda t, what: None)
+    monkeypatch.setattr(ops, "_stream_handle", lambda dev: 0)
+    monkeypatch.setattr(torch.cuda, "device", lambda dev: contextlib.nullcontext())
+    return f
+
+
+def _experts(dtype=torch.bfloat16, sizes=(3, 0, 5), D=16):
+    return [torch.randn(n, D).to(dtype) for n in sizes]
+
+
+def test_autograd_forward_and_backward_calls(fake):
+    xs = [x.requires_grad_(True) for x in _experts()]
+    N = 8
+    idx = torch.randint(0, 4, (N,))
+    w = torch.rand(N, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16))
+    assert out.shape == (4, 16) and out.dtype == torch.bfloat16
+    grads = torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
+    kinds = [c[0] for c in fake.calls]
+    assert kinds == ["metadata", "plan", "fwd", "bwd"]
+    assert fake.calls[0] == ("metadata", 3, [3, 0, 5])
+    assert fake.calls[1] == ("plan", 8, 4, 3, 32, _abi.I64, _abi.F32)
+    assert fake.calls[2] == ("fwd", _abi.MODE_DET, 8, 4, 16, _abi.BF16, _abi.BF16, 16, 0)
+    assert fake.calls[3] == ("bwd", 8, 4, 16, _abi.BF16, 16, True, True, _abi.F32)
+    assert grads[0].shape == (N,) and grads[0].dtype == torch.float32
+    assert [g.shape[0] for g in grads[1:]] == [3, 0, 5]
+
+
+def test_backward_skips_unneeded_outputs(fake):
+    xs = _experts(torch.float32)
+    w = torch.rand(8, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long), w, (2, 16))
+    torch.autograd.grad(out, [w], torch.ones(2, 16))
+    assert fake.calls[-1][6:8] == (False, True)
+    fake.calls.clear()
+    xs = [x.requires_grad_(True) for x in _experts(torch.float32)]
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
+                                                   torch.rand(8), (2, 16))
+    torch.autograd.grad(out, xs, torch.ones(2, 16))
+    assert fake.calls[-1][6:8] == (True, False)
+
+
+def test_atomic_mode_zero_fills_and_skips_plan_in_place(fake):
+    xs = _experts(torch.float32)
+    out = torch.full((4, 16), 3.0)
+    meta = fastmoe_amd.prepare_grouped_metadata(xs, "cuda")
+    assert len(meta) == 5 and meta[3] == 5 and meta[4] == 3
+    ptr_table, chunk_sizes, expert_offsets, max_rows, num_experts = meta
+    assert expert_offsets.numel() == 3 and meta.offsets_full.numel() == 4
+    fake.calls.clear()
+    ret = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.int32),
+                                                   torch.rand(8), (4, 16), out=out, metadata=meta,
+                                                   mode="atomic")
+    assert ret is out and torch.all(out == 3.0)  # in place: never re-zeroed by the API
+    assert [c[0] for c in fake.calls] == ["fwd"]
+    assert fake.calls[0][1] == _abi.MODE_ATOMIC and fake.calls[0][-1] == 1
+    fake.calls.clear()
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
+                                                   torch.rand(8), (4, 16), mode="atomic")
+    assert torch.all(out == 0)
+    assert [c[0] for c in fake.calls] == ["metadata", "plan", "fwd"]
+
+
+def test_stale_metadata_is_rebuilt(fake):
+    xs = _experts(torch.float32)
+    meta = fastmoe_amd.prepare_grouped_metadata(xs, "cuda")
+    other = _experts(torch.float32)
+    fake.calls.clear()
+    fastmoe_amd.grouped_weighted_scatter_add(other, torch.zeros(8, dtype=torch.long), torch.rand(8),
+                                             (4, 16), out=torch.zeros(4, 16), metadata=meta)
+    assert fake.calls[0][0] == "metadata"  # the passed table does not describe `other`
+
+
+def test_argument_validation(fake):
+    xs = _experts(torch.float32)
+    with pytest.raises(ValueError, match="total expert rows"):
+        fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(7, dtype=torch.long),
+                                                 torch.rand(7), (4, 16))
+    with pytest.raises(TypeError):
+        fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8), torch.rand(8), (4, 16))
+    with pytest.raises(ValueError, match="out_shape"):
+        fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
+                                                 torch.rand(8), (4, 15))
+    with pytest.raises(ValueError, match="row-contiguous"):
+        fastmoe_amd.grouped_weighted_scatter_add([torch.randn(16, 4).t()], torch.zeros(4, dtype=torch.long),
+                                                 torch.rand(4), (4, 16))
+    with pytest.raises(ValueError, match="unit column stride"):
+        fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
+                                                 torch.rand(8), (4, 16), out=torch.zeros(16, 4).t())
+    with pytest.raises(ValueError, match="empty"):
+        fastmoe_amd.prepare_grouped_metadata([], "cuda")
+
+
+def test_weighted_scatter_add_single_tensor(fake):
+    src = torch.randn(10, 4)
+    out = fastmoe_amd.weighted_scatter_add(src, torch.randint(0, 5, (10,)), torch.rand(10), (5, 4))
+    assert out.shape == (5, 4)
+    assert fake.calls[0] == ("metadata", 1, [10])

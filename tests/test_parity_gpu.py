@@ -90,8 +90,10 @@ def test_fwd_fp32_atomic_vs_det_on_published_shape():
     assert rel.max() <= 1e-6
 
 
+@pytest.mark.parametrize("order", ["token", "row", "column"])
 @pytest.mark.parametrize("name", ["plumbing", "gigachat", "skewed"])
-def test_bwd_grad_x_bitexact_grad_w_close(name):
+def test_bwd_grad_x_bitexact_grad_w_close(name, order, monkeypatch):
+    monkeypatch.setenv("FMOE_BWD_ORDER", order)
     wl, T, idx, w, experts = _inputs(name)
     xd, idd, wd = _to_dev(experts, idx, w)
     xd = [x.requires_grad_(True) for x in xd]
@@ -238,7 +240,9 @@ def test_edge_large_segments_randint():
     assert np.all(np.abs(g[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
-def test_edge_invalid_indices_dropped_and_flagged():
+@pytest.mark.parametrize("order", ["token", "row", "column"])
+def test_edge_invalid_indices_dropped_and_flagged(order, monkeypatch):
+    monkeypatch.setenv("FMOE_BWD_ORDER", order)
     D, T = 32, 6
     gen = torch.Generator().manual_seed(5)
     experts = [torch.randn(4, D, generator=gen), torch.randn(3, D, generator=gen)]
@@ -365,6 +369,11 @@ def test_plan_matches_oracle():
     rec = plan[rec_off: rec_off + 16 * N].view(torch.int64).view(N, 2).cpu()
     want_rp, want_g = cref.plan(idx.numpy(), T)
     np.testing.assert_array_equal(row_ptr, want_rp)
+    # short segments are unordered in the plan: order each segment by g before comparing
+    g = (rec[:, 1] >> 32).numpy().astype(np.int32)
+    order = np.concatenate([np.arange(want_rp[b], want_rp[b + 1])[np.argsort(g[want_rp[b]:want_rp[b + 1]])]
+                            for b in range(T + 1)])
+    rec = rec[torch.from_numpy(order)]
     g = (rec[:, 1] >> 32).numpy().astype(np.int32)
     np.testing.assert_array_equal(g, want_g)
     wbits = (rec[:, 1] & 0xFFFFFFFF).numpy().astype(np.uint32)
@@ -373,6 +382,14 @@ def test_plan_matches_oracle():
     e_of = np.searchsorted(off, want_g, side="right") - 1
     src = np.array([meta.ptrs[e] for e in e_of], dtype=np.int64) + (want_g - off[e_of]) * wl.D * 2
     np.testing.assert_array_equal(rec[:, 0].numpy(), src)
+    # the g-indexed row records: {src, w, token}
+    rr_off = lib.fmoe_plan_records_offset(N, T) + ((16 * N + 255) // 256) * 256
+    rr = plan[rr_off: rr_off + 16 * N].view(torch.int64).view(N, 2).cpu()
+    tok = (rr[:, 1] >> 32).numpy().astype(np.int32)
+    np.testing.assert_array_equal(tok, idx.numpy())
+    e_of = np.searchsorted(off, np.arange(N), side="right") - 1
+    src = np.array([meta.ptrs[e] for e in e_of], dtype=np.int64) + (np.arange(N) - off[e_of]) * wl.D * 2
+    np.testing.assert_array_equal(rr[:, 0].numpy(), src)
 
 
 def test_metadata_matches_closed_forms():
