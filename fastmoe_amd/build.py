@@ -65,30 +65,38 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build(verbose: bool = True, jobs: int | None = None) -> Path:
-    """Compile every translation unit and link ``libfastmoe_amd.so``; returns its path."""
-    BUILD_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = True, jobs: int | None = None, defines: list[str] | None = None,
+          out: Path | None = None, build_dir: Path | None = None) -> Path:
+    """Compile every translation unit and link ``libfastmoe_amd.so``; returns its path.
+
+    ``defines`` (e.g. ``["FMOE_BWD_WAVES=8"]``) set the kernels' compile-time knobs; ``out`` and
+    ``build_dir`` redirect the result (tuning builds), by default the in-tree library.
+    """
+    bdir = build_dir or BUILD_DIR
+    lib_path = out or LIB_PATH
+    bdir.mkdir(parents=True, exist_ok=True)
+    dflags = [f"-D{d}" for d in (defines or [])]
     hipcc = _hipcc()
     cxx = shutil.which("g++") or "c++"
     cmds: list[list[str]] = []
     objs: list[str] = []
     for src in HIP_SOURCES:
-        obj = BUILD_DIR / (src + ".o")
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        obj = bdir / (src + ".o")
+        cmds.append([hipcc, *HIPCC_FLAGS, *dflags, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
     for src in HOST_SOURCES:
-        obj = BUILD_DIR / (src + ".o")
+        obj = bdir / (src + ".o")
         cmds.append([cxx, *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH}", file=sys.stderr)
-    return LIB_PATH
+        print(f"built {lib_path}", file=sys.stderr)
+    return lib_path
 
 
 if __name__ == "__main__":

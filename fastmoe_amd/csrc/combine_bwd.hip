@@ -1,4 +1,4 @@
-// Backward combine, token-major:
+// Backward combine:
 //   grad_X[g, :] = round_x(f32(grad_out[t, :]) * w[g])          for every row g routed from token t
 //   grad_w[g]    = sum_d grad_out[t, d] * X_e[g - off[e], d]     (fp64 accumulation of fp32
 //                  partial sums of 8 exact products -- v_dot2 on 16-bit data -- rounded once)
@@ -7,13 +7,17 @@
 // grad_out by scatter index, multiplies into an fp32 [N, D] temporary and lets autograd cast it
 // back -- three to four passes over [N, D] -- and which returns no gate gradient (:358-359).
 //
-// A wave owns one token.  It walks the columns in chunks of 64 * V * U; for each chunk it loads
-// grad_out[t] once into registers, then for every routed row of the token (plan segment, ascending
-// g) writes the grad_X chunk and, when the gate gradient is wanted, loads the X chunk, forms the
-// lane's fp64 partial dot product and reduces it across the wave with a xor butterfly (every lane
-// ends with the same sum).  Lane j keeps the running dot of the j-th row of the current batch of
-// up to 64 rows, so grad_out is read from HBM exactly once for up to 64 rows per token.  Segment T
-// of the plan (rows whose index was out of range) is zero-filled.
+// Work decomposition (token-grouped whole rows).  A workgroup owns one token's plan segment; its
+// waves take the token's rows in turn and each streams a whole row front to back: X[g] read and
+// grad_X[g] written with the non-temporal policy, grad_out[t] read with the default policy so the
+// rows of a token, running together on one CU, fetch it from HBM once and share it through L2.
+// grad_w needs no cross-wave reduction: a wave owns whole rows and reduces its dot product with a
+// xor butterfly.  Segment T of the plan (rows whose scatter index was out of range) gets zeros.
+//
+// Two passes.  When both gradients are wanted the grad_X pass (a write stream) and the grad_w pass
+// (read streams only) run as two back-to-back launches rather than one fused kernel: HBM loses
+// about a tenth of its throughput when a kernel interleaves this much reading and writing at fine
+// grain, which costs more than reading grad_out (T * D, one k-th of X at top-k) a second time.
 #include "common.h"
 
 namespace fmoe {
@@ -66,110 +70,6 @@ __device__ __forceinline__ void store_gate(void* gw, int dtype, int64_t g, doubl
   else st1(static_cast<f16_t*>(gw) + g, f);
 }
 
-// Tile: U 16-byte vectors per lane per column step and batches of R rows whose X loads are in
-// flight together and whose dot products are carried across column steps in registers, so each
-// row costs one wave reduction.
-template <typename TX, int V, int U, int RB, bool GX, bool GW, bool AL>
-__device__ __forceinline__ void bwd_body(const int32_t* __restrict__ row_ptr,
-                                         const Rec* __restrict__ rec, const TX* __restrict__ gout,
-                                         int64_t gstride, TX* __restrict__ gx,
-                                         void* __restrict__ gw, int gw_dtype, uint32_t D,
-                                         uint32_t t) {
-  using VX = Vec<TX, V>;
-  using raw_t = typename VX::raw_t;
-  constexpr int CW = kWave * V * U;
-  constexpr int R = AL ? RB : 1;  // misaligned rows: one at a time (register budget)
-  const int lane = threadIdx.x & (kWave - 1);
-  const int beg = row_ptr[t];
-  const int end = row_ptr[t + 1];
-  if (beg == end) return;
-  const uint32_t rowb = D * (uint32_t)sizeof(TX);
-  const rsrc_t rg = make_rsrc(gout + (int64_t)t * gstride, rowb);
-
-  for (int jb = beg; jb < end; jb += kWave) {
-    const int cnt = min(end - jb, kWave);
-    LaneRecs lr;
-    lr.load(rec, jb, cnt, lane);
-    for (int i = 0; i < cnt; i += R) {
-      rsrc_t rx[R], rgx[R];
-      float wr[R];
-      int32_t gr[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int ir = min(i + r, cnt - 1);  // a partial batch repeats its last row (loads only)
-        gr[r] = lr.row(ir);
-        wr[r] = lr.w(ir);
-        rx[r] = make_rsrc(lr.src(ir), rowb);
-        if constexpr (GX) rgx[r] = make_rsrc(gx + (int64_t)gr[r] * D, rowb);
-      }
-      double part[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) part[r] = 0.0;
-      for (uint32_t cb = 0; cb < D; cb += CW) {
-        uint32_t off[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          off[u] = (cb + (uint32_t)lane * V + (uint32_t)u * kWave * V) * (uint32_t)sizeof(TX);
-        raw_t gr_raw[U];
-        raw_t xr[GW ? R : 1][U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) gr_raw[u] = VX::ld(rg, off[u]);  // beyond D: reads 0
-        if constexpr (GW) {
-#pragma unroll
-          for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int u = 0; u < U; ++u) xr[r][u] = load_x<TX, V, AL>(rx[r], off[u]);
-        }
-        float go[U][V];
-#pragma unroll
-        for (int u = 0; u < U; ++u) VX::cvt(gr_raw[u], go[u]);
-        if constexpr (GX) {
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            if (i + r < cnt) {
-#pragma unroll
-              for (int u = 0; u < U; ++u) {
-                float y[V];
-#pragma unroll
-                for (int v = 0; v < V; ++v) y[v] = go[u][v] * wr[r];
-                VX::st(rgx[r], off[u], y);  // beyond D: dropped by the range check
-              }
-            }
-          }
-        }
-        if constexpr (GW) {
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-              float x[V];
-              VX::cvt(xr[r][u], x);
-#pragma unroll
-              for (int v = 0; v < V; ++v)
-                part[r] = __builtin_fma((double)x[v], (double)go[u][v], part[r]);
-            }
-          }
-        }
-      }
-      if constexpr (GW) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          if (i + r < cnt) {
-            const double tot = wave_sum(part[r]);
-            if (lane == 0) store_gate(gw, gw_dtype, gr[r], tot);
-          }
-        }
-      }
-    }
-  }
-}
-
-// ---- packed-row-major variant -------------------------------------------------------------------
-// A wave owns one packed row g: it streams X[g] and grad_X[g] front to back (non-temporal) and
-// gathers grad_out[idx[g]] with the default cache policy, so the k rows of a token re-read their
-// grad_out row from L2 / Infinity Cache rather than HBM.
-int64_t plan_row_records_offset(int64_t num_rows, int64_t num_tokens);
-
 // Zero gradients of a row whose scatter index was out of range.
 template <typename TX, int V, bool GX, bool GW>
 __device__ __forceinline__ void bwd_zero_row(uint32_t g, TX* __restrict__ gx, void* __restrict__ gw,
@@ -188,6 +88,9 @@ __device__ __forceinline__ void bwd_zero_row(uint32_t g, TX* __restrict__ gx, vo
   }
 }
 
+// One whole row g of token t: two column steps of 64 * V * U columns per iteration, so 2 * U
+// loads of each input stream per lane are in flight; columns past D read 0 and drop their stores
+// (buffer range check).
 template <typename TX, int V, int U, bool GX, bool GW, bool AL>
 __device__ __forceinline__ void bwd_row_body(uint64_t src, float wt, uint32_t t, uint32_t g,
                                              const TX* __restrict__ gout, int64_t gstride,
@@ -202,7 +105,7 @@ __device__ __forceinline__ void bwd_row_body(uint64_t src, float wt, uint32_t t,
   const rsrc_t rx = make_rsrc(src, rowb);
   const rsrc_t rgx = make_rsrc(gx + (int64_t)g * D, rowb);
   double part = 0.0;
-  for (uint32_t cb = 0; cb < D; cb += 2 * CW) {  // two column steps in flight per iteration
+  for (uint32_t cb = 0; cb < D; cb += 2 * CW) {
     uint32_t off[2][U];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -215,7 +118,7 @@ __device__ __forceinline__ void bwd_row_body(uint64_t src, float wt, uint32_t t,
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int u = 0; u < U; ++u) gr[h][u] = VX::template ld<kCPolCached>(rg, off[h][u]);
+      for (int u = 0; u < U; ++u) gr[h][u] = VX::template ld<FMOE_GOUT_CPOL>(rg, off[h][u]);
     if constexpr (GW) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -231,7 +134,7 @@ __device__ __forceinline__ void bwd_row_body(uint64_t src, float wt, uint32_t t,
           VX::cvt(gr[h][u], go);
 #pragma unroll
           for (int v = 0; v < V; ++v) y[v] = go[v] * wt;
-          VX::st(rgx, off[h][u], y);  // beyond D: dropped by the range check
+          VX::template st<FMOE_GX_CPOL>(rgx, off[h][u], y);
         }
         if constexpr (GW) part += dot_partial<TX, V>(xr[h][u], gr[h][u]);
       }
@@ -243,94 +146,35 @@ __device__ __forceinline__ void bwd_row_body(uint64_t src, float wt, uint32_t t,
   }
 }
 
-template <typename TX, int V, int U, bool GX, bool GW>
-__global__ __launch_bounds__(kGroup) void k_bwd_rows(const int32_t* __restrict__ status,
-                                                     const Rec* __restrict__ row_rec,
-                                                     const TX* __restrict__ gout, int64_t gstride,
-                                                     TX* __restrict__ gx, void* __restrict__ gw,
-                                                     int gw_dtype, uint32_t D, uint32_t N) {
-  const uint32_t g = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave);
-  if (g >= N) return;
-  const Rec r = row_rec[g];
-  if (r.g < 0) {  // out-of-range scatter index: zero gradients
-    bwd_zero_row<TX, V, GX, GW>(g, gx, gw, gw_dtype, D);
-    return;
-  }
-  if (V > 1 && status[kStatusMisaligned] != 0)
-    bwd_row_body<TX, V, U, GX, GW, false>(r.src, r.w, (uint32_t)r.g, g, gout, gstride, gx, gw,
-                                          gw_dtype, D);
-  else
-    bwd_row_body<TX, V, U, GX, GW, true>(r.src, r.w, (uint32_t)r.g, g, gout, gstride, gx, gw,
-                                         gw_dtype, D);
-}
+constexpr int kBwdWaves = FMOE_BWD_WAVES;
 
-// ---- token-grouped variant (the default) ------------------------------------------------------
-// A workgroup owns one token (plan segment); its 4 waves take the token's rows in turn, each
-// streaming a whole row (X read and grad_X write contiguous, non-temporal).  The rows of a token
-// run together on one CU, so grad_out[t] is fetched from HBM once and served from L2 to the
-// others.  grad_w needs no cross-wave reduction: every wave owns whole rows.
+// Workgroup per plan segment: token t = blockIdx.x; segment T holds the out-of-range rows.
 template <typename TX, int V, int U, bool GX, bool GW>
-__global__ __launch_bounds__(kGroup) void k_bwd_tok(const int32_t* __restrict__ status,
-                                                    const int32_t* __restrict__ row_ptr,
-                                                    const Rec* __restrict__ rec,
-                                                    const TX* __restrict__ gout, int64_t gstride,
-                                                    TX* __restrict__ gx, void* __restrict__ gw,
-                                                    int gw_dtype, uint32_t D, uint32_t T) {
+__global__ __launch_bounds__(kBwdWaves * kWave) void k_bwd_tok(const int32_t* __restrict__ status,
+                                                               const int32_t* __restrict__ row_ptr,
+                                                               const Rec* __restrict__ rec,
+                                                               const TX* __restrict__ gout,
+                                                               int64_t gstride,
+                                                               TX* __restrict__ gx,
+                                                               void* __restrict__ gw, int gw_dtype,
+                                                               uint32_t D, uint32_t T) {
+  const uint32_t t = blockIdx.x;
   const int wave = uniform(threadIdx.x / kWave);
   const bool al = !(V > 1 && status[kStatusMisaligned] != 0);
-  // Segments 0..T (T: out-of-range rows); a grid smaller than T + 1 strides over them.
-  for (uint32_t t = blockIdx.x; t <= T; t += gridDim.x) {
-    const int beg = row_ptr[t];
-    const int end = row_ptr[t + 1];
-    for (int j = beg + wave; j < end; j += kWavesPerGroup) {
-      const Rec r = rec[j];
-      if (t == T) {
-        bwd_zero_row<TX, V, GX, GW>((uint32_t)r.g, gx, gw, gw_dtype, D);
-      } else if (al) {
-        bwd_row_body<TX, V, U, GX, GW, true>(r.src, r.w, t, (uint32_t)r.g, gout, gstride, gx, gw,
-                                             gw_dtype, D);
-      } else {
-        bwd_row_body<TX, V, U, GX, GW, false>(r.src, r.w, t, (uint32_t)r.g, gout, gstride, gx, gw,
-                                              gw_dtype, D);
-      }
+  const int beg = row_ptr[t];
+  const int end = row_ptr[t + 1];
+  for (int j = beg + wave; j < end; j += kBwdWaves) {
+    const Rec r = rec[j];
+    if (t == T) {
+      bwd_zero_row<TX, V, GX, GW>((uint32_t)r.g, gx, gw, gw_dtype, D);
+    } else if (al) {
+      bwd_row_body<TX, V, U, GX, GW, true>(r.src, r.w, t, (uint32_t)r.g, gout, gstride, gx, gw,
+                                           gw_dtype, D);
+    } else {
+      bwd_row_body<TX, V, U, GX, GW, false>(r.src, r.w, t, (uint32_t)r.g, gout, gstride, gx, gw,
+                                            gw_dtype, D);
     }
   }
-}
-
-template <typename TX, int V, int U, int RB, bool GX, bool GW>
-__global__ __launch_bounds__(kGroup) void k_bwd(const int32_t* __restrict__ status,
-                                                const int32_t* __restrict__ row_ptr,
-                                                const Rec* __restrict__ rec,
-                                                const TX* __restrict__ gout, int64_t gstride,
-                                                TX* __restrict__ gx, void* __restrict__ gw,
-                                                int gw_dtype, uint32_t D, uint32_t T) {
-  const uint32_t t = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave);
-  if (t > T) return;
-  if (t == T) {  // rows with an out-of-range scatter index: zero gradients
-    const int lane = threadIdx.x & (kWave - 1);
-    const int beg = row_ptr[t];
-    const int end = row_ptr[t + 1];
-    const uint32_t rowb = D * (uint32_t)sizeof(TX);
-    for (int j = beg; j < end; ++j) {
-      const int64_t g = rec[j].g;
-      if constexpr (GX) {
-        float z[V];
-#pragma unroll
-        for (int v = 0; v < V; ++v) z[v] = 0.f;
-        const rsrc_t rz = make_rsrc(gx + g * D, rowb);
-        for (uint32_t col = (uint32_t)lane * V; col < D; col += kWave * V)
-          Vec<TX, V>::st(rz, col * (uint32_t)sizeof(TX), z);
-      }
-      if constexpr (GW) {
-        if (lane == 0) store_gate(gw, gw_dtype, g, 0.0);
-      }
-    }
-    return;
-  }
-  if (V > 1 && status[kStatusMisaligned] != 0)
-    bwd_body<TX, V, U, RB, GX, GW, false>(row_ptr, rec, gout, gstride, gx, gw, gw_dtype, D, t);
-  else
-    bwd_body<TX, V, U, RB, GX, GW, true>(row_ptr, rec, gout, gstride, gx, gw, gw_dtype, D, t);
 }
 
 static int env_int_b(const char* name, int dflt) {
@@ -342,8 +186,6 @@ struct BwdArgs {
   const int32_t* status;
   const int32_t* row_ptr;
   const Rec* rec;
-  const Rec* row_rec;
-  int64_t N;
   const void* gout;
   int64_t gstride;
   void* gx;
@@ -353,57 +195,28 @@ struct BwdArgs {
   hipStream_t s;
 };
 
-template <typename TX, int V, int U, int RB, bool GX, bool GW>
+template <typename TX, int V, int U, bool GX, bool GW>
 static int launch_bwd_k(const BwdArgs& a) {
-  const int64_t blocks = (a.T + 1 + kWavesPerGroup - 1) / kWavesPerGroup;
-  hipLaunchKernelGGL((k_bwd<TX, V, U, RB, GX, GW>), dim3((unsigned)blocks), dim3(kGroup), 0, a.s,
-                     a.status, a.row_ptr, a.rec, static_cast<const TX*>(a.gout), a.gstride,
-                     static_cast<TX*>(a.gx), a.gw, a.gw_dtype, (uint32_t)a.D, (uint32_t)a.T);
+  hipLaunchKernelGGL((k_bwd_tok<TX, V, U, GX, GW>), dim3((unsigned)(a.T + 1)),
+                     dim3(kBwdWaves * kWave), 0, a.s, a.status, a.row_ptr, a.rec,
+                     static_cast<const TX*>(a.gout), a.gstride, static_cast<TX*>(a.gx), a.gw,
+                     a.gw_dtype, (uint32_t)a.D, (uint32_t)a.T);
   return fmoe_host::check_launch("fmoe_combine_bwd");
 }
 
-template <typename TX, int V, int U, int RB>
+// FMOE_BWD_FUSED=1 runs both gradients in one pass (kept for measurement).
+template <typename TX, int V, int U>
 static int launch_bwd_u(const BwdArgs& a) {
-  if (a.gx && a.gw) return launch_bwd_k<TX, V, U, RB, true, true>(a);
-  if (a.gx) return launch_bwd_k<TX, V, U, RB, true, false>(a);
-  return launch_bwd_k<TX, V, U, RB, false, true>(a);
+  if (a.gx && a.gw) {
+    if (env_int_b("FMOE_BWD_FUSED", 0)) return launch_bwd_k<TX, V, U, true, true>(a);
+    if (int rc = launch_bwd_k<TX, V, U, true, false>(a)) return rc;  // grad_X: write pass
+    return launch_bwd_k<TX, V, U, false, true>(a);                   // grad_w: read pass
+  }
+  if (a.gx) return launch_bwd_k<TX, V, U, true, false>(a);
+  return launch_bwd_k<TX, V, U, false, true>(a);
 }
 
-template <typename TX, int V, int U, bool GX, bool GW>
-static int launch_bwd_rows_k(const BwdArgs& a) {
-  const int64_t blocks = (a.N + kWavesPerGroup - 1) / kWavesPerGroup;
-  hipLaunchKernelGGL((k_bwd_rows<TX, V, U, GX, GW>), dim3((unsigned)blocks), dim3(kGroup), 0, a.s,
-                     a.status, a.row_rec, static_cast<const TX*>(a.gout), a.gstride,
-                     static_cast<TX*>(a.gx), a.gw, a.gw_dtype, (uint32_t)a.D, (uint32_t)a.N);
-  return fmoe_host::check_launch("fmoe_combine_bwd(rows)");
-}
-
-template <typename TX, int V, int U, bool GX, bool GW>
-static int launch_bwd_tok_k(const BwdArgs& a) {
-  int64_t grid = a.T + 1;
-  const int persist = env_int_b("FMOE_BWD_GRID", 0);  // workgroups; 0 = one per segment
-  if (persist > 0 && persist < grid) grid = persist;
-  hipLaunchKernelGGL((k_bwd_tok<TX, V, U, GX, GW>), dim3((unsigned)grid), dim3(kGroup), 0, a.s,
-                     a.status, a.row_ptr, a.rec, static_cast<const TX*>(a.gout), a.gstride,
-                     static_cast<TX*>(a.gx), a.gw, a.gw_dtype, (uint32_t)a.D, (uint32_t)a.T);
-  return fmoe_host::check_launch("fmoe_combine_bwd(tok)");
-}
-
-template <typename TX, int V, int U>
-static int launch_bwd_tok(const BwdArgs& a) {
-  if (a.gx && a.gw) return launch_bwd_tok_k<TX, V, U, true, true>(a);
-  if (a.gx) return launch_bwd_tok_k<TX, V, U, true, false>(a);
-  return launch_bwd_tok_k<TX, V, U, false, true>(a);
-}
-
-template <typename TX, int V, int U>
-static int launch_bwd_rows(const BwdArgs& a) {
-  if (a.gx && a.gw) return launch_bwd_rows_k<TX, V, U, true, true>(a);
-  if (a.gx) return launch_bwd_rows_k<TX, V, U, true, false>(a);
-  return launch_bwd_rows_k<TX, V, U, false, true>(a);
-}
-
-// Tile shapes (U, R); FMOE_BWD_TILE=<U><R> (e.g. "28") overrides the choice for tuning.
+// U 16-byte vectors per lane per column step: 4 unless D is small (FMOE_BWD_U=1|2|4 overrides).
 template <typename TX>
 static int launch_bwd_x(const BwdArgs& a) {
   constexpr int V = vec16<TX>();
@@ -411,31 +224,13 @@ static int launch_bwd_x(const BwdArgs& a) {
   const bool vec_ok = (a.D % V == 0) && ((uintptr_t)a.gout % 16 == 0) &&
                       ((a.gstride * eb) % 16 == 0) && ((uintptr_t)a.gx % 16 == 0) &&
                       env_int_b("FMOE_FORCE_SCALAR", 0) == 0;
-  if (!vec_ok) return launch_bwd_u<TX, 1, 4, 4>(a);
-  // Token-grouped whole rows by default; FMOE_BWD_ORDER=row / =column select the packed-row-major
-  // and the token-major column-tiled kernels (kept for comparison).
-  const char* order = getenv("FMOE_BWD_ORDER");
-  const int ur = env_int_b("FMOE_BWD_ROWS_U", 2);
-  if (!order || order[0] == 't') {
-    if (ur == 4) return launch_bwd_tok<TX, V, 4>(a);
-    if (ur == 1) return launch_bwd_tok<TX, V, 1>(a);
-    return launch_bwd_tok<TX, V, 2>(a);
-  }
-  if (order[0] == 'r') {
-    if (ur == 4) return launch_bwd_rows<TX, V, 4>(a);
-    if (ur == 1) return launch_bwd_rows<TX, V, 1>(a);
-    return launch_bwd_rows<TX, V, 2>(a);
-  }
-  const int tile = env_int_b("FMOE_BWD_TILE", 0);
-  int U = tile / 10, R = tile % 10;
-  if (!((U == 4 && R == 4) || (U == 2 && (R == 8 || R == 4)) || (U == 1 && R == 8))) {
-    U = a.D >= (int64_t)kWave * V * 2 ? 2 : 1;
-    R = U == 2 ? 4 : 8;
-  }
-  if (U == 4) return launch_bwd_u<TX, V, 4, 4>(a);
-  if (U == 2 && R == 8) return launch_bwd_u<TX, V, 2, 8>(a);
-  if (U == 2) return launch_bwd_u<TX, V, 2, 4>(a);
-  return launch_bwd_u<TX, V, 1, 8>(a);
+  if (!vec_ok) return launch_bwd_u<TX, 1, 4>(a);
+  int U = env_int_b("FMOE_BWD_U", 0);
+  if (U != 1 && U != 2 && U != 4)
+    U = a.D >= (int64_t)kWave * V * 4 * 2 ? 4 : (a.D >= (int64_t)kWave * V * 2 * 2 ? 2 : 1);
+  if (U == 4) return launch_bwd_u<TX, V, 4>(a);
+  if (U == 2) return launch_bwd_u<TX, V, 2>(a);
+  return launch_bwd_u<TX, V, 1>(a);
 }
 
 }  // namespace fmoe
@@ -472,8 +267,6 @@ extern "C" int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t nu
   a.status = reinterpret_cast<const int32_t*>(ws + fmoe_plan_status_offset());
   a.row_ptr = reinterpret_cast<const int32_t*>(ws + fmoe_plan_row_ptr_offset(N, T));
   a.rec = reinterpret_cast<const Rec*>(ws + fmoe_plan_records_offset(N, T));
-  a.row_rec = reinterpret_cast<const Rec*>(ws + plan_row_records_offset(N, T));
-  a.N = N;
   a.gout = d_grad_out;
   a.gstride = gout_row_stride;
   a.gx = d_grad_x;

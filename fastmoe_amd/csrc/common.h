@@ -117,6 +117,17 @@ __device__ __forceinline__ rsrc_t make_rsrc(uint64_t base, uint32_t bytes) {
 
 constexpr int kCPolCached = 0;  // default policy: keep in L2 / Infinity Cache (re-read data)
 
+// Backward cache policies and workgroup shape (compile-time knobs; defaults measured best).
+#ifndef FMOE_GX_CPOL
+#define FMOE_GX_CPOL 2   // grad_X stores: non-temporal
+#endif
+#ifndef FMOE_GOUT_CPOL
+#define FMOE_GOUT_CPOL 0 // grad_out loads: cached, shared by the rows of a token through L2
+#endif
+#ifndef FMOE_BWD_WAVES
+#define FMOE_BWD_WAVES 4 // waves per token workgroup of the backward
+#endif
+
 template <int BYTES> struct Raw;
 template <> struct Raw<32> {  // two 16-byte accesses (8 fp32 results of one 16-bit input vector)
   using type = u32x8;
@@ -127,9 +138,10 @@ template <> struct Raw<32> {  // two 16-byte accesses (8 fp32 results of one 16-
         __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off + 16, 0, CP));
     return type{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   }
+  template <int CP = kCPol>
   static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[0], v[1], v[2], v[3]}, r, (int)off, 0, kCPol);
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[4], v[5], v[6], v[7]}, r, (int)off + 16, 0, kCPol);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[0], v[1], v[2], v[3]}, r, (int)off, 0, CP);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[4], v[5], v[6], v[7]}, r, (int)off + 16, 0, CP);
   }
   static __device__ __forceinline__ uint32_t word(const type& v, int i) { return v[i]; }
 };
@@ -139,8 +151,9 @@ template <> struct Raw<16> {
   static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(type, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CP));
   }
+  template <int CP = kCPol>
   static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kCPol);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, CP);
   }
   static __device__ __forceinline__ uint32_t word(const type& v, int i) { return v[i]; }
 };
@@ -150,8 +163,9 @@ template <> struct Raw<8> {
   static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(type, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, CP));
   }
+  template <int CP = kCPol>
   static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
-    __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, kCPol);
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, CP);
   }
   static __device__ __forceinline__ uint32_t word(const type& v, int i) { return v[i]; }
 };
@@ -161,8 +175,9 @@ template <> struct Raw<4> {
   static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, CP);
   }
+  template <int CP = kCPol>
   static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
-    __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, kCPol);
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, CP);
   }
   static __device__ __forceinline__ uint32_t word(const type& v, int) { return v; }
 };
@@ -172,8 +187,9 @@ template <> struct Raw<2> {
   static __device__ __forceinline__ type ld(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, CP);
   }
+  template <int CP = kCPol>
   static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, type v) {
-    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)off, 0, kCPol);
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)off, 0, CP);
   }
   static __device__ __forceinline__ uint32_t word(const type& v, int) { return v; }
 };
@@ -229,8 +245,9 @@ template <typename T, int V> struct Vec {
     }
     return raw;
   }
+  template <int CP = kCPol>
   static __device__ __forceinline__ void st(rsrc_t r, uint32_t off, const float* f) {
-    R::st(r, off, pack(f));
+    R::template st<CP>(r, off, pack(f));
   }
 };
 

@@ -9,15 +9,12 @@
 //   rec[N]          : 16-byte records {source row address, fp32 gate, g}; a segment of up to 64
 //                     rows is unordered (consumers that need the order rank it in registers),
 //                     a longer one is in ascending g
-//   row_rec[N]      : the same per packed row g, in g order, with the token in place of g (-1 for
-//                     an out-of-range index) -- read by the packed-row-major backward
 //
 // Steps (all on the caller's stream, no host synchronisation):
 //   1. count + scan   one 1024-thread workgroup histograms idx into LDS (T + 1 <= kLdsTokens) and
 //                     scans it; larger T fall back to zero / global-atomic count / one-block scan.
 //   2. fill           one thread per row: claims a slot in its segment with an atomic cursor and
-//                     writes its record (arbitrary order inside the segment) plus its g-ordered
-//                     row record.
+//                     writes its record (arbitrary order inside the segment).
 //   3. order          segments longer than 64 rows only (never for top-k routing; the kernel
 //                     exits at once otherwise): one wave per segment ranks its records by g and
 //                     writes them in order.
@@ -31,7 +28,7 @@ constexpr int kScanThreads = 1024;
 constexpr int kLdsTokens = 33792;  // 132 KiB of LDS histogram (gfx950: 160 KiB per workgroup)
 
 struct PlanLayout {
-  int64_t status, cursor, row_ptr, rec_tmp, rec, row_rec, total;
+  int64_t status, cursor, row_ptr, rec_tmp, rec, total;
 };
 
 __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
@@ -42,8 +39,7 @@ __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
   L.row_ptr = L.cursor + up((T + 1) * 4);
   L.rec_tmp = L.row_ptr + up((T + 2) * 4);
   L.rec = L.rec_tmp + up(N * 16);
-  L.row_rec = L.rec + up(N * 16);
-  L.total = L.row_rec + up(N * 16);
+  L.total = L.rec + up(N * 16);
   return L;
 }
 
@@ -207,8 +203,7 @@ __global__ __launch_bounds__(kGroup) void k_plan_fill(
     const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T,
     const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
     int64_t row_bytes, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ cursor,
-    Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, Rec* __restrict__ row_rec,
-    int32_t* __restrict__ status) {
+    Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, int32_t* __restrict__ status) {
   __shared__ int64_t off_lds[kLdsExperts + 1];
   const bool lds_off = E <= kLdsExperts;
   if (lds_off)
@@ -226,8 +221,6 @@ __global__ __launch_bounds__(kGroup) void k_plan_fill(
     r.w = ld1(w + g);
     r.g = (int32_t)g;
     (long_seg ? rec_tmp : rec)[pos] = r;
-    r.g = (b == T) ? -1 : (int32_t)t;
-    row_rec[g] = r;
     if (r.src & 15) atomicOr(&status[kStatusMisaligned], 1);
   }
 }
@@ -267,12 +260,6 @@ extern "C" int64_t fmoe_plan_row_ptr_offset(int64_t num_rows, int64_t num_tokens
 extern "C" int64_t fmoe_plan_records_offset(int64_t num_rows, int64_t num_tokens) {
   return fmoe::plan_layout(num_rows, num_tokens).rec;
 }
-namespace fmoe {
-int64_t plan_row_records_offset(int64_t num_rows, int64_t num_tokens) {
-  return plan_layout(num_rows, num_tokens).row_rec;
-}
-}  // namespace fmoe
-
 extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d_weights,
                                int w_dtype, int64_t num_rows, int64_t num_tokens,
                                const int64_t* d_ptr_table, const int64_t* d_offsets,
@@ -305,7 +292,6 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
   Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
-  Rec* row_rec = reinterpret_cast<Rec*>(ws + L.row_rec);
   const int64_t nb = T + 1;
 
   if (nb <= kLdsTokens && N < (int64_t(1) << 27)) {
@@ -334,8 +320,7 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
 #define FMOE_FILL(TI, TW)                                                                          \
   hipLaunchKernelGGL((k_plan_fill<TI, TW>), grid, dim3(kGroup), 0, s,                              \
                      static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
-                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, cursor, rec_tmp, rec, row_rec, \
-                     status)
+                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, cursor, rec_tmp, rec, status)
   if (idx_dtype == FMOE_I64) {
     if (w_dtype == FMOE_F32) FMOE_FILL(int64_t, float);
     else if (w_dtype == FMOE_BF16) FMOE_FILL(int64_t, bf16_t);

@@ -359,15 +359,26 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
     gx = torch.empty((N, D), dtype=ctx.x_dtype, device=dev) if need_x else None
     gw = torch.empty(N, dtype=w.dtype, device=dev) if needs_w else None
     lib = _abi.lib()
-    with torch.cuda.device(dev), _span("bwd"):
-        rc = lib.fmoe_combine_bwd(
-            ctx.plan.data_ptr(), N, T, D, _FLOAT_CODES[ctx.x_dtype], go.data_ptr(),
-            _FLOAT_CODES[go.dtype], go.stride(0) if T > 1 else D,
-            gx.data_ptr() if gx is not None else None,
-            gw.data_ptr() if gw is not None else None,
-            _FLOAT_CODES[w.dtype], _stream_handle(dev),
-        )
-    _abi.check(rc, "fmoe_combine_bwd")
+
+    def launch(name, gx_ptr, gw_ptr):
+        with torch.cuda.device(dev), _span(name):
+            rc = lib.fmoe_combine_bwd(
+                ctx.plan.data_ptr(), N, T, D, _FLOAT_CODES[ctx.x_dtype], go.data_ptr(),
+                _FLOAT_CODES[go.dtype], go.stride(0) if T > 1 else D, gx_ptr, gw_ptr,
+                _FLOAT_CODES[w.dtype], _stream_handle(dev),
+            )
+        _abi.check(rc, "fmoe_combine_bwd")
+
+    gx_ptr = gx.data_ptr() if gx is not None else None
+    gw_ptr = gw.data_ptr() if gw is not None else None
+    fused = os.environ.get("FMOE_BWD_FUSED", "") not in ("", "0")
+    if gx_ptr and gw_ptr and not fused:
+        # The grad_X (write) and grad_w (read) passes, one call each -- the same two launches
+        # fmoe_combine_bwd makes when given both outputs, issued separately so each is timed.
+        launch("bwd_gx", gx_ptr, None)
+        launch("bwd_gw", None, gw_ptr)
+    else:
+        launch("bwd" if gx_ptr and gw_ptr else ("bwd_gx" if gx_ptr else "bwd_gw"), gx_ptr, gw_ptr)
     if need_x:
         parts = torch.split(gx, list(sizes))
         grads_x = [p if n else None for p, n in zip(parts, needs_x)]

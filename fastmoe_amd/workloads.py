@@ -101,3 +101,22 @@ def algorithmic_bytes(T: int, D: int, N: int, x_bytes: int, out_bytes: int, gate
     if grad_w:
         bwd += N * gate_bytes
     return fwd, bwd
+
+
+def kernel_bytes(T: int, D: int, N: int, x_bytes: int, out_bytes: int,
+                 gate_bytes: int = 4) -> dict:
+    """Compulsory HBM bytes of one launch of each kernel of the step, by timing-span name.
+
+    fwd_det / fwd_atomic : the forward (as ``algorithmic_bytes``)
+    bwd_gx               : read grad_out (T*D) + write grad_X (N*D) + read idx and w per row
+    bwd_gw               : read grad_out (T*D) + read X (N*D) + read idx, write grad_w per row
+    bwd                  : both gradients in one pass (as ``algorithmic_bytes``)
+    """
+    fwd, bwd = algorithmic_bytes(T, D, N, x_bytes, out_bytes, gate_bytes)
+    return {
+        "fwd_det": fwd,
+        "fwd_atomic": fwd,
+        "bwd_gx": T * D * x_bytes + N * D * x_bytes + N * (8 + gate_bytes),
+        "bwd_gw": T * D * x_bytes + N * D * x_bytes + N * (8 + gate_bytes),
+        "bwd": bwd,
+    }

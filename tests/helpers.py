@@ -61,3 +61,40 @@ def abs_sum(experts, idx, w, T):
     xs_abs = [np.abs(cref.widen(x, code)) for x in xs]
     acc, _ = cref.combine_fwd(xs_abs, to_np(idx.long()), np.abs(to_np(w.float())), T, D, cref.F32)
     return acc
+
+
+# ---- golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py) -------------
+GOLDEN_DIR = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+_TORCH_DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def golden_names():
+    return sorted(p.stem for p in GOLDEN_DIR.glob("*.npz"))
+
+
+def _from_store(a: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+    if dtype in (torch.bfloat16, torch.float16):
+        return torch.from_numpy(a.view(np.int16).copy()).view(dtype)
+    return torch.from_numpy(a.copy())
+
+
+def load_golden(name: str) -> dict:
+    """A fixture as CPU tensors: experts (list), idx, w, grad_out, T, D, and the stored expected
+    arrays (bit patterns) under their own keys."""
+    z = np.load(GOLDEN_DIR / f"{name}.npz", allow_pickle=False)
+    xdt = _TORCH_DTYPES[str(z["x_dtype"])]
+    wdt = _TORCH_DTYPES[str(z["w_dtype"])]
+    x = _from_store(z["x"], xdt)
+    sizes = [int(s) for s in z["sizes"]]
+    case = {k: z[k] for k in z.files}
+    case.update(
+        experts=[t.contiguous() for t in torch.split(x, sizes)],
+        idx=torch.from_numpy(z["idx"].copy()),
+        w=_from_store(z["w"], wdt),
+        grad_out=_from_store(z["grad_out"], xdt),
+        T=int(z["T"]),
+        D=int(z["D"]),
+        x_dtype=xdt,
+        w_dtype=wdt,
+    )
+    return case

@@ -90,13 +90,25 @@ def test_autograd_forward_and_backward_calls(fake):
     assert out.shape == (4, 16) and out.dtype == torch.bfloat16
     grads = torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
     kinds = [c[0] for c in fake.calls]
-    assert kinds == ["metadata", "plan", "fwd", "bwd"]
+    assert kinds == ["metadata", "plan", "fwd", "bwd", "bwd"]
     assert fake.calls[0] == ("metadata", 3, [3, 0, 5])
     assert fake.calls[1] == ("plan", 8, 4, 3, 32, _abi.I64, _abi.F32)
     assert fake.calls[2] == ("fwd", _abi.MODE_DET, 8, 4, 16, _abi.BF16, _abi.BF16, 16, 0)
-    assert fake.calls[3] == ("bwd", 8, 4, 16, _abi.BF16, 16, True, True, _abi.F32)
+    # grad_X pass, then grad_w pass
+    assert fake.calls[3] == ("bwd", 8, 4, 16, _abi.BF16, 16, True, False, _abi.F32)
+    assert fake.calls[4] == ("bwd", 8, 4, 16, _abi.BF16, 16, False, True, _abi.F32)
     assert grads[0].shape == (N,) and grads[0].dtype == torch.float32
     assert [g.shape[0] for g in grads[1:]] == [3, 0, 5]
+
+
+def test_fused_backward_is_one_call(fake, monkeypatch):
+    monkeypatch.setenv("FMOE_BWD_FUSED", "1")
+    xs = [x.requires_grad_(True) for x in _experts()]
+    w = torch.rand(8, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, 4, (8,)), w, (4, 16))
+    torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
+    assert [c[0] for c in fake.calls] == ["metadata", "plan", "fwd", "bwd"]
+    assert fake.calls[3][6:8] == (True, True)
 
 
 def test_backward_skips_unneeded_outputs(fake):

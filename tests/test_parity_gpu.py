@@ -90,10 +90,25 @@ def test_fwd_fp32_atomic_vs_det_on_published_shape():
     assert rel.max() <= 1e-6
 
 
-@pytest.mark.parametrize("order", ["token", "row", "column"])
+# Backward launch shapes: split grad_X / grad_w passes (default), the fused single pass, and the
+# narrower column steps chosen for small D.
+_BWD_VARIANTS = {
+    "split": {},
+    "fused": {"FMOE_BWD_FUSED": "1"},
+    "split_u1": {"FMOE_BWD_U": "1"},
+    "fused_u2": {"FMOE_BWD_FUSED": "1", "FMOE_BWD_U": "2"},
+}
+
+
+def _set_bwd_variant(monkeypatch, variant):
+    for k, v in _BWD_VARIANTS[variant].items():
+        monkeypatch.setenv(k, v)
+
+
+@pytest.mark.parametrize("variant", list(_BWD_VARIANTS))
 @pytest.mark.parametrize("name", ["plumbing", "gigachat", "skewed"])
-def test_bwd_grad_x_bitexact_grad_w_close(name, order, monkeypatch):
-    monkeypatch.setenv("FMOE_BWD_ORDER", order)
+def test_bwd_grad_x_bitexact_grad_w_close(name, variant, monkeypatch):
+    _set_bwd_variant(monkeypatch, variant)
     wl, T, idx, w, experts = _inputs(name)
     xd, idd, wd = _to_dev(experts, idx, w)
     xd = [x.requires_grad_(True) for x in xd]
@@ -111,6 +126,33 @@ def test_bwd_grad_x_bitexact_grad_w_close(name, order, monkeypatch):
     err = np.abs(gw.double().cpu().numpy() - want_gw)
     assert np.all(err <= 1e-6 * scale + 1e-30)
     assert gw.dtype == wd.dtype
+
+
+@pytest.mark.parametrize("fused", ["0", "1"])
+def test_bwd_abi_both_outputs_in_one_call(fused, monkeypatch):
+    """fmoe_combine_bwd given both outputs (the call a C-ABI binding makes): grad_X and grad_w
+    from its two back-to-back passes (or the fused pass) equal the oracle."""
+    monkeypatch.setenv("FMOE_BWD_FUSED", fused)
+    wl, T, idx, w, experts = _inputs("gigachat")
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
+    plan = fastmoe_amd.build_plan(meta, idd, wd, T)
+    N, D = idx.numel(), wl.D
+    gen = torch.Generator().manual_seed(11)
+    grad_out = torch.randn(T, D, generator=gen).to(wl.dtype)
+    god = grad_out.to(DEV)
+    gx = torch.full((N, D), float("nan"), dtype=wl.dtype, device=DEV)
+    gw = torch.full((N,), float("nan"), dtype=torch.float32, device=DEV)
+    lib = fastmoe_amd._abi.lib()
+    rc = lib.fmoe_combine_bwd(plan.data_ptr(), N, T, D, fastmoe_amd._abi.BF16, god.data_ptr(),
+                              fastmoe_amd._abi.BF16, D, gx.data_ptr(), gw.data_ptr(),
+                              fastmoe_amd._abi.F32, torch.cuda.current_stream().cuda_stream)
+    fastmoe_amd._abi.check(rc, "fmoe_combine_bwd")
+    torch.cuda.synchronize()
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, grad_out)
+    np.testing.assert_array_equal(to_np(gx), want_gx)
+    scale = abs_dot(experts, idx, grad_out, T)
+    assert np.all(np.abs(gw.double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
 def test_bwd_without_gate_grad_and_without_expert_grad():
@@ -240,9 +282,9 @@ def test_edge_large_segments_randint():
     assert np.all(np.abs(g[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
-@pytest.mark.parametrize("order", ["token", "row", "column"])
-def test_edge_invalid_indices_dropped_and_flagged(order, monkeypatch):
-    monkeypatch.setenv("FMOE_BWD_ORDER", order)
+@pytest.mark.parametrize("variant", ["split", "fused"])
+def test_edge_invalid_indices_dropped_and_flagged(variant, monkeypatch):
+    _set_bwd_variant(monkeypatch, variant)
     D, T = 32, 6
     gen = torch.Generator().manual_seed(5)
     experts = [torch.randn(4, D, generator=gen), torch.randn(3, D, generator=gen)]
@@ -382,14 +424,7 @@ def test_plan_matches_oracle():
     e_of = np.searchsorted(off, want_g, side="right") - 1
     src = np.array([meta.ptrs[e] for e in e_of], dtype=np.int64) + (want_g - off[e_of]) * wl.D * 2
     np.testing.assert_array_equal(rec[:, 0].numpy(), src)
-    # the g-indexed row records: {src, w, token}
-    rr_off = lib.fmoe_plan_records_offset(N, T) + ((16 * N + 255) // 256) * 256
-    rr = plan[rr_off: rr_off + 16 * N].view(torch.int64).view(N, 2).cpu()
-    tok = (rr[:, 1] >> 32).numpy().astype(np.int32)
-    np.testing.assert_array_equal(tok, idx.numpy())
-    e_of = np.searchsorted(off, np.arange(N), side="right") - 1
-    src = np.array([meta.ptrs[e] for e in e_of], dtype=np.int64) + (np.arange(N) - off[e_of]) * wl.D * 2
-    np.testing.assert_array_equal(rr[:, 0].numpy(), src)
+    assert lib.fmoe_plan_workspace_bytes(N, T) == plan.numel()
 
 
 def test_metadata_matches_closed_forms():
