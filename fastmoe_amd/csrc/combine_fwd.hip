@@ -96,7 +96,8 @@ __device__ __forceinline__ void fwd_det_body(const int32_t* __restrict__ row_ptr
     }
   }
 #pragma unroll
-  for (int u = 0; u < U; ++u) VO::st(ro, ooff[u], acc[u]);  // columns >= D: dropped by range check
+  for (int u = 0; u < U; ++u)  // columns >= D: dropped by range check
+    VO::template st<FMOE_OUT_CPOL>(ro, ooff[u], acc[u]);
 }
 
 template <typename TX, typename TO, int V, int U, int RB>

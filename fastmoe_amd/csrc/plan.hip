@@ -20,6 +20,8 @@
 //                     writes them in order.
 //                     Shorter segments are ordered by the consumer in registers, so every result
 //                     is bit-identical run to run even though the fill order is not.
+#include <algorithm>
+
 #include "common.h"
 
 namespace fmoe {
@@ -225,8 +227,11 @@ __global__ __launch_bounds__(kGroup) void k_plan_fill(
   }
 }
 
-// One wave per token segment, launched after the fill; it exits at once unless some segment is
-// longer than one wave (never for top-k routing: the scan recorded the longest segment).
+// Launched after the fill; exits at once unless some segment is longer than one wave (never for
+// top-k routing: the scan recorded the longest segment).  Otherwise each wave takes token
+// segments in turn (a small grid strides over them, so the early exit costs little dispatch).
+constexpr int kSortGroups = 256;
+
 __global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __restrict__ row_ptr,
                                                            int64_t T,
                                                            const int32_t* __restrict__ status,
@@ -234,16 +239,17 @@ __global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __rest
                                                            Rec* __restrict__ rec) {
   if (status[kStatusLongest] <= kWave) return;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t b = (int64_t)blockIdx.x * kWavesPerGroup + uniform(threadIdx.x / kWave);
-  if (b >= T) return;
-  const int beg = row_ptr[b];
-  const int c = row_ptr[b + 1] - beg;
-  if (c <= kWave) return;
-  for (int i = lane; i < c; i += kWave) {
-    const Rec r = scratch[beg + i];
-    int rank = 0;
-    for (int m = 0; m < c; ++m) rank += (scratch[beg + m].g < r.g) ? 1 : 0;
-    rec[beg + rank] = r;
+  for (int64_t b = (int64_t)blockIdx.x * kWavesPerGroup + uniform(threadIdx.x / kWave); b < T;
+       b += (int64_t)gridDim.x * kWavesPerGroup) {
+    const int beg = row_ptr[b];
+    const int c = row_ptr[b + 1] - beg;
+    if (c <= kWave) continue;
+    for (int i = lane; i < c; i += kWave) {
+      const Rec r = scratch[beg + i];
+      int rank = 0;
+      for (int m = 0; m < c; ++m) rank += (scratch[beg + m].g < r.g) ? 1 : 0;
+      rec[beg + rank] = r;
+    }
   }
 }
 
@@ -332,7 +338,8 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   }
 #undef FMOE_FILL
   if (int rc = fmoe_host::check_launch("fmoe_build_plan(fill)")) return rc;
-  hipLaunchKernelGGL(k_plan_sort_long, dim3((unsigned)((T + kWavesPerGroup - 1) / kWavesPerGroup)),
-                     dim3(kGroup), 0, s, row_ptr, T, status, rec_tmp, rec);
+  const int64_t sort_groups = std::min<int64_t>((T + kWavesPerGroup - 1) / kWavesPerGroup, kSortGroups);
+  hipLaunchKernelGGL(k_plan_sort_long, dim3((unsigned)sort_groups), dim3(kGroup), 0, s, row_ptr, T,
+                     status, rec_tmp, rec);
   return fmoe_host::check_launch("fmoe_build_plan(sort)");
 }

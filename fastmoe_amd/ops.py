@@ -247,9 +247,10 @@ def build_plan(meta: GroupedMetadata, indices: torch.Tensor, weights: torch.Tens
 
 
 def plan_status(plan: torch.Tensor) -> torch.Tensor:
-    """The plan's int32 status words [invalid_index_count, misaligned_flag] (a device view)."""
+    """The plan's int32 status words [invalid_index_count, misaligned_flag, longest_segment]
+    (a device view; longest_segment counts the rows of the busiest token)."""
     off = _abi.lib().fmoe_plan_status_offset()
-    return plan[off: off + 8].view(torch.int32)
+    return plan[off: off + 12].view(torch.int32)
 
 
 def _check_out(out: torch.Tensor, num_tokens_hint, hidden: int, dev) -> None:

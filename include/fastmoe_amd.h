@@ -103,7 +103,7 @@ FMOE_API int fmoe_build_metadata(const int64_t* host_ptrs, const int64_t* host_r
  * idx[g] == t, each as a 16-byte record {source row address, fp32 gate, g}; a segment of up to
  * 64 rows is stored in no particular order (the deterministic forward orders it by g in
  * registers), a longer one in ascending g.  Rows with an out-of-range index form one extra
- * segment (number T).  The plan also holds the same records indexed by g for the backward.
+ * segment (number T).
  *
  * Workspace: fmoe_plan_workspace_bytes(N, T) bytes of device memory, 256-byte aligned, owned by the
  * caller; no zero-fill is needed.  Layout (byte offsets from the workspace base):
@@ -153,6 +153,7 @@ FMOE_API int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indice
  *              NULL to skip it.  grad_X[g] = round_x(f32(grad_out[idx[g]]) * w[g]).
  * d_grad_w   : [N] of gw_dtype, or NULL to skip it (then the expert buffers are not read).
  *              grad_w[g] accumulates the D products in fp64 and rounds once.
+ * Given both outputs, the call enqueues two kernels: the grad_X pass, then the grad_w pass.
  */
 FMOE_API int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t num_tokens, int64_t hidden,
                      int x_dtype, const void* d_grad_out, int gout_dtype, int64_t gout_row_stride,

@@ -260,7 +260,7 @@ def test_edge_all_experts_empty():
 
 
 def test_edge_large_segments_randint():
-    """Many rows per token (segments > 64) take the plan's large-segment sort."""
+    """Many rows per token (segments > 64) take the plan's long-segment ordering pass."""
     D, T, N = 40, 3, 700
     gen = torch.Generator().manual_seed(11)
     experts = [torch.randn(n, D, generator=gen) for n in (300, 0, 400)]
@@ -396,10 +396,18 @@ def test_dtype_combinations(xdt, wdt, idt, odt):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
-def test_plan_matches_oracle():
+@pytest.mark.parametrize("T", [512, 40])
+def test_plan_matches_oracle(T):
+    """row_ptr, the records (source address, gate bits, g) and the status words equal the
+    oracle's inverse.  At T=40, 200 extra rows on tokens 0..2 make segments longer than 64."""
     from oracle import cref
 
-    wl, T, idx, w, experts = _inputs("skewed", T=512)
+    wl, T, idx, w, experts = _inputs("skewed", T=T)
+    if T == 40:  # pile 200 extra rows onto tokens 0..2 through one more expert
+        gen = torch.Generator().manual_seed(3)
+        experts = experts + [torch.randn(200, wl.D, generator=gen).to(wl.dtype)]
+        idx = torch.cat([idx, torch.randint(0, 3, (200,), generator=gen)])
+        w = torch.cat([w, torch.rand(200, generator=gen)])
     xd, idd, wd = _to_dev(experts, idx, w)
     meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
     plan = fastmoe_amd.build_plan(meta, idd, wd, T)
@@ -411,8 +419,16 @@ def test_plan_matches_oracle():
     rec = plan[rec_off: rec_off + 16 * N].view(torch.int64).view(N, 2).cpu()
     want_rp, want_g = cref.plan(idx.numpy(), T)
     np.testing.assert_array_equal(row_ptr, want_rp)
-    # short segments are unordered in the plan: order each segment by g before comparing
     g = (rec[:, 1] >> 32).numpy().astype(np.int32)
+    seg_len = np.diff(want_rp)
+    for b in range(T):  # long segments are in ascending g
+        if seg_len[b] > 64:
+            assert np.all(np.diff(g[want_rp[b]:want_rp[b + 1]]) > 0), b
+    st = ops.plan_status(plan).cpu().numpy()
+    assert st[0] == 0 and st[1] == 0 and st[2] == seg_len[:T].max()
+    if T == 40:
+        assert st[2] > 64
+    # short segments may be unordered: order each segment by g before comparing
     order = np.concatenate([np.arange(want_rp[b], want_rp[b + 1])[np.argsort(g[want_rp[b]:want_rp[b + 1]])]
                             for b in range(T + 1)])
     rec = rec[torch.from_numpy(order)]
