@@ -109,6 +109,47 @@ def _cpu_baseline(wl, sample_tokens: int, reps: int):
     }
 
 
+def _standard_gpu(wl, xs, idx, w, grad_out, backward, steps, warmup, fast_ms):
+    """The reference's STANDARD combine in torch GPU ops on the same inputs and GPU: cat -> * w ->
+    index_add_ into fp32 zeros (run_on_cloud.py:43-48, the reference's own comparison column), and
+    with backward its autograd (index_select, mul, split, gate dot).  Eager, event-timed like the
+    reference's benchmark_standard (run_on_cloud.py:35-53); peak memory above the inputs."""
+    import torch
+
+    dev = idx.device
+    inputs = [w, *xs]
+
+    def std_step():
+        combined = torch.cat(xs, dim=0)
+        weighted = combined * w.unsqueeze(-1)
+        out = torch.zeros((wl.T, wl.D), device=dev)
+        out.index_add_(0, idx, weighted)
+        if backward:
+            torch.autograd.grad(out, inputs, grad_out.float())
+        return out
+
+    for _ in range(max(1, warmup)):
+        std_step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        std_step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    return {
+        "ms_per_step": round(ms, 4),
+        "peak_mem_gb": round((torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30, 3),
+        "speedup_of_fast": round(ms / fast_ms, 2),
+        "what": "torch GPU cat -> * w -> index_add_ into fp32 zeros"
+                + (" + autograd backward" if backward else "") + ", eager",
+    }
+
+
 def _cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -126,14 +167,18 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gigachat")
     ap.add_argument("--mode", default="det", choices=["det", "atomic"])
-    ap.add_argument("--fwd-only", action="store_true", help="time the forward alone")
+    ap.add_argument("--fwd-only", action="store_true",
+                    help="time the forward alone (the default for forward-only workloads)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager steps instead of graph replays")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="K",
                     help="also run K plain 1 GiB device copies (a reference kernel of known bytes "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=512)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=0,
+                    help="tokens of the CPU baseline sample (0 = the whole workload)")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-standard", action="store_true",
+                    help="skip the torch STANDARD combine timed on the same GPU")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -159,7 +204,7 @@ def main() -> int:
     idx, w, counts = make_routing(wl)
     idx, w = idx.to(dev), w.to(dev)
     xs = make_experts(counts, wl.D, wl.dtype, dev, wl.seed)
-    backward = not args.fwd_only
+    backward = wl.backward and not args.fwd_only
     if backward:
         xs = [x.requires_grad_(True) for x in xs]
         w.requires_grad_(True)
@@ -183,6 +228,12 @@ def main() -> int:
             b.copy_(a)
         torch.cuda.synchronize()
         del a, b
+
+    torch.cuda.reset_peak_memory_stats(dev)
+    base_mem = torch.cuda.memory_allocated(dev)
+    step()
+    torch.cuda.synchronize()
+    fast_peak = torch.cuda.max_memory_allocated(dev) - base_mem
 
     timer = EventTimer()
     ops._TIMER = timer
@@ -317,8 +368,12 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if not args.no_standard:
+        res["standard"] = _standard_gpu(wl, xs, idx, w, grad_out, backward, args.steps,
+                                         args.warmup, ms)
+        res["peak_mem_gb"] = round(fast_peak / 2 ** 30, 3)
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = _cpu_baseline(wl, args.cpu_sample_tokens, args.cpu_reps)
+        res["cpu_baseline"] = _cpu_baseline(wl, args.cpu_sample_tokens or wl.T, args.cpu_reps)
     print(json.dumps(res), flush=True)
     return 0
 
