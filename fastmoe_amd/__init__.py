@@ -4,6 +4,8 @@ The operator API mirrors ``fastmoe.kernels.ops``; the work runs in hand-written 
 ``libfastmoe_amd.so`` through its C ABI (``include/fastmoe_amd.h``).
 """
 from .consts import MoEImplementation
+from .dispatch import PermutedTokens, permute_tokens
+from .moe import MoEFeedForward, compute_experts, gate_and_sort, unpermute
 from .ops import (
     GroupedMetadata,
     GroupedWeightedScatterAdd,
@@ -16,7 +18,13 @@ from .ops import (
 __all__ = [
     "GroupedMetadata",
     "GroupedWeightedScatterAdd",
+    "MoEFeedForward",
     "MoEImplementation",
+    "PermutedTokens",
+    "compute_experts",
+    "gate_and_sort",
+    "permute_tokens",
+    "unpermute",
     "build_plan",
     "grouped_weighted_scatter_add",
     "prepare_grouped_metadata",

@@ -48,6 +48,14 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _c_int, _c_i64, _c_vp, _c_vp, _c_int, _c_vp],
     ),
+    "fmoe_permute_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "fmoe_permute_build": (
+        _c_int,
+        [_c_vp, _c_int, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+         _c_vp, _c_vp, _c_vp],
+    ),
+    "fmoe_permute_gather": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp]),
+    "fmoe_permute_gate_grad": (_c_int, [_c_vp, _c_i64, _c_vp, _c_int, _c_vp, _c_vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

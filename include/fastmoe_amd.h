@@ -30,6 +30,8 @@
  *   fmoe_build_plan        <- no counterpart: the token-major inverse of the scatter index that the
  *                             deterministic combine and the backward read (ops.py:344 gathers by
  *                             scatter index on the fly instead)
+ *   fmoe_permute_*         <- the sort-and-gather of MoEFeedForward.gate_and_sort
+ *                             src/fastmoe/models/tiny_model.py:108-138 (the combine's producer)
  */
 #ifndef FASTMOE_AMD_H
 #define FASTMOE_AMD_H
@@ -158,6 +160,46 @@ FMOE_API int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indice
 FMOE_API int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t num_tokens, int64_t hidden,
                      int x_dtype, const void* d_grad_out, int gout_dtype, int64_t gout_row_stride,
                      void* d_grad_x, void* d_grad_w, int gw_dtype, void* stream);
+
+/*
+ * Dispatch-side permutation: the routing slots of T tokens x top_k choices grouped by expert
+ * (replaces the sort-and-gather of MoEFeedForward.gate_and_sort,
+ * src/fastmoe/models/tiny_model.py:108-138).  Slot i = t * top_k + j.
+ *
+ * fmoe_permute_build (tiny_model.py:112 argsort, :121-125 reverse map, :128 sorted gates,
+ *                     :138 bincount):
+ *   d_expert_ids [T * top_k]  FMOE_I64 / FMOE_I32 expert id of each slot
+ *   d_gates      [T * top_k]  gate of each slot (any float dtype; copied bit for bit)
+ *   d_counts     [E] int64    rows per expert
+ *   d_offsets    [E + 1] int64 exclusive prefix of d_counts; d_offsets[E] = valid slots
+ *   d_rev        [T * top_k] int64  token of each packed row (the combine's scatter index)
+ *   d_sorted_gates [T * top_k]      gate of each packed row (the combine's gate weight)
+ *   d_slot_pos   [T * top_k] int32  packed row of each slot
+ *   d_status     [1] int32    slots whose id lies outside [0, E) (they go after every expert's
+ *                             rows, in slot order)
+ *   Packed order: experts ascending, and within an expert the slots in ascending order (a stable
+ *   sort; the reference's argsort is unstable, so its order of equal ids is unspecified).
+ *   Workspace: fmoe_permute_workspace_bytes(T * top_k, E) bytes, 256-byte aligned, no zero-fill.
+ *   E <= 4096.
+ *
+ * fmoe_permute_gather (tiny_model.py:133, x_flat[reverse_map_indices]):
+ *   out[d_slot_pos[t * top_k + j], :] = x[t, :] for every slot: a byte copy of row_bytes per
+ *   row; x rows are x_row_stride_bytes apart, out is packed [T * top_k, row_bytes].
+ *
+ * fmoe_permute_gate_grad (the backward of :128): grad_gates[i] = grad_sorted[d_slot_pos[i]].
+ * The backward of the gather is the deterministic combine with unit gates (fmoe_build_plan +
+ * fmoe_combine_fwd with the packed rows as one expert buffer and d_rev as scatter index).
+ */
+FMOE_API int64_t fmoe_permute_workspace_bytes(int64_t num_slots, int64_t num_experts);
+FMOE_API int fmoe_permute_build(const void* d_expert_ids, int id_dtype, const void* d_gates,
+                       int gate_dtype, int64_t num_tokens, int64_t top_k, int64_t num_experts,
+                       int64_t* d_counts, int64_t* d_offsets, int64_t* d_rev, void* d_sorted_gates,
+                       int32_t* d_slot_pos, int32_t* d_status, void* d_workspace, void* stream);
+FMOE_API int fmoe_permute_gather(const int32_t* d_slot_pos, int64_t num_tokens, int64_t top_k,
+                        int64_t row_bytes, const void* d_x, int64_t x_row_stride_bytes,
+                        void* d_out, void* stream);
+FMOE_API int fmoe_permute_gate_grad(const int32_t* d_slot_pos, int64_t num_slots,
+                           const void* d_grad_sorted, int dtype, void* d_grad_gates, void* stream);
 
 #ifdef __cplusplus
 }

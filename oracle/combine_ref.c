@@ -14,6 +14,10 @@
  *              grad_w[g] = sum_d grad_out[idx[g], d] * X[g, d], accumulated here in double.
  *   metadata : ops.py:233-256,268 -- offsets = exclusive cumsum of the row counts, max_rows.
  *   plan     : the token-major inverse of idx (CSR, ascending g per token, invalid rows last).
+ *   permute  : src/fastmoe/models/tiny_model.py:108-138 -- slots i = t*k + j sorted by expert id
+ *              (stable: a counting sort in ascending slot order, as torch.argsort(stable=True)),
+ *              the reverse map rev[pos] = i / k (:121-125), counts = bincount (:138); ids outside
+ *              [0, E) form one extra bucket after every expert.
  *
  * Element codes follow include/fastmoe_amd.h: 0 = f32, 1 = bf16, 2 = f16.  Out-of-range indices
  * are skipped and counted (the product drops them the same way).
@@ -183,4 +187,39 @@ void oracle_plan(const int64_t* idx, int64_t N, int64_t T, int32_t* row_ptr, int
     g_list[cnt[b]++] = (int32_t)g;
   }
   free(cnt);
+}
+
+/* ---- dispatch permutation (tiny_model.py:108-138) ------------------------------------------
+ * ids[T * k] -> counts[E], offsets[E + 1] (offsets[E] = valid slots), rev[N] (token of each packed
+ * row), slot_pos[N] (packed row of each slot).  Returns the number of slots whose id lies outside
+ * [0, E). */
+int64_t oracle_permute(const int64_t* ids, int64_t T, int64_t k, int64_t E, int64_t* counts,
+                       int64_t* offsets, int64_t* rev, int32_t* slot_pos) {
+  const int64_t N = T * k;
+  int64_t* cur = (int64_t*)calloc((size_t)(E + 1), sizeof(int64_t));
+  for (int64_t i = 0; i < N; ++i) {
+    const int64_t e = ids[i];
+    cur[(e >= 0 && e < E) ? e : E] += 1;
+  }
+  int64_t run = 0;
+  for (int64_t e = 0; e <= E; ++e) {
+    const int64_t c = cur[e];
+    if (e < E) {
+      counts[e] = c;
+      offsets[e] = run;
+    } else {
+      offsets[E] = run;
+    }
+    cur[e] = run;
+    run += c;
+  }
+  const int64_t bad = N - offsets[E];
+  for (int64_t i = 0; i < N; ++i) { /* ascending slot order: a stable sort */
+    const int64_t e = ids[i];
+    const int64_t pos = cur[(e >= 0 && e < E) ? e : E]++;
+    rev[pos] = i / k;
+    slot_pos[i] = (int32_t)pos;
+  }
+  free(cur);
+  return bad;
 }

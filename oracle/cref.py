@@ -39,6 +39,8 @@ def lib():
         l.oracle_round_f32.argtypes = [_p, _i64, ctypes.c_int, _p]
         l.oracle_widen_f32.restype = None
         l.oracle_widen_f32.argtypes = [_p, _i64, ctypes.c_int, _p]
+        l.oracle_permute.restype = _i64
+        l.oracle_permute.argtypes = [_p, _i64, _i64, _i64, _p, _p, _p, _p]
         _LIB = l
     return _LIB
 
@@ -122,3 +124,18 @@ def widen(a: np.ndarray, code: int) -> np.ndarray:
     out = np.empty(a.shape, dtype=np.float32)
     lib().oracle_widen_f32(_ptr(a), a.size, code, _ptr(out))
     return out
+
+
+def permute(ids: np.ndarray, E: int):
+    """Dispatch permutation of ids[T, k] (tiny_model.py:108-138, stable):
+    (counts int64[E], offsets int64[E + 1], rev int64[N], slot_pos int32[N], invalid_slots)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int64)
+    T, k = ids.shape
+    N = T * k
+    counts = np.zeros(E, dtype=np.int64)
+    offsets = np.zeros(E + 1, dtype=np.int64)
+    rev = np.zeros(N, dtype=np.int64)
+    slot_pos = np.zeros(N, dtype=np.int32)
+    bad = lib().oracle_permute(_ptr(ids), T, k, E, _ptr(counts), _ptr(offsets), _ptr(rev),
+                               _ptr(slot_pos))
+    return counts, offsets, rev, slot_pos, int(bad)

@@ -1,0 +1,183 @@
+"""GPU parity of the dispatch permutation and the MoE layer stages (fastmoe_amd.dispatch, .moe).
+
+Bars:
+  * permute_tokens: counts, offsets, reverse map and slot -> row map equal the C oracle's stable
+    counting sort exactly; sorted gates and permuted rows are bit copies.
+  * its backward: grad of x_flat equals the oracle combine of the packed gradient rows with unit
+    gates (ascending row order, fp32, rounded once) bit for bit; grad of the gates is the inverse
+    permutation, bit for bit.
+  * gate_and_sort / unpermute / MoEFeedForward: the reference's torch formulation of the same
+    layer (tiny_model.py:79-164, :282-294, :396-409, with a stable argsort) on the same weights,
+    fp32: permutation outputs bit-equal, layer output and every gradient within fp32 reordering
+    bounds.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import fastmoe_amd
+from fastmoe_amd.consts import MoEImplementation
+from oracle import cref
+from tests.helpers import bits, oracle_fwd, to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _routing(T, E, k, seed, zipf=False):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(T, E, generator=g)
+    if zipf:
+        bias = np.minimum(np.random.default_rng(seed).zipf(1.2, E), 10).astype(np.float32)
+        logits = logits + torch.from_numpy(bias)[None, :]
+    w, ids = torch.topk(logits, k, dim=-1)
+    return ids, torch.softmax(w, -1, dtype=torch.float32)
+
+
+def _check_permute(x, ids, w, E):
+    T, k = ids.shape
+    p = fastmoe_amd.permute_tokens(x.to(DEV), ids.to(DEV), w.to(DEV), E)
+    torch.cuda.synchronize()
+    counts, offsets, rev, slot_pos, bad = cref.permute(ids.numpy(), E)
+    np.testing.assert_array_equal(p.expert_counts.cpu().numpy(), counts)
+    np.testing.assert_array_equal(p.expert_offsets.cpu().numpy(), offsets)
+    np.testing.assert_array_equal(p.reverse_map_indices.cpu().numpy(), rev)
+    np.testing.assert_array_equal(p.slot_pos.cpu().numpy(), slot_pos)
+    want_w = np.empty(T * k, dtype=to_np(w).dtype)
+    want_w[slot_pos] = to_np(w).reshape(-1)
+    np.testing.assert_array_equal(to_np(p.sorted_weights), want_w)
+    want_x = to_np(x)[rev]
+    np.testing.assert_array_equal(to_np(p.permuted_data), want_x)
+    return p, bad
+
+
+@pytest.mark.parametrize("T,D,E,k,dtype", [
+    (256, 512, 8, 2, torch.float32),       # plumbing shape
+    (512, 4096, 64, 6, torch.bfloat16),    # mid shape, scaled
+    (256, 16384, 256, 8, torch.bfloat16),  # gigachat shape, scaled
+    (300, 100, 16, 4, torch.float16),      # 200-byte rows: 4-byte copies
+    (65, 7, 3, 3, torch.bfloat16),         # 14-byte rows: 2-byte copies
+    (40, 64, 1, 1, torch.float32),         # one expert, k = 1
+])
+def test_permute_matches_oracle(T, D, E, k, dtype):
+    ids, w = _routing(T, E, k, seed=T + D)
+    x = torch.randn(T, D, generator=torch.Generator().manual_seed(1)).to(dtype)
+    _check_permute(x, ids, w.to(dtype) if dtype != torch.float32 else w, E)
+
+
+def test_permute_skewed_int32_ids_and_empty_experts():
+    ids, w = _routing(2048, 256, 8, seed=3, zipf=True)
+    x = torch.randn(2048, 256).to(torch.bfloat16)
+    p, _ = _check_permute(x, ids.to(torch.int32), w, 256)
+    assert (p.expert_counts == 0).any()
+
+
+def test_permute_many_experts_uses_large_variant():
+    ids, w = _routing(300, 3000, 4, seed=4)
+    _check_permute(torch.randn(300, 32), ids, w, 3000)
+
+
+def test_permute_invalid_ids_go_last_and_validate_raises():
+    ids, w = _routing(100, 8, 2, seed=5)
+    ids[3, 0] = 8
+    ids[50, 1] = -1
+    x = torch.randn(100, 32)
+    _, bad = _check_permute(x, ids, w, 8)
+    assert bad == 2
+    with pytest.raises(IndexError):
+        fastmoe_amd.permute_tokens(x.to(DEV), ids.to(DEV), w.to(DEV), 8, validate=True)
+
+
+def test_permute_strided_rows():
+    ids, w = _routing(64, 8, 2, seed=6)
+    base = torch.randn(64, 96)
+    x = base[:, 16:80]  # row stride 96, unit column stride
+    p = fastmoe_amd.permute_tokens(base.to(DEV)[:, 16:80], ids.to(DEV), w.to(DEV), 8)
+    _, _, rev, _, _ = cref.permute(ids.numpy(), 8)
+    np.testing.assert_array_equal(p.permuted_data.cpu().numpy(), x.numpy()[rev])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_permute_backward(dtype):
+    T, D, E, k = 128, 320, 16, 4
+    ids, w = _routing(T, E, k, seed=7)
+    x = torch.randn(T, D).to(dtype)
+    wd = w.to(dtype).to(DEV).requires_grad_(True)
+    xd = x.to(DEV).requires_grad_(True)
+    p = fastmoe_amd.permute_tokens(xd, ids.to(DEV), wd, E)
+    g_rows = torch.randn(T * k, D, generator=torch.Generator().manual_seed(8)).to(dtype)
+    g_sw = torch.randn(T * k, generator=torch.Generator().manual_seed(9)).to(dtype)
+    gx, gw = torch.autograd.grad([p.permuted_data, p.sorted_weights], [xd, wd],
+                                 [g_rows.to(DEV), g_sw.to(DEV)])
+    _, _, rev, slot_pos, _ = cref.permute(ids.numpy(), E)
+    want, _, _ = oracle_fwd([g_rows], torch.from_numpy(rev), torch.ones(T * k), T, dtype)
+    np.testing.assert_array_equal(bits(gx), want.view(np.uint32) if dtype == torch.float32 else want)
+    np.testing.assert_array_equal(to_np(gw).reshape(-1), to_np(g_sw)[slot_pos])
+
+
+# ---- the layer: FAST (HIP permutation + grouped combine over the per-expert list) vs the
+# reference's torch formulation on the same weights ------------------------------------------
+def _reference_layer(layer, x):
+    """tiny_model.py:79-164 (stable argsort), :282-294 and :396-409 (STANDARD), world size 1."""
+    B, T, D = x.shape
+    x_flat = x.view(-1, D)
+    logits = layer.router(x_flat)
+    tw, ti = torch.topk(logits, layer.top_k, dim=-1)
+    tw = F.softmax(tw, dim=-1, dtype=torch.float32).type_as(x)
+    flat = ti.view(-1)
+    order = torch.argsort(flat, stable=True)
+    rev = torch.arange(x_flat.shape[0], device=x.device).repeat_interleave(layer.top_k)[order]
+    sw = tw.view(-1)[order]
+    permuted = x_flat[rev]
+    counts = torch.bincount(flat[order], minlength=layer.num_experts).tolist()
+    outs = [e(c) if c.shape[0] else c for e, c in zip(layer.experts, permuted.split(counts))]
+    x_out = torch.cat(outs, 0) * sw.unsqueeze(-1)
+    out = torch.zeros(B * T, D, device=x.device, dtype=x_out.dtype).index_add_(0, rev, x_out)
+    return out.view(B, T, D), permuted, rev, sw
+
+
+def test_gate_and_sort_matches_reference_formulation():
+    torch.manual_seed(0)
+    layer = fastmoe_amd.MoEFeedForward(64, 128, 8, 2).to(DEV)
+    x = torch.randn(2, 48, 64, device=DEV)
+    permuted, rank_counts, counts_by_rank, rev, sw, shape = fastmoe_amd.gate_and_sort(
+        x, layer.router, 2, 8)
+    _, want_perm, want_rev, want_sw = _reference_layer(layer, x)
+    assert shape == (2, 48) and rank_counts.tolist() == [192] and counts_by_rank.shape == (1, 8)
+    assert torch.equal(rev, want_rev) and torch.equal(sw, want_sw)
+    assert torch.equal(permuted, want_perm)
+
+
+@pytest.mark.parametrize("impl", [MoEImplementation.FAST, MoEImplementation.STANDARD])
+def test_moe_layer_forward_backward(impl):
+    torch.manual_seed(1)
+    layer = fastmoe_amd.MoEFeedForward(64, 96, 8, 2, implementation=impl).to(DEV)
+    x = torch.randn(2, 40, 64, device=DEV, requires_grad=True)
+    y = layer(x)
+    go = torch.randn_like(y)
+    params = [x, layer.router.weight, *[p for e in layer.experts for p in e.parameters()]]
+    grads = torch.autograd.grad(y, params, go, allow_unused=True)
+    x2 = x.detach().clone().requires_grad_(True)
+    want, _, _, _ = _reference_layer(layer, x2)
+    want_grads = torch.autograd.grad(want, [x2, *params[1:]], go, allow_unused=True)
+    torch.testing.assert_close(y, want, rtol=1e-5, atol=1e-5)
+    for g, wg in zip(grads, want_grads):
+        if g is None or wg is None:  # an expert that received no rows
+            assert g is None and wg is None
+            continue
+        torch.testing.assert_close(g, wg, rtol=1e-4, atol=1e-5)
+
+
+def test_unpermute_list_equals_packed():
+    """The per-expert list and its concatenation give the same combine bits (no cat needed)."""
+    g = torch.Generator().manual_seed(2)
+    sizes = [5, 0, 9, 2]
+    xs = [torch.randn(n, 40, generator=g).to(DEV) for n in sizes]
+    rev = torch.randint(0, 8, (16,), generator=g).to(DEV)
+    sw = torch.rand(16, generator=g).to(DEV)
+    a = fastmoe_amd.unpermute(xs, rev, sw, (2, 4))
+    b = fastmoe_amd.unpermute(torch.cat(xs), rev, sw, (2, 4))
+    assert torch.equal(a, b) and a.shape == (2, 4, 40)
