@@ -109,30 +109,16 @@ def _cpu_baseline(wl, sample_tokens: int, reps: int):
     }
 
 
-def _standard_gpu(wl, xs, idx, w, grad_out, backward, steps, warmup, fast_ms):
-    """The reference's STANDARD combine in torch GPU ops on the same inputs and GPU: cat -> * w ->
-    index_add_ into fp32 zeros (run_on_cloud.py:43-48, the reference's own comparison column), and
-    with backward its autograd (index_select, mul, split, gate dot).  Eager, event-timed like the
-    reference's benchmark_standard (run_on_cloud.py:35-53); peak memory above the inputs."""
+def _time_standard(std_step, steps, warmup, fast_ms, what):
+    """Eager event timing of a torch formulation of the same step (the reference's own comparison
+    column, run_on_cloud.py:35-53) and its peak memory above the inputs."""
     import torch
-
-    dev = idx.device
-    inputs = [w, *xs]
-
-    def std_step():
-        combined = torch.cat(xs, dim=0)
-        weighted = combined * w.unsqueeze(-1)
-        out = torch.zeros((wl.T, wl.D), device=dev)
-        out.index_add_(0, idx, weighted)
-        if backward:
-            torch.autograd.grad(out, inputs, grad_out.float())
-        return out
 
     for _ in range(max(1, warmup)):
         std_step()
     torch.cuda.synchronize()
-    torch.cuda.reset_peak_memory_stats(dev)
-    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -143,11 +129,54 @@ def _standard_gpu(wl, xs, idx, w, grad_out, backward, steps, warmup, fast_ms):
     ms = start.elapsed_time(stop) / steps
     return {
         "ms_per_step": round(ms, 4),
-        "peak_mem_gb": round((torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30, 3),
+        "peak_mem_gb": round((torch.cuda.max_memory_allocated() - base) / 2 ** 30, 3),
         "speedup_of_fast": round(ms / fast_ms, 2),
-        "what": "torch GPU cat -> * w -> index_add_ into fp32 zeros"
-                + (" + autograd backward" if backward else "") + ", eager",
+        "what": what,
     }
+
+
+def _standard_combine_step(wl, xs, idx, w, grad_out, backward):
+    """The reference's STANDARD combine in torch GPU ops on the same inputs: cat -> * w ->
+    index_add_ into fp32 zeros (run_on_cloud.py:43-48) and, with backward, its autograd
+    (index_select, mul, split, gate dot)."""
+    import torch
+
+    inputs = [w, *xs]
+
+    def std_step():
+        combined = torch.cat(xs, dim=0)
+        weighted = combined * w.unsqueeze(-1)
+        out = torch.zeros((wl.T, wl.D), device=idx.device)
+        out.index_add_(0, idx, weighted)
+        if backward:
+            torch.autograd.grad(out, inputs, grad_out.float())
+        return out
+
+    what = ("torch GPU cat -> * w -> index_add_ into fp32 zeros"
+            + (" + autograd backward" if backward else "") + ", eager")
+    return std_step, what
+
+
+def _standard_dispatch_step(wl, x, ids, gates, g_rows, g_sw, backward):
+    """The reference's gate_and_sort permutation in torch GPU ops (tiny_model.py:108-138):
+    argsort, reverse map, gate permutation, x_flat[rev] gather, bincount; with backward its
+    autograd (index_put_ accumulate into x, gate scatter)."""
+    import torch
+
+    def std_step():
+        flat = ids.view(-1)
+        order = torch.argsort(flat)
+        rev = torch.arange(wl.T, device=x.device).repeat_interleave(wl.k)[order]
+        sw = gates.view(-1)[order]
+        permuted = x[rev]
+        torch.bincount(flat[order], minlength=wl.E)
+        if backward:
+            torch.autograd.grad([permuted, sw], [x, gates], [g_rows, g_sw])
+        return permuted
+
+    what = ("torch GPU argsort -> reverse map -> x[rev] gather -> bincount"
+            + (" + autograd backward" if backward else "") + ", eager")
+    return std_step, what
 
 
 def _cpu_model() -> str:
@@ -167,6 +196,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gigachat")
     ap.add_argument("--mode", default="det", choices=["det", "atomic"])
+    ap.add_argument("--path", default="combine", choices=["combine", "dispatch"],
+                    help="combine: the grouped combine (the headline); dispatch: the permutation "
+                         "that feeds it (gate_and_sort's sort + gather) and its backward")
+    ap.add_argument("--inplace", action="store_true",
+                    help="the reference's kernel benchmark (run_on_cloud.py:56-96): fp32 out, "
+                         "metadata prepared once, each step out.zero_() + the in-place call "
+                         "(forward only)")
     ap.add_argument("--fwd-only", action="store_true",
                     help="time the forward alone (the default for forward-only workloads)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -192,8 +228,8 @@ def main() -> int:
 
     import fastmoe_amd
     from fastmoe_amd import ops
-    from fastmoe_amd.workloads import (WORKLOADS, algorithmic_bytes, kernel_bytes, make_experts,
-                                       make_routing)
+    from fastmoe_amd.workloads import (WORKLOADS, algorithmic_bytes, dispatch_bytes,
+                                       kernel_bytes, make_experts, make_routing, make_topk)
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -201,25 +237,64 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     wl = WORKLOADS[args.workload]
-    idx, w, counts = make_routing(wl)
-    idx, w = idx.to(dev), w.to(dev)
-    xs = make_experts(counts, wl.D, wl.dtype, dev, wl.seed)
-    backward = wl.backward and not args.fwd_only
-    if backward:
-        xs = [x.requires_grad_(True) for x in xs]
-        w.requires_grad_(True)
-    grad_out = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
-                           generator=torch.Generator(device=dev).manual_seed(1)).to(wl.dtype)
-    xb = xs[0].element_size()
-    fwd_b, bwd_b = algorithmic_bytes(wl.T, wl.D, wl.N, xb, xb)
-    step_bytes = fwd_b + (bwd_b if backward else 0)
-    inputs = [w, *xs]
-
-    def step():
-        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (wl.T, wl.D), mode=args.mode)
+    backward = wl.backward and not args.fwd_only and not args.inplace
+    gen_dev = torch.Generator(device=dev)
+    xb = torch.empty(0, dtype=wl.dtype).element_size()
+    if args.path == "combine":
+        metric = METRIC
+        idx, w, counts = make_routing(wl)
+        idx, w = idx.to(dev), w.to(dev)
+        xs = make_experts(counts, wl.D, wl.dtype, dev, wl.seed)
         if backward:
-            torch.autograd.grad(out, inputs, grad_out)
-        return out
+            xs = [x.requires_grad_(True) for x in xs]
+            w.requires_grad_(True)
+        grad_out = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
+                               generator=gen_dev.manual_seed(1)).to(wl.dtype)
+        fwd_b, bwd_b = algorithmic_bytes(wl.T, wl.D, wl.N, xb, 4 if args.inplace else xb)
+        inputs = [w, *xs]
+
+        if args.inplace:
+            out_static = torch.zeros((wl.T, wl.D), device=dev)
+            meta = fastmoe_amd.prepare_grouped_metadata(xs, dev)
+
+            def step():
+                out_static.zero_()
+                return fastmoe_amd.grouped_weighted_scatter_add(
+                    xs, idx, w, (wl.T, wl.D), out=out_static, metadata=meta, mode=args.mode)
+        else:
+            def step():
+                out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (wl.T, wl.D),
+                                                                mode=args.mode)
+                if backward:
+                    torch.autograd.grad(out, inputs, grad_out)
+                return out
+
+        std = lambda: _standard_combine_step(wl, xs, idx, w, grad_out, backward)  # noqa: E731
+    else:
+        metric = ("dispatch permutation fwd+bwd GB/s & % HBM peak (gate_and_sort sort + gather, "
+                  "its backward)")
+        ids, gates = make_topk(wl)
+        ids, gates = ids.to(dev), gates.to(dev)
+        x = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
+                        generator=gen_dev.manual_seed(3)).to(wl.dtype)
+        g_rows = torch.randn(wl.N, wl.D, device=dev, dtype=torch.float32,
+                             generator=gen_dev.manual_seed(4)).to(wl.dtype)
+        g_sw = torch.randn(wl.N, device=dev, generator=gen_dev.manual_seed(5))
+        if backward:
+            x.requires_grad_(True)
+            gates.requires_grad_(True)
+        fwd_b, bwd_b = dispatch_bytes(wl.T, wl.D, wl.N, xb)
+
+        def step():
+            p = fastmoe_amd.permute_tokens(x, ids, gates, wl.E)
+            if backward:
+                torch.autograd.grad([p.permuted_data, p.sorted_weights], [x, gates],
+                                    [g_rows, g_sw])
+            return p.permuted_data
+
+        std = lambda: _standard_dispatch_step(wl, x, ids, gates, g_rows, g_sw,  # noqa: E731
+                                              backward)
+    step_bytes = fwd_b + (bwd_b if backward else 0)
 
     if args.copy_probe:
         a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -307,7 +382,7 @@ def main() -> int:
     wall = wall_ms * args.steps / 1e3
 
     # Dominant kernel: the single-kernel span with the longest average launch.
-    kbytes = kernel_bytes(wl.T, wl.D, wl.N, xb, xb)
+    kbytes = kernel_bytes(wl.T, wl.D, wl.N, xb, 4 if args.inplace else xb)
     for name, k in kernels.items():
         if name in kbytes:
             k["algorithmic_bytes"] = kbytes[name]
@@ -324,7 +399,7 @@ def main() -> int:
 
     value = step_bytes / (ms * 1e-3) / 1e9
     res = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -338,8 +413,9 @@ def main() -> int:
         "data": "synthetic (seeded top-k routing of N(0,1) logits; N(0,1) expert outputs, one "
                 "allocation per expert; fp32 softmax gates; N(0,1) grad_out)",
         "config": {
-            "workload": wl.name, "tokens": wl.T, "hidden": wl.D, "experts": wl.E, "top_k": wl.k,
-            "rows": wl.N, "mode": args.mode, "backward": backward,
+            "workload": wl.name, "path": args.path, "tokens": wl.T, "hidden": wl.D,
+            "experts": wl.E, "top_k": wl.k, "rows": wl.N, "mode": args.mode, "backward": backward,
+            "inplace": args.inplace,
             "fwd_bytes": fwd_b, "bwd_bytes": bwd_b if backward else 0,
         },
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
@@ -369,10 +445,10 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_standard:
-        res["standard"] = _standard_gpu(wl, xs, idx, w, grad_out, backward, args.steps,
-                                         args.warmup, ms)
+        std_step, what = std()
+        res["standard"] = _time_standard(std_step, args.steps, args.warmup, ms, what)
         res["peak_mem_gb"] = round(fast_peak / 2 ** 30, 3)
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.path == "combine":
         res["cpu_baseline"] = _cpu_baseline(wl, args.cpu_sample_tokens or wl.T, args.cpu_reps)
     print(json.dumps(res), flush=True)
     return 0

@@ -274,6 +274,8 @@ __device__ __forceinline__ typename Vec<TX, V>::raw_t load_x(rsrc_t r, uint32_t 
 #pragma unroll
     for (int v = 0; v < V; ++v) raw[v] = Raw<4>::ld(r, off + 4 * v);
     return raw;
+  } else if constexpr (V == 2) {  // one 32-bit word of two 16-bit elements
+    return (uint32_t)Raw<2>::ld(r, off) | ((uint32_t)Raw<2>::ld(r, off + 2) << 16);
   } else {
     typename VX::raw_t raw;
 #pragma unroll

@@ -13,8 +13,8 @@
 //              block's slots of the same expert (wave ballots on the key bits give the lanes of
 //              a wave with an equal key; per-wave counts in LDS give the waves before it), and
 //              the block's count of every expert (row b of blkcnt[nb][E + 1]).
-//   2. scan    one 1024-thread workgroup: per expert, exclusive prefix over the blocks (in place),
-//              then the exclusive prefix over experts of the totals -> offsets.
+//   2. scan    one 1024-thread workgroup: per expert, exclusive prefix over the blocks (in place,
+//              through LDS tiles), then the exclusive prefix over experts of the totals -> offsets.
 //   3. fill    one thread per slot: pos = off[e] + blkcnt[b][e] + rank; writes the reverse map,
 //              the gate in packed order and the slot -> row map (slot_pos).
 //   4. gather  one workgroup per token: its waves copy x[t] into the token's k packed rows (the row
@@ -99,40 +99,64 @@ __global__ __launch_bounds__(kPermBlock) void k_perm_rank(const TI* __restrict__
 }
 
 // Per expert, exclusive prefix of blkcnt down the nb blocks (in place); then offsets over experts.
-// P = max(1, 1024 / (E + 1)) consecutive threads share one expert, each owning a contiguous range
-// of blocks, so the block loads of a thread are independent and stay in flight together.
+// The table is walked in tiles of whole block rows staged in LDS: a coalesced load of the tile,
+// one thread per expert column scanning it in LDS (consecutive threads, consecutive words: no
+// bank conflicts) with a carry kept in registers across tiles, and a coalesced store back.
+constexpr int kPermTileInts = 32768;                      // 128 KiB of LDS per tile
+constexpr int kPermKeysPerThread = (kPermMaxExperts + 1 + kPermScanThreads - 1) / kPermScanThreads;
+
 __global__ __launch_bounds__(kPermScanThreads) void k_perm_scan(
-    int32_t* __restrict__ blkcnt, int64_t nb, int64_t E, int P, int32_t* __restrict__ off,
+    int32_t* __restrict__ blkcnt, int64_t nb, int64_t E, int32_t* __restrict__ off,
     int64_t* __restrict__ counts, int64_t* __restrict__ offsets, int32_t* __restrict__ status) {
-  __shared__ int32_t part[kPermScanThreads];
+  __shared__ int32_t tile[kPermTileInts];
   __shared__ int32_t tot[kPermMaxExperts + 1];
   const int E1 = (int)E + 1;
-  const int keys_per_pass = kPermScanThreads / P;
-  const int p = threadIdx.x % P;
-  const int64_t per = (nb + P - 1) / P;
-  const int64_t blo = std::min<int64_t>(nb, p * per);
-  const int64_t bhi = std::min<int64_t>(nb, blo + per);
-  for (int kb = 0; kb < E1; kb += keys_per_pass) {
-    const int k = kb + (int)threadIdx.x / P;
-    const bool live = (int)threadIdx.x < keys_per_pass * P && k < E1;
-    int s = 0;
-    if (live)
-      for (int64_t b = blo; b < bhi; ++b) s += blkcnt[b * E1 + k];
-    part[threadIdx.x] = s;
-    __syncthreads();
-    if (live) {
-      int run = 0;
-      const int first = (int)threadIdx.x - p;
-      for (int q = 0; q < p; ++q) run += part[first + q];
-      if (p == P - 1) tot[k] = run + s;
-      for (int64_t b = blo; b < bhi; ++b) {
-        const int v = blkcnt[b * E1 + k];
-        blkcnt[b * E1 + k] = run;
-        run += v;
+  const int rows_per_tile = kPermTileInts / E1;  // >= 7 for E1 <= 4097
+  int carry[kPermKeysPerThread];
+#pragma unroll
+  for (int m = 0; m < kPermKeysPerThread; ++m) carry[m] = 0;
+  for (int64_t r0 = 0; r0 < nb; r0 += rows_per_tile) {
+    const int rows = (int)std::min<int64_t>(rows_per_tile, nb - r0);
+    const int n = rows * E1;
+    int32_t* g = blkcnt + r0 * E1;
+    constexpr int kBatch = 8;  // independent global loads in flight per thread
+    for (int base = 0; base < n; base += kPermScanThreads * kBatch) {
+      int v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int i = base + j * kPermScanThreads + (int)threadIdx.x;
+        v[j] = i < n ? g[i] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int i = base + j * kPermScanThreads + (int)threadIdx.x;
+        if (i < n) tile[i] = v[j];
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int m = 0; m < kPermKeysPerThread; ++m) {
+      const int k = (int)threadIdx.x + m * kPermScanThreads;
+      if (k < E1) {
+        int run = carry[m];
+        for (int r = 0; r < rows; ++r) {
+          const int v = tile[r * E1 + k];
+          tile[r * E1 + k] = run;
+          run += v;
+        }
+        carry[m] = run;
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kPermScanThreads) g[i] = tile[i];
+    __syncthreads();
   }
+#pragma unroll
+  for (int m = 0; m < kPermKeysPerThread; ++m) {
+    const int k = (int)threadIdx.x + m * kPermScanThreads;
+    if (k < E1) tot[k] = carry[m];
+  }
+  __syncthreads();
   // exclusive prefix over the E + 1 keys (serial chunks of 1024 with a carried total)
   __shared__ int32_t carry_s;
   __shared__ int32_t wave_tot[kPermScanThreads / kWave];
@@ -297,8 +321,7 @@ extern "C" int fmoe_permute_build(const void* d_expert_ids, int id_dtype, const 
 #undef FMOE_PRANK
     if (int rc = fmoe_host::check_launch("fmoe_permute_build(rank)")) return rc;
   }
-  const int P = std::max<int>(1, kPermScanThreads / (int)(E + 1));
-  hipLaunchKernelGGL(k_perm_scan, dim3(1), dim3(kPermScanThreads), 0, s, blkcnt, nb, E, P, off,
+  hipLaunchKernelGGL(k_perm_scan, dim3(1), dim3(kPermScanThreads), 0, s, blkcnt, nb, E, off,
                      d_counts, d_offsets, d_status);
   if (int rc = fmoe_host::check_launch("fmoe_permute_build(scan)")) return rc;
   if (N == 0) return FMOE_OK;

@@ -13,8 +13,9 @@
 // Steps (all on the caller's stream, no host synchronisation):
 //   1. count + scan   one 1024-thread workgroup histograms idx into LDS (T + 1 <= kLdsTokens) and
 //                     scans it; larger T fall back to zero / global-atomic count / one-block scan.
-//   2. fill           one thread per row: claims a slot in its segment with an atomic cursor and
-//                     writes its record (arbitrary order inside the segment).
+//   2. fill           one thread per row: writes its record at row_ptr[t] + rank, where rank is
+//                     the row's slot in its segment, returned by the count's atomic increment
+//                     (arbitrary order inside the segment; no atomics in the fill).
 //   3. order          segments longer than 64 rows only (never for top-k routing; the kernel
 //                     exits at once otherwise): one wave per segment ranks its records by g and
 //                     writes them in order.
@@ -30,16 +31,17 @@ constexpr int kScanThreads = 1024;
 constexpr int kLdsTokens = 33792;  // 132 KiB of LDS histogram (gfx950: 160 KiB per workgroup)
 
 struct PlanLayout {
-  int64_t status, cursor, row_ptr, rec_tmp, rec, total;
+  int64_t status, count, row_ptr, rank, rec_tmp, rec, total;
 };
 
 __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   PlanLayout L;
   L.status = 0;
-  L.cursor = 256;
-  L.row_ptr = L.cursor + up((T + 1) * 4);
-  L.rec_tmp = L.row_ptr + up((T + 2) * 4);
+  L.count = 256;
+  L.row_ptr = L.count + up((T + 1) * 4);
+  L.rank = L.row_ptr + up((T + 2) * 4);
+  L.rec_tmp = L.rank + up(N * 4);
   L.rec = L.rec_tmp + up(N * 16);
   L.total = L.rec + up(N * 16);
   return L;
@@ -89,7 +91,7 @@ __device__ int block_max_1024(int v) {
 // N read 0 and are masked at the atomic) and stays in flight together.
 template <typename TI>
 __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
-    const TI* __restrict__ idx, int64_t N, int64_t T, int32_t* __restrict__ cursor,
+    const TI* __restrict__ idx, int64_t N, int64_t T, int32_t* __restrict__ rank,
     int32_t* __restrict__ row_ptr, int32_t* __restrict__ status) {
   __shared__ int hist[kLdsTokens];
   const int nb = (int)T + 1;
@@ -109,13 +111,16 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
     for (int i = 0; i < kBatch; ++i) {
       const int64_t g = base + (int64_t)i * kScanThreads + threadIdx.x;
       const int64_t t = (int64_t)v[i];
-      if (g < N) atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
+      if (g < N) rank[g] = atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
     }
   }
   __syncthreads();
+  // Scan: each thread owns `per` consecutive bins; the prefixes go back into LDS and are copied
+  // out with coalesced stores (consecutive threads, consecutive bins).
   const int per = (nb + kScanThreads - 1) / kScanThreads;
   const int b0 = min(nb, (int)threadIdx.x * per);
   const int b1 = min(nb, b0 + per);
+  const int invalid = hist[T];  // read before the scan's barrier; bin T is rewritten after it
   int local = 0, longest = 0;
   for (int b = b0; b < b1; ++b) {
     local += hist[b];
@@ -125,15 +130,16 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
   int run = block_exclusive_scan_1024(local, &total);
   for (int b = b0; b < b1; ++b) {
     const int c = hist[b];
-    row_ptr[b] = run;
-    cursor[b] = run;
+    hist[b] = run;
     run += c;
   }
-  // longest token segment (the out-of-range segment T is never ordered)
+  // longest token segment (the out-of-range segment T is never ordered); the reduction's barriers
+  // also publish the prefixes written above
   longest = block_max_1024(longest);
+  for (int b = threadIdx.x; b < nb; b += kScanThreads) row_ptr[b] = hist[b];
   if (threadIdx.x == 0) {
     row_ptr[nb] = total;
-    status[kStatusInvalid] = hist[T];
+    status[kStatusInvalid] = invalid;
     status[kStatusMisaligned] = 0;
     status[kStatusLongest] = longest;
   }
@@ -147,14 +153,15 @@ __global__ __launch_bounds__(kGroup) void k_plan_zero(int32_t* __restrict__ p, i
 
 __global__ __launch_bounds__(kGroup) void k_plan_count_global(const void* __restrict__ idx,
                                                               int idx_dtype, int64_t N, int64_t T,
-                                                              int32_t* __restrict__ cnt) {
+                                                              int32_t* __restrict__ cnt,
+                                                              int32_t* __restrict__ rank) {
   const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
   if (g >= N) return;
   const int64_t t = load_index(idx, idx_dtype, g);
-  atomicAdd(&cnt[(t >= 0 && t < T) ? t : T], 1);
+  rank[g] = atomicAdd(&cnt[(t >= 0 && t < T) ? t : T], 1);
 }
 
-// In-place: cnt[b] (counts) becomes the cursor (= row_ptr[b]).
+// Exclusive scan of the counts cnt[T + 1] into row_ptr.
 __global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __restrict__ cnt,
                                                                    int64_t T,
                                                                    int32_t* __restrict__ row_ptr,
@@ -182,10 +189,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __re
     int run = carry + block_exclusive_scan_1024(local, &total);
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      if (b0 + i < nb) {
-        row_ptr[b0 + i] = run;
-        cnt[b0 + i] = run;
-      }
+      if (b0 + i < nb) row_ptr[b0 + i] = run;
       run += v[i];
     }
     carry += total;
@@ -204,7 +208,7 @@ template <typename TI, typename TW>
 __global__ __launch_bounds__(kGroup) void k_plan_fill(
     const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T,
     const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
-    int64_t row_bytes, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ cursor,
+    int64_t row_bytes, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ rank,
     Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, int32_t* __restrict__ status) {
   __shared__ int64_t off_lds[kLdsExperts + 1];
   const bool lds_off = E <= kLdsExperts;
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(kGroup) void k_plan_fill(
   if (g < N) {
     const int64_t t = (int64_t)idx[g];
     const int64_t b = (t >= 0 && t < T) ? t : T;
-    const int pos = atomicAdd(&cursor[b], 1);
+    const int pos = row_ptr[b] + rank[g];
     const bool long_seg = b < T && row_ptr[b + 1] - row_ptr[b] > kWave;
     const int64_t e = expert_of_row(lds_off ? off_lds : offsets, E, g);
     Rec r;
@@ -230,7 +234,7 @@ __global__ __launch_bounds__(kGroup) void k_plan_fill(
 // Launched after the fill; exits at once unless some segment is longer than one wave (never for
 // top-k routing: the scan recorded the longest segment).  Otherwise each wave takes token
 // segments in turn (a small grid strides over them, so the early exit costs little dispatch).
-constexpr int kSortGroups = 256;
+constexpr int kSortGroups = 64;
 
 __global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __restrict__ row_ptr,
                                                            int64_t T,
@@ -294,7 +298,8 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   const PlanLayout L = plan_layout(N, T);
   char* ws = static_cast<char*>(d_workspace);
   int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
-  int32_t* cursor = reinterpret_cast<int32_t*>(ws + L.cursor);
+  int32_t* count = reinterpret_cast<int32_t*>(ws + L.count);  // global-path counts
+  int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
   Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
@@ -303,21 +308,21 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   if (nb <= kLdsTokens && N < (int64_t(1) << 27)) {
     if (idx_dtype == FMOE_I64)
       hipLaunchKernelGGL(k_plan_count_scan_lds<int64_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int64_t*>(d_indices), N, T, cursor, row_ptr, status);
+                         static_cast<const int64_t*>(d_indices), N, T, rank, row_ptr, status);
     else
       hipLaunchKernelGGL(k_plan_count_scan_lds<int32_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int32_t*>(d_indices), N, T, cursor, row_ptr, status);
+                         static_cast<const int32_t*>(d_indices), N, T, rank, row_ptr, status);
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(count_scan)")) return rc;
   } else {
     hipLaunchKernelGGL(k_plan_zero, dim3((unsigned)((nb + kGroup - 1) / kGroup)), dim3(kGroup), 0,
-                       s, cursor, nb);
+                       s, count, nb);
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(zero)")) return rc;
     if (N > 0) {
       hipLaunchKernelGGL(k_plan_count_global, dim3((unsigned)((N + kGroup - 1) / kGroup)),
-                         dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, cursor);
+                         dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, count, rank);
       if (int rc = fmoe_host::check_launch("fmoe_build_plan(count)")) return rc;
     }
-    hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, cursor, T, row_ptr,
+    hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, count, T, row_ptr,
                        status);
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(scan)")) return rc;
   }
@@ -326,7 +331,7 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
 #define FMOE_FILL(TI, TW)                                                                          \
   hipLaunchKernelGGL((k_plan_fill<TI, TW>), grid, dim3(kGroup), 0, s,                              \
                      static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
-                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, cursor, rec_tmp, rec, status)
+                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, rank, rec_tmp, rec, status)
   if (idx_dtype == FMOE_I64) {
     if (w_dtype == FMOE_F32) FMOE_FILL(int64_t, float);
     else if (w_dtype == FMOE_BF16) FMOE_FILL(int64_t, bf16_t);

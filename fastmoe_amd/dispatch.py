@@ -79,17 +79,20 @@ class _TokenPermute(torch.autograd.Function):
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         out = torch.empty((N, D), dtype=x_flat.dtype, device=dev)
         es = x_flat.element_size()
-        with torch.cuda.device(dev), _span("permute"):
-            rc = lib.fmoe_permute_build(
-                ids.data_ptr(), _INDEX_CODES[ids.dtype], gates.data_ptr(),
-                _FLOAT_CODES[gates.dtype], T, k, E, counts.data_ptr(), offsets.data_ptr(),
-                rev.data_ptr(), sorted_w.data_ptr(), slot_pos.data_ptr(), status.data_ptr(),
-                ws.data_ptr(), _stream_handle(dev))
+        with torch.cuda.device(dev):
+            with _span("permute_build"):
+                rc = lib.fmoe_permute_build(
+                    ids.data_ptr(), _INDEX_CODES[ids.dtype], gates.data_ptr(),
+                    _FLOAT_CODES[gates.dtype], T, k, E, counts.data_ptr(), offsets.data_ptr(),
+                    rev.data_ptr(), sorted_w.data_ptr(), slot_pos.data_ptr(), status.data_ptr(),
+                    ws.data_ptr(), _stream_handle(dev))
             _abi.check(rc, "fmoe_permute_build")
             if N and D:
-                rc = lib.fmoe_permute_gather(
-                    slot_pos.data_ptr(), T, k, D * es, x_flat.data_ptr(),
-                    (x_flat.stride(0) if T > 1 else D) * es, out.data_ptr(), _stream_handle(dev))
+                with _span("permute_gather"):
+                    rc = lib.fmoe_permute_gather(
+                        slot_pos.data_ptr(), T, k, D * es, x_flat.data_ptr(),
+                        (x_flat.stride(0) if T > 1 else D) * es, out.data_ptr(),
+                        _stream_handle(dev))
                 _abi.check(rc, "fmoe_permute_gather")
         if validate:
             bad = int(status[0])

@@ -74,6 +74,20 @@ def make_routing(wl: Workload, T: int | None = None) -> Tuple[torch.Tensor, torc
     return idx.contiguous(), w, counts
 
 
+def make_topk(wl: Workload, T: int | None = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The routing decision before the sort: (expert ids int64[T, k], fp32 gates [T, k]), seeded
+    like make_routing (same logits, so the same rows result)."""
+    if wl.routing == "randint":
+        raise ValueError("the randint workload has no top-k routing decision")
+    T = wl.T if T is None else T
+    gen = torch.Generator().manual_seed(wl.seed)
+    logits = torch.randn(T, wl.E, generator=gen)
+    if wl.routing == "zipf":
+        logits = logits + torch.from_numpy(zipf_bias(wl.E, wl.seed))[None, :]
+    top_w, top_i = torch.topk(logits, wl.k, dim=-1)
+    return top_i.contiguous(), torch.softmax(top_w, dim=-1, dtype=torch.float32).contiguous()
+
+
 def make_experts(counts: List[int], D: int, dtype: torch.dtype, device, seed: int) -> List[torch.Tensor]:
     """One ~N(0, 1) buffer per expert, each its own allocation (empty experts get [0, D])."""
     dev = torch.device(device)
@@ -103,6 +117,19 @@ def algorithmic_bytes(T: int, D: int, N: int, x_bytes: int, out_bytes: int, gate
     return fwd, bwd
 
 
+def dispatch_bytes(T: int, D: int, N: int, x_bytes: int, gate_bytes: int = 4) -> Tuple[int, int]:
+    """Compulsory HBM bytes (forward, backward) of one dispatch permutation.
+
+    forward : read x (T*D) + write the packed rows (N*D) + per slot: read id (8) and gate, write
+              sorted gate, reverse map (8) and slot -> row map (4)
+    backward: read the packed-row gradient (N*D) + write grad x (T*D) + per slot: read reverse map
+              (8) and unit gate (4), read gate grad, slot -> row map (4), write gate grad
+    """
+    fwd = T * D * x_bytes + N * D * x_bytes + N * (8 + 2 * gate_bytes + 8 + 4)
+    bwd = N * D * x_bytes + T * D * x_bytes + N * (8 + 4 + 2 * gate_bytes + 4)
+    return fwd, bwd
+
+
 def kernel_bytes(T: int, D: int, N: int, x_bytes: int, out_bytes: int,
                  gate_bytes: int = 4) -> dict:
     """Compulsory HBM bytes of one launch of each kernel of the step, by timing-span name.
@@ -111,9 +138,11 @@ def kernel_bytes(T: int, D: int, N: int, x_bytes: int, out_bytes: int,
     bwd_gx               : read grad_out (T*D) + write grad_X (N*D) + read idx and w per row
     bwd_gw               : read grad_out (T*D) + read X (N*D) + read idx, write grad_w per row
     bwd                  : both gradients in one pass (as ``algorithmic_bytes``)
+    permute_gather       : read x (T*D) + write the packed rows (N*D) + read slot_pos per slot
     """
     fwd, bwd = algorithmic_bytes(T, D, N, x_bytes, out_bytes, gate_bytes)
     return {
+        "permute_gather": T * D * x_bytes + N * D * x_bytes + N * 4,
         "fwd_det": fwd,
         "fwd_atomic": fwd,
         "bwd_gx": T * D * x_bytes + N * D * x_bytes + N * (8 + gate_bytes),
