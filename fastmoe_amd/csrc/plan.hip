@@ -13,9 +13,8 @@
 // Steps (all on the caller's stream, no host synchronisation):
 //   1. count + scan   one 1024-thread workgroup histograms idx into LDS (T + 1 <= kLdsTokens) and
 //                     scans it; larger T fall back to zero / global-atomic count / one-block scan.
-//   2. fill           one thread per row: writes its record at row_ptr[t] + rank, where rank is
-//                     the row's slot in its segment, returned by the count's atomic increment
-//                     (arbitrary order inside the segment; no atomics in the fill).
+//   2. fill           one thread per row: claims a slot in its segment with an atomic cursor and
+//                     writes its record (arbitrary order inside the segment).
 //   3. order          segments longer than 64 rows only (never for top-k routing; the kernel
 //                     exits at once otherwise): one wave per segment ranks its records by g and
 //                     writes them in order.
@@ -31,17 +30,16 @@ constexpr int kScanThreads = 1024;
 constexpr int kLdsTokens = 33792;  // 132 KiB of LDS histogram (gfx950: 160 KiB per workgroup)
 
 struct PlanLayout {
-  int64_t status, count, row_ptr, rank, rec_tmp, rec, total;
+  int64_t status, cursor, row_ptr, rec_tmp, rec, total;
 };
 
 __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   PlanLayout L;
   L.status = 0;
-  L.count = 256;
-  L.row_ptr = L.count + up((T + 1) * 4);
-  L.rank = L.row_ptr + up((T + 2) * 4);
-  L.rec_tmp = L.rank + up(N * 4);
+  L.cursor = 256;
+  L.row_ptr = L.cursor + up((T + 1) * 4);
+  L.rec_tmp = L.row_ptr + up((T + 2) * 4);
   L.rec = L.rec_tmp + up(N * 16);
   L.total = L.rec + up(N * 16);
   return L;
@@ -91,7 +89,7 @@ __device__ int block_max_1024(int v) {
 // N read 0 and are masked at the atomic) and stays in flight together.
 template <typename TI>
 __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
-    const TI* __restrict__ idx, int64_t N, int64_t T, int32_t* __restrict__ rank,
+    const TI* __restrict__ idx, int64_t N, int64_t T, int32_t* __restrict__ cursor,
     int32_t* __restrict__ row_ptr, int32_t* __restrict__ status) {
   __shared__ int hist[kLdsTokens];
   const int nb = (int)T + 1;
@@ -111,7 +109,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
     for (int i = 0; i < kBatch; ++i) {
       const int64_t g = base + (int64_t)i * kScanThreads + threadIdx.x;
       const int64_t t = (int64_t)v[i];
-      if (g < N) rank[g] = atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
+      if (g < N) atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
     }
   }
   __syncthreads();
@@ -136,7 +134,11 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
   // longest token segment (the out-of-range segment T is never ordered); the reduction's barriers
   // also publish the prefixes written above
   longest = block_max_1024(longest);
-  for (int b = threadIdx.x; b < nb; b += kScanThreads) row_ptr[b] = hist[b];
+  for (int b = threadIdx.x; b < nb; b += kScanThreads) {
+    const int v = hist[b];
+    row_ptr[b] = v;
+    cursor[b] = v;
+  }
   if (threadIdx.x == 0) {
     row_ptr[nb] = total;
     status[kStatusInvalid] = invalid;
@@ -153,15 +155,14 @@ __global__ __launch_bounds__(kGroup) void k_plan_zero(int32_t* __restrict__ p, i
 
 __global__ __launch_bounds__(kGroup) void k_plan_count_global(const void* __restrict__ idx,
                                                               int idx_dtype, int64_t N, int64_t T,
-                                                              int32_t* __restrict__ cnt,
-                                                              int32_t* __restrict__ rank) {
+                                                              int32_t* __restrict__ cnt) {
   const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
   if (g >= N) return;
   const int64_t t = load_index(idx, idx_dtype, g);
-  rank[g] = atomicAdd(&cnt[(t >= 0 && t < T) ? t : T], 1);
+  atomicAdd(&cnt[(t >= 0 && t < T) ? t : T], 1);
 }
 
-// Exclusive scan of the counts cnt[T + 1] into row_ptr.
+// In-place: cnt[b] (counts) becomes the cursor (= row_ptr[b]).
 __global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __restrict__ cnt,
                                                                    int64_t T,
                                                                    int32_t* __restrict__ row_ptr,
@@ -189,7 +190,10 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __re
     int run = carry + block_exclusive_scan_1024(local, &total);
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      if (b0 + i < nb) row_ptr[b0 + i] = run;
+      if (b0 + i < nb) {
+        row_ptr[b0 + i] = run;
+        cnt[b0 + i] = run;
+      }
       run += v[i];
     }
     carry += total;
@@ -208,7 +212,7 @@ template <typename TI, typename TW>
 __global__ __launch_bounds__(kGroup) void k_plan_fill(
     const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T,
     const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
-    int64_t row_bytes, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ rank,
+    int64_t row_bytes, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ cursor,
     Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, int32_t* __restrict__ status) {
   __shared__ int64_t off_lds[kLdsExperts + 1];
   const bool lds_off = E <= kLdsExperts;
@@ -219,7 +223,7 @@ __global__ __launch_bounds__(kGroup) void k_plan_fill(
   if (g < N) {
     const int64_t t = (int64_t)idx[g];
     const int64_t b = (t >= 0 && t < T) ? t : T;
-    const int pos = row_ptr[b] + rank[g];
+    const int pos = atomicAdd(&cursor[b], 1);
     const bool long_seg = b < T && row_ptr[b + 1] - row_ptr[b] > kWave;
     const int64_t e = expert_of_row(lds_off ? off_lds : offsets, E, g);
     Rec r;
@@ -298,8 +302,7 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   const PlanLayout L = plan_layout(N, T);
   char* ws = static_cast<char*>(d_workspace);
   int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
-  int32_t* count = reinterpret_cast<int32_t*>(ws + L.count);  // global-path counts
-  int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
+  int32_t* cursor = reinterpret_cast<int32_t*>(ws + L.cursor);
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
   Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
@@ -308,21 +311,21 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   if (nb <= kLdsTokens && N < (int64_t(1) << 27)) {
     if (idx_dtype == FMOE_I64)
       hipLaunchKernelGGL(k_plan_count_scan_lds<int64_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int64_t*>(d_indices), N, T, rank, row_ptr, status);
+                         static_cast<const int64_t*>(d_indices), N, T, cursor, row_ptr, status);
     else
       hipLaunchKernelGGL(k_plan_count_scan_lds<int32_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int32_t*>(d_indices), N, T, rank, row_ptr, status);
+                         static_cast<const int32_t*>(d_indices), N, T, cursor, row_ptr, status);
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(count_scan)")) return rc;
   } else {
     hipLaunchKernelGGL(k_plan_zero, dim3((unsigned)((nb + kGroup - 1) / kGroup)), dim3(kGroup), 0,
-                       s, count, nb);
+                       s, cursor, nb);
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(zero)")) return rc;
     if (N > 0) {
       hipLaunchKernelGGL(k_plan_count_global, dim3((unsigned)((N + kGroup - 1) / kGroup)),
-                         dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, count, rank);
+                         dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, cursor);
       if (int rc = fmoe_host::check_launch("fmoe_build_plan(count)")) return rc;
     }
-    hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, count, T, row_ptr,
+    hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, cursor, T, row_ptr,
                        status);
     if (int rc = fmoe_host::check_launch("fmoe_build_plan(scan)")) return rc;
   }
@@ -331,7 +334,7 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
 #define FMOE_FILL(TI, TW)                                                                          \
   hipLaunchKernelGGL((k_plan_fill<TI, TW>), grid, dim3(kGroup), 0, s,                              \
                      static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
-                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, rank, rec_tmp, rec, status)
+                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, cursor, rec_tmp, rec, status)
   if (idx_dtype == FMOE_I64) {
     if (w_dtype == FMOE_F32) FMOE_FILL(int64_t, float);
     else if (w_dtype == FMOE_BF16) FMOE_FILL(int64_t, bf16_t);
