@@ -140,6 +140,7 @@ class GroupedMetadata(tuple):
 
 
 def _check_experts(expert_tensors: Sequence[torch.Tensor]):
+    """Validate the expert buffers in one pass; returns (dtype, device, hidden, sizes, ptrs)."""
     if len(expert_tensors) == 0:
         raise ValueError("fastmoe_amd: expert_tensors is empty")
     ref = expert_tensors[0]
@@ -148,21 +149,28 @@ def _check_experts(expert_tensors: Sequence[torch.Tensor]):
         raise TypeError(f"fastmoe_amd: unsupported expert dtype {ref.dtype}")
     if ref.dim() != 2:
         raise ValueError(f"fastmoe_amd: expert tensors must be 2-D [rows, D], got {tuple(ref.shape)}")
-    hidden = ref.shape[1]
+    dtype, device, hidden = ref.dtype, ref.device, ref.shape[1]
+    dev_index = ref.get_device()
+    row_strides = (hidden, 1)
+    sizes, ptrs = [], []
     for i, t in enumerate(expert_tensors):
-        if t.device != ref.device or t.dtype != ref.dtype:
+        shape = t.shape
+        if t.dtype != dtype or t.get_device() != dev_index:
             raise ValueError(f"fastmoe_amd: expert_tensors[{i}] differs in device/dtype from [0]")
-        if t.dim() != 2 or t.shape[1] != hidden:
+        if len(shape) != 2 or shape[1] != hidden:
             raise ValueError(
-                f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(t.shape)}, expected [*, {hidden}]"
+                f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(shape)}, expected [*, {hidden}]"
             )
-        if t.shape[0] > 1 and (t.stride(1) != 1 or t.stride(0) != hidden):
+        n = shape[0]
+        if n > 1 and t.stride() != row_strides:
             raise ValueError(
                 f"fastmoe_amd: expert_tensors[{i}] must be row-contiguous (strides {t.stride()})"
             )
-        if t.shape[0] == 1 and hidden > 1 and t.stride(1) != 1:
+        if n == 1 and hidden > 1 and t.stride(1) != 1:
             raise ValueError(f"fastmoe_amd: expert_tensors[{i}] must have unit column stride")
-    return ref.dtype, ref.device, hidden
+        sizes.append(n)
+        ptrs.append(t.data_ptr() if n else 0)
+    return dtype, device, hidden, sizes, ptrs
 
 
 def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None) -> GroupedMetadata:
@@ -172,13 +180,11 @@ def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None
     the device by one kernel launch whose arguments carry the (address, rows) pairs
     (``fmoe_build_metadata``): no host staging buffer and no synchronous copy.
     """
-    dtype, dev, hidden = _check_experts(expert_tensors)
+    dtype, dev, hidden, sizes, ptrs = _check_experts(expert_tensors)
     if device is not None:
         _require_cuda(_DeviceProbe(device), "device")
     lib = _abi.lib()
     E = len(expert_tensors)
-    sizes = [int(t.shape[0]) for t in expert_tensors]
-    ptrs = [int(t.data_ptr()) if n > 0 else 0 for t, n in zip(expert_tensors, sizes)]
     ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
     chunk_sizes = torch.empty(E, dtype=torch.int32, device=dev)
     offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
