@@ -523,6 +523,48 @@ def test_full_size_fwd_bwd_parity(name):
     assert np.all(np.abs(grads[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
+@pytest.mark.parametrize("name", ["mid", "skewed"])
+def test_full_size_forward_parity(name):
+    """BASELINE configs 2 and 4 at their full sizes: the deterministic forward is bit-exact
+    against the C oracle (skewed: Zipf-biased routing with empty and hot experts)."""
+    wl = WORKLOADS[name]
+    idx, w, counts = make_routing(wl)
+    xd = make_experts(counts, wl.D, wl.dtype, DEV, wl.seed)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idx.to(DEV), w.to(DEV), (wl.T, wl.D))
+    torch.cuda.synchronize()
+    if name == "skewed":
+        assert 0 in counts and max(counts) > 1.5 * wl.N / wl.E  # empty and hot experts
+    experts = [x.cpu() for x in xd]
+    want, _, bad = oracle_fwd(experts, idx, w, wl.T, wl.dtype)
+    assert bad == 0
+    np.testing.assert_array_equal(bits(out), want)
+
+
+def test_full_size_det_repeatable_and_atomic_bounded():
+    """BASELINE config 5 at its full size (T=32768, D=16384, E=256, top-2, bf16): ten
+    deterministic runs are bit-identical; ten atomic runs each stay within the packed-bf16
+    rounding bound of the deterministic result: k roundings of the atomic adds plus the one
+    rounding of the deterministic result, each at most 2^-8 of sum|terms|."""
+    wl = WORKLOADS["detatomic"]
+    idx, w, counts = make_routing(wl)
+    xd = make_experts(counts, wl.D, wl.dtype, DEV, wl.seed)
+    idd, wd = idx.to(DEV), w.to(DEV)
+    shape = (wl.T, wl.D)
+    det = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, shape, mode="det")
+    det_bits = det.view(torch.int16).clone()
+    for _ in range(9):
+        again = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, shape, mode="det")
+        assert torch.equal(again.view(torch.int16), det_bits)
+    # sum|terms| per output element, torch fp32 ops on the GPU (a tolerance scale only)
+    scale = torch.zeros(shape, device=DEV)
+    scale.index_add_(0, idd, torch.cat(xd).float().abs() * wd.abs()[:, None])
+    tol = (wl.k + 1) * 2.0 ** -8 * scale + 2.0 ** -126
+    det32 = det.float()
+    for _ in range(10):
+        atom = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, shape, mode="atomic")
+        assert bool(((atom.float() - det32).abs() <= tol).all())
+
+
 def test_atomic_mode_refuses_16bit_output_without_vector_layout():
     D, T = 100, 8
     x = torch.randn(6, D).to(torch.bfloat16).to(DEV)
