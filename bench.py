@@ -179,6 +179,27 @@ def _standard_dispatch_step(wl, x, ids, gates, g_rows, g_sw, backward):
     return std_step, what
 
 
+def _standard_moe_step(wl, x, ids, gates):
+    """The reference's layer data movement in torch GPU ops, identity experts:
+    gate_and_sort's sort + gather (tiny_model.py:108-138) and unpermute's STANDARD combine
+    (:399-403, gates in the activation dtype as :100 casts them)."""
+    import torch
+
+    def std_step():
+        with torch.no_grad():
+            flat = ids.view(-1)
+            order = torch.argsort(flat)
+            rev = torch.arange(wl.T, device=x.device).repeat_interleave(wl.k)[order]
+            sw = gates.view(-1)[order].type_as(x)
+            permuted = x[rev]
+            torch.bincount(flat[order], minlength=wl.E).tolist()
+            x_out = permuted * sw.unsqueeze(-1)
+            out = torch.zeros(wl.T, wl.D, device=x.device, dtype=x_out.dtype)
+            return out.index_add_(0, rev, x_out)
+
+    return std_step, "torch GPU argsort -> x[rev] -> bincount -> * w -> index_add_, eager"
+
+
 def _cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -196,9 +217,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gigachat")
     ap.add_argument("--mode", default="det", choices=["det", "atomic"])
-    ap.add_argument("--path", default="combine", choices=["combine", "dispatch"],
+    ap.add_argument("--path", default="combine", choices=["combine", "dispatch", "moe"],
                     help="combine: the grouped combine (the headline); dispatch: the permutation "
-                         "that feeds it (gate_and_sort's sort + gather) and its backward")
+                         "that feeds it (gate_and_sort's sort + gather) and its backward; moe: "
+                         "the MoE layer's data movement, permutation then combine with identity "
+                         "experts (forward; the combine's plan comes from the permutation)")
     ap.add_argument("--inplace", action="store_true",
                     help="the reference's kernel benchmark (run_on_cloud.py:56-96): fp32 out, "
                          "metadata prepared once, each step out.zero_() + the in-place call "
@@ -213,6 +236,9 @@ def main() -> int:
     ap.add_argument("--cpu-sample-tokens", type=int, default=0,
                     help="tokens of the CPU baseline sample (0 = the whole workload)")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-slot-plan", action="store_true",
+                    help="moe path: build the combine's plan from the scatter index instead of "
+                         "the permutation's slot map")
     ap.add_argument("--no-standard", action="store_true",
                     help="skip the torch STANDARD combine timed on the same GPU")
     args = ap.parse_args()
@@ -270,6 +296,31 @@ def main() -> int:
                 return out
 
         std = lambda: _standard_combine_step(wl, xs, idx, w, grad_out, backward)  # noqa: E731
+    elif args.path == "moe":
+        metric = ("MoE layer data movement GB/s & % HBM peak (permutation + grouped combine, "
+                  "identity experts, forward)")
+        backward = False
+        ids, gates = make_topk(wl)
+        ids, gates = ids.to(dev), gates.to(dev)
+        x = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
+                        generator=gen_dev.manual_seed(3)).to(wl.dtype)
+        pf, _ = dispatch_bytes(wl.T, wl.D, wl.N, xb)
+        cf, _ = algorithmic_bytes(wl.T, wl.D, wl.N, xb, xb)
+        fwd_b, bwd_b = pf + cf, 0
+        use_slots = not args.no_slot_plan
+        # rows per expert on the host once (the routing is the same every step), so the step has
+        # no device->host synchronisation and can be captured in a graph
+        with torch.no_grad():
+            counts_host = fastmoe_amd.permute_tokens(x, ids, gates, wl.E).expert_counts.tolist()
+
+        def step():
+            with torch.no_grad():
+                p = fastmoe_amd.permute_tokens(x, ids, gates, wl.E)
+                parts = p.permuted_data.split(counts_host)
+                return fastmoe_amd.unpermute(parts, p.reverse_map_indices, p.sorted_weights,
+                                             (1, wl.T), permutation=p if use_slots else None)
+
+        std = lambda: _standard_moe_step(wl, x, ids, gates)  # noqa: E731
     else:
         metric = ("dispatch permutation fwd+bwd GB/s & % HBM peak (gate_and_sort sort + gather, "
                   "its backward)")

@@ -39,6 +39,10 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_vp, _c_int, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp],
     ),
+    "fmoe_build_plan_from_slots": (
+        _c_int,
+        [_c_vp, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
+    ),
     "fmoe_combine_fwd": (
         _c_int,
         [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,

@@ -317,11 +317,16 @@ struct LaneRecs {
   }
   __device__ __forceinline__ int32_t row(int i) const { return __builtin_amdgcn_readlane(g, i); }
   // Reorder the `count` records to ascending g: each lane ranks its key against all others
-  // (readlane broadcasts) and pushes its record to lane `rank` (ds_permute).  Keys are distinct.
+  // (readlane broadcasts) and pushes its record to lane `rank` (ds_permute).  Equal keys (never
+  // produced by a consistent plan) are ranked by lane, so the ranks always form a permutation and
+  // every destination lane receives exactly one record.
   __device__ __forceinline__ void sort_by_row(int count, int lane) {
     const int key = lane < count ? g : 0x7fffffff;
     int rank = 0;
-    for (int m = 0; m < count; ++m) rank += (__builtin_amdgcn_readlane(key, m) < key) ? 1 : 0;
+    for (int m = 0; m < count; ++m) {
+      const int km = __builtin_amdgcn_readlane(key, m);
+      rank += (km < key || (km == key && m < lane)) ? 1 : 0;
+    }
     const int addr = rank * 4;  // lanes >= count all push to lane `count`, which is never read
     src_lo = (uint32_t)__builtin_amdgcn_ds_permute(addr, (int)src_lo);
     src_hi = (uint32_t)__builtin_amdgcn_ds_permute(addr, (int)src_hi);

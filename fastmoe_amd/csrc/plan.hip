@@ -261,6 +261,53 @@ __global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __rest
   }
 }
 
+// ---- plan of a combine fed by the dispatch permutation -------------------------------------
+// fmoe_permute_build already knows every token's rows: slot t * k + j sits at packed row
+// slot_pos[t * k + j].  When every slot is a row of the combine (N == T * k), token t's segment
+// is exactly slots [t * k, t * k + k): row_ptr[t] = t * k and one thread per slot writes its
+// record -- no count, scan or atomics.  Segments have k <= 64 rows, so the consumers order them in
+// registers and the ordering pass is not needed.  A slot_pos entry outside [0, N) (an
+// inconsistent caller) yields a zero-gate record on packed row 0, so nothing is ever addressed
+// outside the expert buffers.
+template <typename TW>
+__global__ __launch_bounds__(kGroup) void k_plan_from_slots(
+    const int32_t* __restrict__ slot_pos, int64_t T, int64_t k, const TW* __restrict__ w,
+    const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
+    int64_t row_bytes, int32_t* __restrict__ row_ptr, Rec* __restrict__ rec,
+    int32_t* __restrict__ status) {
+  __shared__ int64_t off_lds[kLdsExperts + 1];
+  __shared__ int misaligned;
+  for (int i = threadIdx.x; i <= E; i += kGroup) off_lds[i] = offsets[i];
+  if (threadIdx.x == 0) misaligned = 0;
+  __syncthreads();
+  const int64_t N = T * k;  // == off_lds[E], checked on the host
+  const int64_t i = (int64_t)blockIdx.x * kGroup + threadIdx.x;
+  if (i < N) {
+    const int64_t p = slot_pos[i];
+    const bool ok = p >= 0 && p < N;
+    const int64_t g = ok ? p : 0;
+    const int64_t e = expert_of_row(off_lds, E, g);
+    Rec r;
+    r.src = (uint64_t)ptr_table[e] + (uint64_t)((g - off_lds[e]) * row_bytes);
+    r.w = ok ? ld1(w + g) : 0.f;
+    r.g = (int32_t)g;
+    rec[i] = r;
+  }
+  if (i <= T + 1) row_ptr[i] = (int32_t)(std::min<int64_t>(i, T) * k);
+  // Block 0 also writes the status words: no invalid rows, the longest segment is k, and a row
+  // is misaligned iff its expert's base or the row length is not a multiple of 16 bytes.
+  if (blockIdx.x == 0) {
+    for (int64_t x = threadIdx.x; x < E; x += kGroup)
+      if (off_lds[x + 1] > off_lds[x] && ((ptr_table[x] & 15) || (row_bytes & 15))) misaligned = 1;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      status[kStatusInvalid] = 0;
+      status[kStatusMisaligned] = misaligned;
+      status[kStatusLongest] = (int32_t)k;
+    }
+  }
+}
+
 }  // namespace fmoe
 
 extern "C" int64_t fmoe_plan_workspace_bytes(int64_t num_rows, int64_t num_tokens) {
@@ -350,4 +397,51 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   hipLaunchKernelGGL(k_plan_sort_long, dim3((unsigned)sort_groups), dim3(kGroup), 0, s, row_ptr, T,
                      status, rec_tmp, rec);
   return fmoe_host::check_launch("fmoe_build_plan(sort)");
+}
+
+extern "C" int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num_tokens,
+                                          int64_t top_k, const void* d_weights, int w_dtype,
+                                          const int64_t* d_ptr_table, const int64_t* d_offsets,
+                                          int64_t num_experts, int64_t num_rows,
+                                          int64_t row_bytes, void* d_workspace, void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  const int64_t T = num_tokens, K = top_k, E = num_experts, N = num_rows;
+  FMOE_REQUIRE(T >= 1 && K >= 1 && K <= kWave,
+               "fmoe_build_plan_from_slots: need T >= 1 and 1 <= top_k <= %d (T=%lld k=%lld)",
+               kWave, (long long)T, (long long)K);
+  FMOE_REQUIRE(E >= 1 && E <= kLdsExperts, "fmoe_build_plan_from_slots: num_experts not in [1, %d]",
+               kLdsExperts);
+  if (T >= (int64_t(1) << 30) || T * K >= (int64_t(1) << 31)) {
+    fmoe_host::set_error("fmoe_build_plan_from_slots: T*k exceeds the 32-bit row counters");
+    return FMOE_ERANGE;
+  }
+  FMOE_REQUIRE(N == T * K,
+               "fmoe_build_plan_from_slots: every slot must be a row of the combine (rows %lld != "
+               "T*k %lld); build the plan from the scatter index instead",
+               (long long)N, (long long)(T * K));
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_build_plan_from_slots: bad weight dtype %d",
+               w_dtype);
+  FMOE_REQUIRE(d_slot_pos && d_weights && d_ptr_table && d_offsets && d_workspace,
+               "fmoe_build_plan_from_slots: null device pointer");
+  FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
+               "fmoe_build_plan_from_slots: workspace not 256B-aligned");
+  FMOE_REQUIRE(row_bytes > 0, "fmoe_build_plan_from_slots: row_bytes must be > 0");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const PlanLayout L = plan_layout(N, T);
+  char* ws = static_cast<char*>(d_workspace);
+  int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
+  int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
+  Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
+  const int64_t threads = std::max<int64_t>(N, T + 2);
+  const dim3 grid((unsigned)((threads + kGroup - 1) / kGroup));
+#define FMOE_FROM_SLOTS(TW)                                                                        \
+  hipLaunchKernelGGL((k_plan_from_slots<TW>), grid, dim3(kGroup), 0, s, d_slot_pos, T, K,          \
+                     static_cast<const TW*>(d_weights), d_ptr_table, d_offsets, E, row_bytes,      \
+                     row_ptr, rec, status)
+  if (w_dtype == FMOE_F32) FMOE_FROM_SLOTS(float);
+  else if (w_dtype == FMOE_BF16) FMOE_FROM_SLOTS(bf16_t);
+  else FMOE_FROM_SLOTS(f16_t);
+#undef FMOE_FROM_SLOTS
+  return fmoe_host::check_launch("fmoe_build_plan_from_slots");
 }

@@ -19,15 +19,15 @@ The router GEMM, top-k, softmax and the expert MLPs are torch library calls, as 
 """
 from __future__ import annotations
 
-from typing import List, Sequence, Union
+from typing import List, Optional, Sequence, Union
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
 from .consts import MoEImplementation
-from .dispatch import permute_tokens
-from .ops import grouped_weighted_scatter_add
+from .dispatch import PermutedTokens, permute_tokens
+from .ops import _GroupedCombinePermuted, grouped_weighted_scatter_add
 
 __all__ = ["MoEFeedForward", "compute_experts", "gate_and_sort", "unpermute"]
 
@@ -46,8 +46,17 @@ def gate_and_sort(x: torch.Tensor, router: nn.Module, top_k: int, num_experts: i
     topk_weights = F.softmax(topk_weights, dim=-1, dtype=torch.float32).type_as(x)
     p = permute_tokens(x_flat, topk_indices, topk_weights, num_experts)
     rank_counts = torch.tensor([p.permuted_data.shape[0]], device=x.device, dtype=torch.long)
-    return (p.permuted_data, rank_counts, p.expert_counts.view(1, num_experts),
-            p.reverse_map_indices, p.sorted_weights, (B, T))
+    return _Routed((p.permuted_data, rank_counts, p.expert_counts.view(1, num_experts),
+                    p.reverse_map_indices, p.sorted_weights, (B, T)), p)
+
+
+class _Routed(tuple):
+    """gate_and_sort's 6-tuple (tiny_model.py:160-166) that also carries the permutation."""
+
+    def __new__(cls, items, permutation):
+        self = super().__new__(cls, items)
+        self.permutation = permutation
+        return self
 
 
 def compute_experts(experts: Sequence[nn.Module], recv_data: torch.Tensor,
@@ -66,15 +75,24 @@ def compute_experts(experts: Sequence[nn.Module], recv_data: torch.Tensor,
 
 
 def unpermute(x_out: Union[torch.Tensor, Sequence[torch.Tensor]], reverse_map_indices: torch.Tensor,
-              sorted_weights: torch.Tensor, original_shape, implementation=MoEImplementation.FAST):
+              sorted_weights: torch.Tensor, original_shape, implementation=MoEImplementation.FAST,
+              permutation: Optional[PermutedTokens] = None):
     """Combine of tiny_model.py:396-409.  ``x_out`` is the packed [T*k, D] tensor (as the
-    reference passes it) or the list of per-expert outputs (no concatenation)."""
+    reference passes it) or the list of per-expert outputs (no concatenation).  Given the
+    ``permutation`` that produced ``reverse_map_indices``, the FAST combine builds its plan from
+    the permutation's slot map (one kernel) instead of inverting the scatter index."""
     B, T = original_shape
     parts = list(x_out) if isinstance(x_out, (list, tuple)) else [x_out]
     D = parts[0].shape[1]
     impl = MoEImplementation(implementation)
     if impl == MoEImplementation.FAST:
-        out = grouped_weighted_scatter_add(parts, reverse_map_indices, sorted_weights, (B * T, D))
+        if permutation is not None:
+            k = permutation.slot_pos.numel() // (B * T) if B * T else 0
+            out = _GroupedCombinePermuted.apply((permutation.slot_pos, k), reverse_map_indices,
+                                                sorted_weights, (B * T, D), *parts)
+        else:
+            out = grouped_weighted_scatter_add(parts, reverse_map_indices, sorted_weights,
+                                               (B * T, D))
         return out.view(B, T, D)
     if impl == MoEImplementation.STANDARD:
         packed = parts[0] if len(parts) == 1 else torch.cat(parts, dim=0)
@@ -102,11 +120,12 @@ class MoEFeedForward(nn.Module):
                            nn.Linear(ff_dim, dim, bias=False)) for _ in range(num_experts)])
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        permuted, _, counts_by_rank, rev, weights, shape = gate_and_sort(
-            x, self.router, self.top_k, self.num_experts)
+        routed = gate_and_sort(x, self.router, self.top_k, self.num_experts)
+        permuted, _, counts_by_rank, rev, weights, shape = routed
         # the split sizes go to the host, as in the reference (recv_splits .tolist(), :197-207)
         tokens_per_expert = counts_by_rank.view(-1).tolist()
         outs = compute_experts(self.experts, permuted, tokens_per_expert)
         if self.implementation == MoEImplementation.FAST:
-            return unpermute(outs, rev, weights, shape, self.implementation)
+            return unpermute(outs, rev, weights, shape, self.implementation,
+                             permutation=routed.permutation)
         return unpermute(torch.cat(outs, 0), rev, weights, shape, self.implementation)

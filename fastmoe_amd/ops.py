@@ -44,6 +44,7 @@ __all__ = [
     "GroupedMetadata",
     "GroupedWeightedScatterAdd",
     "build_plan",
+    "build_plan_from_slots",
     "grouped_weighted_scatter_add",
     "prepare_grouped_metadata",
     "weighted_scatter_add",
@@ -252,6 +253,37 @@ def build_plan(meta: GroupedMetadata, indices: torch.Tensor, weights: torch.Tens
     return ws
 
 
+def build_plan_from_slots(meta: GroupedMetadata, slot_pos: torch.Tensor, weights: torch.Tensor,
+                          num_tokens: int, top_k: int) -> torch.Tensor:
+    """The plan of a combine fed by the dispatch permutation (``fmoe_build_plan_from_slots``).
+
+    ``slot_pos`` is the permutation's int32 slot -> packed-row map; token t's rows are
+    ``slot_pos[t * top_k : (t + 1) * top_k]``.  Requires every slot to be a row of the combine
+    (``meta.num_rows == num_tokens * top_k``) and ``top_k <= 64``.  Same layout as build_plan.
+    """
+    lib = _abi.lib()
+    N = meta.num_rows
+    if N != num_tokens * top_k or not (1 <= top_k <= 64):
+        raise ValueError(f"fastmoe_amd: a slot plan needs rows == T*k and k <= 64 "
+                         f"(rows {N}, T {num_tokens}, k {top_k})")
+    if slot_pos.dtype != torch.int32 or slot_pos.numel() != N or slot_pos.device != meta.device:
+        raise ValueError("fastmoe_amd: slot_pos must be int32 [T*k] on the experts' device")
+    w = weights.reshape(-1).contiguous()
+    if w.dtype not in _FLOAT_CODES or w.numel() != N:
+        raise ValueError("fastmoe_amd: weights must be a float [T*k] tensor")
+    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8,
+                     device=meta.device)
+    with torch.cuda.device(meta.device), _span("plan"):
+        rc = lib.fmoe_build_plan_from_slots(
+            slot_pos.contiguous().data_ptr(), num_tokens, top_k, w.data_ptr(),
+            _FLOAT_CODES[w.dtype], meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(),
+            len(meta.sizes), N, meta.hidden * meta.tensors[0].element_size(), ws.data_ptr(),
+            _stream_handle(meta.device),
+        )
+    _abi.check(rc, "fmoe_build_plan_from_slots")
+    return ws
+
+
 def plan_status(plan: torch.Tensor) -> torch.Tensor:
     """The plan's int32 status words [invalid_index_count, misaligned_flag, longest_segment]
     (a device view; longest_segment counts the rows of the busiest token)."""
@@ -318,7 +350,7 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
 
 
 def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices, weights,
-                     out_shape, expert_tensors):
+                     out_shape, expert_tensors, slots=None):
     meta = prepare_grouped_metadata(expert_tensors, indices.device)
     shape = tuple(int(s) for s in out_shape)
     if len(shape) != 2 or shape[1] != meta.hidden:
@@ -326,7 +358,12 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
     T, D = shape
     idx, w = _routing_args(indices, weights, meta.num_rows, meta.device)
     code = _mode_code(mode)
-    plan = build_plan(meta, idx, w, T, validate) if meta.num_rows > 0 else None
+    if meta.num_rows == 0:
+        plan = None
+    elif slots is not None and meta.num_rows == T * slots[1] and slots[1] <= 64:
+        plan = build_plan_from_slots(meta, slots[0], w, T, slots[1])
+    else:
+        plan = build_plan(meta, idx, w, T, validate)
     if plan is None:
         out = torch.zeros(shape, dtype=meta.dtype, device=meta.device)
     elif code == _abi.MODE_DET:
@@ -422,6 +459,22 @@ class _GroupedCombineWithOptions(torch.autograd.Function):
     def forward(ctx, options, indices, weights, out_shape, *expert_tensors):
         mode, validate = options
         return _combine_forward(ctx, mode, validate, indices, weights, out_shape, expert_tensors)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        gw, gx = _combine_backward(ctx, grad_output, ctx.needs_input_grad[2],
+                                   ctx.needs_input_grad[4:])
+        return (None, None, gw, None, *gx)
+
+
+class _GroupedCombinePermuted(torch.autograd.Function):
+    """GroupedWeightedScatterAdd for a scatter index produced by the dispatch permutation: the
+    plan comes from the permutation's slot map (first argument: (slot_pos, top_k))."""
+
+    @staticmethod
+    def forward(ctx, slots, indices, weights, out_shape, *expert_tensors):
+        return _combine_forward(ctx, None, None, indices, weights, out_shape, expert_tensors,
+                                slots=slots)
 
     @staticmethod
     def backward(ctx, grad_output):

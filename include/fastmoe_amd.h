@@ -128,6 +128,21 @@ FMOE_API int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d
                     void* d_workspace, void* stream);
 
 /*
+ * Plan of a combine fed by fmoe_permute_build (no counterpart in the reference; it replaces
+ * fmoe_build_plan when the scatter index is that permutation's reverse map): token t's rows are
+ * d_slot_pos[t * top_k + j], j < top_k, so the plan is written by one thread per slot with no
+ * counting or scanning.  Requires num_rows == num_tokens * top_k (every slot is a row of the
+ * combine: all expert ids were in range) and top_k <= 64.  d_weights are the gates in packed-row
+ * order (the permutation's sorted gates); d_ptr_table / d_offsets from fmoe_build_metadata over the
+ * per-expert buffers.  Same workspace size and layout as fmoe_build_plan(num_rows, num_tokens).
+ */
+FMOE_API int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num_tokens,
+                               int64_t top_k, const void* d_weights, int w_dtype,
+                               const int64_t* d_ptr_table, const int64_t* d_offsets,
+                               int64_t num_experts, int64_t num_rows, int64_t row_bytes,
+                               void* d_workspace, void* stream);
+
+/*
  * Forward combine (replaces _launch_grouped_kernel + _grouped_weighted_scatter_add_kernel,
  * src/fastmoe/kernels/ops.py:277-310 and :57-194).
  *

@@ -181,3 +181,73 @@ def test_unpermute_list_equals_packed():
     a = fastmoe_amd.unpermute(xs, rev, sw, (2, 4))
     b = fastmoe_amd.unpermute(torch.cat(xs), rev, sw, (2, 4))
     assert torch.equal(a, b) and a.shape == (2, 4, 40)
+
+
+# ---- the combine's plan built from the permutation's slot map ------------------------------------
+def _plan_segments(plan, N, T):
+    """{token: sorted [(g, w bits, src)]} of a plan workspace (device -> host)."""
+    lib = fastmoe_amd._abi.lib()
+    h = plan.cpu()
+    rp = h[lib.fmoe_plan_row_ptr_offset(N, T):].view(torch.int32)[: T + 2].numpy()
+    rec = h[lib.fmoe_plan_records_offset(N, T):][: 16 * N].view(torch.int64).view(-1, 2).numpy()
+    st = h[lib.fmoe_plan_status_offset():][:12].view(torch.int32).numpy()
+    segs = {}
+    for t in range(T):
+        rows = [(int(r[1] >> 32), int(r[1] & 0xFFFFFFFF), int(r[0])) for r in rec[rp[t]:rp[t + 1]]]
+        segs[t] = sorted(rows)
+    return rp, segs, st
+
+
+def test_plan_from_slots_equals_plan_from_scatter_index():
+    T, D, E, k = 300, 96, 16, 4
+    ids, w = _routing(T, E, k, seed=21)
+    x = torch.randn(T, D).to(DEV)
+    p = fastmoe_amd.permute_tokens(x, ids.to(DEV), w.to(DEV), E)
+    experts = [c.contiguous() for c in p.permuted_data.split(p.expert_counts.tolist())]
+    meta = fastmoe_amd.prepare_grouped_metadata(experts, DEV)
+    N = T * k
+    general = fastmoe_amd.build_plan(meta, p.reverse_map_indices, p.sorted_weights, T)
+    from_slots = fastmoe_amd.ops.build_plan_from_slots(meta, p.slot_pos, p.sorted_weights, T, k)
+    torch.cuda.synchronize()
+    rp_a, seg_a, st_a = _plan_segments(general, N, T)
+    rp_b, seg_b, st_b = _plan_segments(from_slots, N, T)
+    np.testing.assert_array_equal(rp_a, rp_b)
+    assert seg_a == seg_b
+    assert st_b[0] == 0 and st_b[2] == k and st_a[0] == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_unpermute_with_permutation_is_bit_identical(dtype):
+    T, D, E, k = 256, 192, 32, 6
+    ids, w = _routing(T, E, k, seed=22)
+    x = torch.randn(T, D).to(dtype).to(DEV)
+    p = fastmoe_amd.permute_tokens(x, ids.to(DEV), w.to(dtype).to(DEV), E)
+    parts = [c.clone().requires_grad_(True) for c in p.permuted_data.split(p.expert_counts.tolist())]
+    sw = p.sorted_weights.detach().clone().requires_grad_(True)
+    go = torch.randn(1, T, D, generator=torch.Generator().manual_seed(3)).to(dtype).to(DEV)
+    a = fastmoe_amd.unpermute(parts, p.reverse_map_indices, sw, (1, T), permutation=p)
+    ga = torch.autograd.grad(a, [sw, *parts], go)
+    b = fastmoe_amd.unpermute(parts, p.reverse_map_indices, sw, (1, T))
+    gb = torch.autograd.grad(b, [sw, *parts], go)
+    assert torch.equal(a, b)
+    for u, v in zip(ga, gb):
+        assert torch.equal(u, v)
+
+
+def test_plan_from_slots_with_inconsistent_slots_stays_in_bounds():
+    """Out-of-range and repeated slot positions (an inconsistent caller) are clamped to zero-gate
+    records on packed row 0: the combine runs, reads and writes only inside its buffers."""
+    T, D, E, k = 64, 32, 4, 2
+    N = T * k
+    experts = [torch.randn(N // E, D, device=DEV) for _ in range(E)]
+    meta = fastmoe_amd.prepare_grouped_metadata(experts, DEV)
+    slots = torch.arange(N, dtype=torch.int32)
+    slots[5] = N + 7
+    slots[9] = -3
+    slots[11] = slots[12]
+    w = torch.rand(N, device=DEV)
+    plan = fastmoe_amd.ops.build_plan_from_slots(meta, slots.to(DEV), w, T, k)
+    out = torch.empty(T, D, device=DEV)
+    fastmoe_amd.ops._launch_fwd(meta, fastmoe_amd._abi.MODE_DET, plan, None, None, out, False)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
