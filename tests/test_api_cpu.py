@@ -54,7 +54,8 @@ def test_workloads_match_baseline_configs():
     wl = WORKLOADS["gigachat"]
     assert (wl.T, wl.D, wl.E, wl.k, wl.dtype) == (4096, 16384, 256, 8, torch.bfloat16)
     fwd, bwd = algorithmic_bytes(wl.T, wl.D, wl.N, 2, 2)
-    assert (fwd, bwd, fwd + bwd) == (1208352768, 2282225664, 3490578432)  # BASELINE.md table
+    # compulsory bytes: fwd = N*D*2 + T*D*2 + 12N, bwd = T*D*2 + 2*N*D*2 + 16N
+    assert (fwd, bwd, fwd + bwd) == (1208352768, 2282225664, 3490578432)
     assert algorithmic_bytes(256, 512, 512, 4, 4) == (1579008, 2629632)
     assert algorithmic_bytes(8192, 4096, 49152, 2, 2)[0] == 470351872
     assert algorithmic_bytes(16384, 7168, 131072, 2, 2)[0] == 2115502080
