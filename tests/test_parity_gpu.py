@@ -500,6 +500,40 @@ def test_graph_capture_replays():
         _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum().item()
 
 
+def test_graph_capture_autograd_step_replays():
+    """The bench's timed step -- metadata, plan, forward and both backward passes through the
+    autograd API -- captured once as a graph: every replay (with eager work in between) gives the
+    eager step's output and gradients bit for bit."""
+    wl, T, idx, w, experts = _inputs("gigachat", T=128)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    xs = [x.requires_grad_(True) for x in xd]
+    wd.requires_grad_(True)
+    go = torch.randn(T, wl.D, generator=torch.Generator().manual_seed(5)).to(wl.dtype).to(DEV)
+    inputs = [wd, *xs]
+
+    def step():
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idd, wd, (T, wl.D))
+        return (out, *torch.autograd.grad(out, inputs, go))
+
+    eager = [bits(t) for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static = step()
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(static, eager):
+            np.testing.assert_array_equal(bits(got), want)
+        _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum().item()
+
+
 @pytest.mark.parametrize("name", ["gigachat"])
 def test_full_size_fwd_bwd_parity(name):
     """The BASELINE headline config at its full size: forward bit-exact, grad_X bit-exact,
