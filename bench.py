@@ -235,7 +235,7 @@ def main() -> int:
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=0,
                     help="tokens of the CPU baseline sample (0 = the whole workload)")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=8)
     ap.add_argument("--no-slot-plan", action="store_true",
                     help="moe path: build the combine's plan from the scatter index instead of "
                          "the permutation's slot map")
