@@ -15,6 +15,9 @@ algorithm on them, computed with torch CPU ops exactly as the reference calls th
   grad_w  sum_d grad_out[idx[g], d] * X[g, d] in fp64 (autograd of the STANDARD combine,
           src/fastmoe/models/tiny_model.py:400-403; the reference's fast path returns none)
 
+The ``permute_*`` cases hold the dispatch permutation of src/fastmoe/models/tiny_model.py:94-138
+(stable argsort) on seeded top-k routing.
+
 The ``kat_n10_d4`` case is the shape of the reference's only known-answer test
 (tests/test_cpu_moe.py:94-114, N=10, D=4, 5 tokens), seeded here; ``out_loop`` is that test's
 brute-force loop.  16-bit tensors are stored as their uint16 bit patterns; dtypes as strings.
@@ -108,6 +111,41 @@ def long_segments() -> dict:
     return _case(xs, idx, w, T, grad_out, True)
 
 
+def permute_case(T: int, D: int, E: int, k: int, dtype, seed: int, zipf: bool = False) -> dict:
+    """The dispatch permutation (src/fastmoe/models/tiny_model.py:94-138) evaluated with the
+    reference's own torch calls, argsort made stable: expert ids, gates, token rows, and the
+    expected counts, offsets, reverse map, slot -> row map, sorted gates and gathered rows."""
+    gen = torch.Generator().manual_seed(seed)
+    logits = torch.randn(T, E, generator=gen)
+    if zipf:
+        logits = logits + torch.from_numpy(np.minimum(np.random.default_rng(seed).zipf(1.2, E), 10)
+                                           .astype(np.float32))[None, :]
+    x = torch.randn(T, D, generator=gen).to(dtype)
+    topk_weights, topk_indices = torch.topk(logits, k, dim=-1)                      # :95
+    topk_weights = torch.softmax(topk_weights, dim=-1, dtype=torch.float32).to(dtype)  # :100
+    flat = topk_indices.view(-1)
+    sort_indices = torch.argsort(flat, stable=True)                                 # :112
+    rev = torch.arange(T).repeat_interleave(k)[sort_indices]                        # :121-125
+    sorted_weights = topk_weights.view(-1)[sort_indices]                            # :128
+    permuted = x[rev]                                                               # :133
+    counts = torch.bincount(flat[sort_indices], minlength=E)                        # :138
+    slot_pos = torch.empty_like(sort_indices)
+    slot_pos[sort_indices] = torch.arange(T * k)
+    return {
+        "ids": topk_indices.numpy().astype(np.int64),
+        "gates": _store(topk_weights),
+        "x": _store(x),
+        "E": np.array(E, dtype=np.int64),
+        "x_dtype": np.array(NAMES[dtype]),
+        "counts": counts.numpy().astype(np.int64),
+        "offsets": np.concatenate([[0], np.cumsum(counts.numpy())]).astype(np.int64),
+        "rev": rev.numpy().astype(np.int64),
+        "slot_pos": slot_pos.numpy().astype(np.int32),
+        "sorted_gates": _store(sorted_weights),
+        "permuted": _store(permuted),
+    }
+
+
 CASES = {
     "kat_n10_d4": kat_n10_d4,
     # plumbing recipe (top-2 of 8 experts, fp32) at a fixture-sized T and D
@@ -118,6 +156,9 @@ CASES = {
     "topk_f16_t16_d24_bf16w": lambda: routed("topk_f16", 16, 24, 4, 2, torch.float16, 5,
                                              w_dtype=torch.bfloat16),
     "long_segments_f32": long_segments,
+    # the dispatch permutation that produces such scatter indices
+    "permute_topk_bf16_t40_d24": lambda: permute_case(40, 24, 8, 3, torch.bfloat16, 11),
+    "permute_zipf_f32_t64_d16": lambda: permute_case(64, 16, 12, 4, torch.float32, 12, zipf=True),
 }
 
 

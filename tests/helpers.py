@@ -69,7 +69,23 @@ _TORCH_DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.floa
 
 
 def golden_names():
-    return sorted(p.stem for p in GOLDEN_DIR.glob("*.npz"))
+    """The combine fixtures."""
+    return sorted(p.stem for p in GOLDEN_DIR.glob("*.npz") if not p.stem.startswith("permute_"))
+
+
+def permute_golden_names():
+    """The dispatch-permutation fixtures."""
+    return sorted(p.stem for p in GOLDEN_DIR.glob("permute_*.npz"))
+
+
+def load_permute_golden(name: str) -> dict:
+    """A permutation fixture as CPU tensors (ids, gates, x) plus the stored expected arrays."""
+    z = np.load(GOLDEN_DIR / f"{name}.npz", allow_pickle=False)
+    dt = _TORCH_DTYPES[str(z["x_dtype"])]
+    case = {k: z[k] for k in z.files}
+    case.update(ids=torch.from_numpy(z["ids"].copy()), gates=_from_store(z["gates"], dt),
+                x=_from_store(z["x"], dt), E=int(z["E"]), dtype=dt)
+    return case
 
 
 def _from_store(a: np.ndarray, dtype: torch.dtype) -> torch.Tensor:

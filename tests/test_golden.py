@@ -68,3 +68,29 @@ def test_torch_restatement_reproduces_fixture(name):
     sizes = [x.shape[0] for x in c["experts"]]
     gx = torch.cat(torch_ref.bwd_grad_x(c["grad_out"], c["idx"], c["w"], sizes, c["x_dtype"]), 0)
     np.testing.assert_array_equal(to_np(gx), c["grad_x"])
+
+
+PERMUTE_NAMES = __import__("tests.helpers", fromlist=["x"]).permute_golden_names()
+
+
+def test_permutation_fixture_set_is_complete():
+    assert set(PERMUTE_NAMES) >= {"permute_topk_bf16_t40_d24", "permute_zipf_f32_t64_d16"}
+
+
+@pytest.mark.parametrize("name", PERMUTE_NAMES)
+def test_oracle_permutation_matches_fixture(name):
+    """The C oracle's stable counting sort against the reference's torch calls
+    (tiny_model.py:108-138 with a stable argsort) stored in the fixture."""
+    from tests.helpers import load_permute_golden
+
+    c = load_permute_golden(name)
+    counts, offsets, rev, slot_pos, bad = cref.permute(c["ids"].numpy(), c["E"])
+    assert bad == 0
+    np.testing.assert_array_equal(counts, c["counts"])
+    np.testing.assert_array_equal(offsets, c["offsets"])
+    np.testing.assert_array_equal(rev, c["rev"])
+    np.testing.assert_array_equal(slot_pos, c["slot_pos"])
+    np.testing.assert_array_equal(to_np(c["x"])[rev], c["permuted"])
+    sorted_gates = np.empty_like(c["sorted_gates"])
+    sorted_gates[slot_pos] = to_np(c["gates"]).reshape(-1)
+    np.testing.assert_array_equal(sorted_gates, c["sorted_gates"])

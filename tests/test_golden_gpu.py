@@ -43,3 +43,20 @@ def test_weighted_scatter_add_matches_fixture(name):
     fastmoe_amd.weighted_scatter_add(src, c["idx"].to(DEV), c["w"].to(DEV), (c["T"], c["D"]),
                                      out=out)
     np.testing.assert_array_equal(to_np(out).view(np.uint32), c["out_fb"].view(np.uint32))
+
+
+@pytest.mark.parametrize("name", __import__("tests.helpers", fromlist=["x"]).permute_golden_names())
+@pytest.mark.parametrize("id_dtype", [torch.int64, torch.int32])
+def test_permute_tokens_matches_fixture(name, id_dtype):
+    from tests.helpers import load_permute_golden
+
+    c = load_permute_golden(name)
+    p = fastmoe_amd.permute_tokens(c["x"].to(DEV), c["ids"].to(id_dtype).to(DEV),
+                                   c["gates"].to(DEV), c["E"])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(p.expert_counts.cpu().numpy(), c["counts"])
+    np.testing.assert_array_equal(p.expert_offsets.cpu().numpy(), c["offsets"])
+    np.testing.assert_array_equal(p.reverse_map_indices.cpu().numpy(), c["rev"])
+    np.testing.assert_array_equal(p.slot_pos.cpu().numpy(), c["slot_pos"])
+    np.testing.assert_array_equal(to_np(p.sorted_weights), c["sorted_gates"])
+    np.testing.assert_array_equal(to_np(p.permuted_data), c["permuted"])
