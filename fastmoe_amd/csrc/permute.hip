@@ -9,7 +9,7 @@
 // of equal ids unspecified.
 //
 // Slot i = t * k + j is token t's j-th routing choice.  Steps (caller's stream, no host sync):
-//   1. rank    one 256-thread workgroup per block of 256 slots: each slot's stable rank among the
+//   1. rank    one workgroup per block of 1024 slots (256 when E > 1024): each slot's stable rank among the
 //              block's slots of the same expert (wave ballots on the key bits give the lanes of
 //              a wave with an equal key; per-wave counts in LDS give the waves before it), and
 //              the block's count of every expert (row b of blkcnt[nb][E + 1]).
@@ -28,9 +28,12 @@
 
 namespace fmoe {
 
-constexpr int kPermBlock = kGroup;        // slots per ranking block
-constexpr int kPermMaxExperts = 4096;     // LDS-resident per-wave counters (64 KiB)
-constexpr int kPermSmallExperts = 1024;   // the 16 KiB variant of the ranking kernel
+// Slots per ranking block: 1024 (16 waves) while the per-wave expert counters fit in 64 KiB of
+// LDS (E <= 1024), else 256 (4 waves).  Bigger blocks keep the block-count table small for the scan.
+constexpr int kPermBlockLarge = 1024;
+constexpr int kPermBlockSmall = kGroup;
+constexpr int kPermMaxExperts = 4096;     // 4 waves x 4097 per-wave counters: 64 KiB of LDS
+constexpr int kPermSmallExperts = 1024;   // 16 waves x 1025 per-wave counters: 64 KiB of LDS
 constexpr int kPermScanThreads = 1024;
 constexpr int kPermGatherWaves = 8;
 
@@ -40,9 +43,14 @@ struct PermLayout {
   int64_t blkcnt, rank, off, total;
 };
 
+__host__ __device__ inline int perm_block(int64_t E) {
+  return E <= kPermSmallExperts ? kPermBlockLarge : kPermBlockSmall;
+}
+
 __host__ __device__ inline PermLayout perm_layout(int64_t N, int64_t E) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
-  const int64_t nb = (N + kPermBlock - 1) / kPermBlock;
+  const int blk = perm_block(E);
+  const int64_t nb = (N + blk - 1) / blk;
   PermLayout L;
   L.blkcnt = 0;
   L.rank = L.blkcnt + up(nb * (E + 1) * 4);
@@ -58,18 +66,19 @@ __device__ __forceinline__ int slot_key(const TI* __restrict__ ids, int64_t i, i
   return (e >= 0 && e < E) ? (int)e : (int)E;
 }
 
-template <typename TI, int MAXE>
-__global__ __launch_bounds__(kPermBlock) void k_perm_rank(const TI* __restrict__ ids, int64_t N,
-                                                          int64_t E, int key_bits,
-                                                          int32_t* __restrict__ blkcnt,
-                                                          int32_t* __restrict__ rank) {
-  __shared__ int32_t wcnt[kWavesPerGroup][MAXE + 1];
+template <typename TI, int MAXE, int BLK>
+__global__ __launch_bounds__(BLK) void k_perm_rank(const TI* __restrict__ ids, int64_t N,
+                                                   int64_t E, int key_bits,
+                                                   int32_t* __restrict__ blkcnt,
+                                                   int32_t* __restrict__ rank) {
+  constexpr int W = BLK / kWave;
+  __shared__ int32_t wcnt[W][MAXE + 1];
   const int E1 = (int)E + 1;
-  for (int w = 0; w < kWavesPerGroup; ++w)
-    for (int k = threadIdx.x; k < E1; k += kPermBlock) wcnt[w][k] = 0;
+  for (int w = 0; w < W; ++w)
+    for (int k = threadIdx.x; k < E1; k += BLK) wcnt[w][k] = 0;
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
-  const int64_t i = (int64_t)blockIdx.x * kPermBlock + threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * BLK + threadIdx.x;
   const bool live = i < N;
   const int key = live ? slot_key(ids, i, E) : 0;
   // lanes of this wave holding the same key (dead lanes excluded)
@@ -90,10 +99,10 @@ __global__ __launch_bounds__(kPermBlock) void k_perm_rank(const TI* __restrict__
     rank[i] = before;
   }
   int32_t* row = blkcnt + (int64_t)blockIdx.x * E1;
-  for (int k = threadIdx.x; k < E1; k += kPermBlock) {
+  for (int k = threadIdx.x; k < E1; k += BLK) {
     int c = 0;
 #pragma unroll
-    for (int w = 0; w < kWavesPerGroup; ++w) c += wcnt[w][k];
+    for (int w = 0; w < W; ++w) c += wcnt[w][k];
     row[k] = c;
   }
 }
@@ -201,7 +210,7 @@ __global__ __launch_bounds__(kPermScanThreads) void k_perm_scan(
 template <typename TI, typename TG>
 __global__ __launch_bounds__(kGroup) void k_perm_fill(const TI* __restrict__ ids,
                                                       const TG* __restrict__ gates, int64_t N,
-                                                      int64_t E, int64_t k,
+                                                      int64_t E, int64_t k, int blk,
                                                       const int32_t* __restrict__ blkcnt,
                                                       const int32_t* __restrict__ rank,
                                                       const int32_t* __restrict__ off,
@@ -211,7 +220,7 @@ __global__ __launch_bounds__(kGroup) void k_perm_fill(const TI* __restrict__ ids
   const int64_t i = (int64_t)blockIdx.x * kGroup + threadIdx.x;
   if (i >= N) return;
   const int key = slot_key(ids, i, E);
-  const int64_t b = i / kPermBlock;
+  const int64_t b = i / blk;
   const int pos = off[key] + blkcnt[b * (E + 1) + key] + rank[i];
   if (pos < 0 || pos >= N) return;  // unreachable for a consistent rank/scan; never write outside
   rev[pos] = i / k;
@@ -284,7 +293,8 @@ extern "C" int fmoe_permute_build(const void* d_expert_ids, int id_dtype, const 
     return FMOE_ERANGE;
   }
   const int64_t N = T * K;
-  const int64_t nb = (N + kPermBlock - 1) / kPermBlock;
+  const int blk = perm_block(E);
+  const int64_t nb = (N + blk - 1) / blk;
   if (nb * (E + 1) >= (int64_t(1) << 31)) {
     fmoe_host::set_error("fmoe_permute_build: block count table too large");
     return FMOE_ERANGE;
@@ -308,15 +318,15 @@ extern "C" int fmoe_permute_build(const void* d_expert_ids, int id_dtype, const 
   int key_bits = 0;
   while ((int64_t(1) << key_bits) <= E) ++key_bits;  // keys lie in [0, E]
   if (N > 0) {
-#define FMOE_PRANK(TI, MAXE)                                                                       \
-  hipLaunchKernelGGL((k_perm_rank<TI, MAXE>), dim3((unsigned)nb), dim3(kPermBlock), 0, s,          \
+#define FMOE_PRANK(TI, MAXE, BLK)                                                                  \
+  hipLaunchKernelGGL((k_perm_rank<TI, MAXE, BLK>), dim3((unsigned)nb), dim3(BLK), 0, s,            \
                      static_cast<const TI*>(d_expert_ids), N, E, key_bits, blkcnt, rank)
     if (id_dtype == FMOE_I64) {
-      if (E <= kPermSmallExperts) FMOE_PRANK(int64_t, kPermSmallExperts);
-      else FMOE_PRANK(int64_t, kPermMaxExperts);
+      if (blk == kPermBlockLarge) FMOE_PRANK(int64_t, kPermSmallExperts, kPermBlockLarge);
+      else FMOE_PRANK(int64_t, kPermMaxExperts, kPermBlockSmall);
     } else {
-      if (E <= kPermSmallExperts) FMOE_PRANK(int32_t, kPermSmallExperts);
-      else FMOE_PRANK(int32_t, kPermMaxExperts);
+      if (blk == kPermBlockLarge) FMOE_PRANK(int32_t, kPermSmallExperts, kPermBlockLarge);
+      else FMOE_PRANK(int32_t, kPermMaxExperts, kPermBlockSmall);
     }
 #undef FMOE_PRANK
     if (int rc = fmoe_host::check_launch("fmoe_permute_build(rank)")) return rc;
@@ -330,7 +340,8 @@ extern "C" int fmoe_permute_build(const void* d_expert_ids, int id_dtype, const 
 #define FMOE_PFILL(TI, TG)                                                                         \
   hipLaunchKernelGGL((k_perm_fill<TI, TG>), grid, dim3(kGroup), 0, s,                              \
                      static_cast<const TI*>(d_expert_ids), static_cast<const TG*>(d_gates), N, E,  \
-                     K, blkcnt, rank, off, d_rev, static_cast<TG*>(d_sorted_gates), d_slot_pos)
+                     K, blk, blkcnt, rank, off, d_rev, static_cast<TG*>(d_sorted_gates),          \
+                     d_slot_pos)
   if (id_dtype == FMOE_I64) {
     if (g4) FMOE_PFILL(int64_t, uint32_t);
     else FMOE_PFILL(int64_t, uint16_t);

@@ -25,8 +25,11 @@ def test_cpu_tensors_raise():
 def test_workspace_size():
     lib = _abi.lib()
     n = lib.fmoe_permute_workspace_bytes(32768, 256)
-    nb = 32768 // 256
+    nb = 32768 // 1024  # 1024-slot ranking blocks while E <= 1024
     assert n >= nb * 257 * 4 + 32768 * 4 + 257 * 4 and n % 256 == 0
+    n = lib.fmoe_permute_workspace_bytes(32768, 3000)
+    nb = 32768 // 256  # 256-slot blocks beyond
+    assert n >= nb * 3001 * 4 + 32768 * 4 + 3001 * 4 and n % 256 == 0
     assert lib.fmoe_permute_workspace_bytes(-1, 4) < 0
     assert lib.fmoe_permute_workspace_bytes(10, 0) < 0
 
