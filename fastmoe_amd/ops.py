@@ -152,23 +152,21 @@ def _check_experts(expert_tensors: Sequence[torch.Tensor]):
         raise ValueError(f"fastmoe_amd: expert tensors must be 2-D [rows, D], got {tuple(ref.shape)}")
     dtype, device, hidden = ref.dtype, ref.device, ref.shape[1]
     dev_index = ref.get_device()
-    row_strides = (hidden, 1)
     sizes, ptrs = [], []
     for i, t in enumerate(expert_tensors):
         shape = t.shape
-        if t.dtype != dtype or t.get_device() != dev_index:
-            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] differs in device/dtype from [0]")
-        if len(shape) != 2 or shape[1] != hidden:
+        # is_contiguous() on a 2-D tensor is exactly the layout the kernels address: strides
+        # (D, 1) for several rows, a unit column stride for one row, anything for no rows.
+        if (t.dtype != dtype or t.get_device() != dev_index or len(shape) != 2
+                or shape[1] != hidden or not t.is_contiguous()):
+            if t.dtype != dtype or t.get_device() != dev_index:
+                raise ValueError(f"fastmoe_amd: expert_tensors[{i}] differs in device/dtype from [0]")
+            if len(shape) != 2 or shape[1] != hidden:
+                raise ValueError(f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(shape)}, "
+                                 f"expected [*, {hidden}]")
             raise ValueError(
-                f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(shape)}, expected [*, {hidden}]"
-            )
+                f"fastmoe_amd: expert_tensors[{i}] must be row-contiguous (strides {t.stride()})")
         n = shape[0]
-        if n > 1 and t.stride() != row_strides:
-            raise ValueError(
-                f"fastmoe_amd: expert_tensors[{i}] must be row-contiguous (strides {t.stride()})"
-            )
-        if n == 1 and hidden > 1 and t.stride(1) != 1:
-            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] must have unit column stride")
         sizes.append(n)
         ptrs.append(t.data_ptr() if n else 0)
     return dtype, device, hidden, sizes, ptrs
