@@ -11,6 +11,7 @@ from .ops import (
     GroupedWeightedScatterAdd,
     build_plan,
     grouped_weighted_scatter_add,
+    invert_scatter_index,
     prepare_grouped_metadata,
     weighted_scatter_add,
 )
@@ -27,6 +28,7 @@ __all__ = [
     "unpermute",
     "build_plan",
     "grouped_weighted_scatter_add",
+    "invert_scatter_index",
     "prepare_grouped_metadata",
     "weighted_scatter_add",
 ]

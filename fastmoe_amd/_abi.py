@@ -43,6 +43,9 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_vp, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
     ),
+    "fmoe_invert_scatter_index": (
+        _c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp],
+    ),
     "fmoe_combine_fwd": (
         _c_int,
         [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,

@@ -20,6 +20,9 @@
 //                     writes them in order.
 //                     Shorter segments are ordered by the consumer in registers, so every result
 //                     is bit-identical run to run even though the fill order is not.
+//
+// fmoe_invert_scatter_index runs the same count + scan, then writes bare row numbers (ascending
+// in every segment) instead of records.
 #include <algorithm>
 
 #include "common.h"
@@ -261,6 +264,47 @@ __global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __rest
   }
 }
 
+// ---- the bare CSR inverse (fmoe_invert_scatter_index) ---------------------------------------
+// Same count + scan as the plan.  The fill writes bare row numbers; then one wave per segment
+// writes its rows in ascending order.  Row numbers are distinct, so a row's place in its segment
+// is the count of smaller row numbers there.
+template <typename TI>
+__global__ __launch_bounds__(kGroup) void k_invert_fill(const TI* __restrict__ idx, int64_t N,
+                                                        int64_t T, int32_t* __restrict__ cursor,
+                                                        int32_t* __restrict__ tmp) {
+  const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
+  if (g >= N) return;
+  const int64_t t = (int64_t)idx[g];
+  tmp[atomicAdd(&cursor[(t >= 0 && t < T) ? t : T], 1)] = (int32_t)g;
+}
+
+// Segments b in [0, T] (b == T: out-of-range rows), one wave each, grid-strided.  A segment of up
+// to 64 rows is ranked in registers; a longer one from memory, quadratic in its length.
+__global__ __launch_bounds__(kGroup) void k_invert_order(const int32_t* __restrict__ row_ptr,
+                                                         int64_t T,
+                                                         const int32_t* __restrict__ tmp,
+                                                         int32_t* __restrict__ rows) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int64_t b = (int64_t)blockIdx.x * kWavesPerGroup + uniform(threadIdx.x / kWave); b <= T;
+       b += (int64_t)gridDim.x * kWavesPerGroup) {
+    const int beg = row_ptr[b];
+    const int c = row_ptr[b + 1] - beg;
+    if (c <= kWave) {
+      const int v = lane < c ? tmp[beg + lane] : 0x7fffffff;
+      int rank = 0;
+      for (int m = 0; m < c; ++m) rank += (__shfl(v, m, kWave) < v) ? 1 : 0;
+      if (lane < c) rows[beg + rank] = v;
+    } else {
+      for (int i = lane; i < c; i += kWave) {
+        const int v = tmp[beg + i];
+        int rank = 0;
+        for (int m = 0; m < c; ++m) rank += (tmp[beg + m] < v) ? 1 : 0;
+        rows[beg + rank] = v;
+      }
+    }
+  }
+}
+
 // ---- plan of a combine fed by the dispatch permutation -------------------------------------
 // fmoe_permute_build already knows every token's rows: slot t * k + j sits at packed row
 // slot_pos[t * k + j].  When every slot is a row of the combine (N == T * k), token t's segment
@@ -310,6 +354,37 @@ __global__ __launch_bounds__(kGroup) void k_plan_from_slots(
 
 }  // namespace fmoe
 
+namespace {
+
+// Count + scan of the scatter index into row_ptr[T + 2] and cursor[T + 1] (= row_ptr[0..T]).
+int launch_count_scan(const void* d_indices, int idx_dtype, int64_t N, int64_t T, int32_t* cursor,
+                      int32_t* row_ptr, int32_t* status, hipStream_t s, const char* who) {
+  using namespace fmoe;
+  const int64_t nb = T + 1;
+  if (nb <= kLdsTokens && N < (int64_t(1) << 27)) {
+    if (idx_dtype == FMOE_I64)
+      hipLaunchKernelGGL(k_plan_count_scan_lds<int64_t>, dim3(1), dim3(kScanThreads), 0, s,
+                         static_cast<const int64_t*>(d_indices), N, T, cursor, row_ptr, status);
+    else
+      hipLaunchKernelGGL(k_plan_count_scan_lds<int32_t>, dim3(1), dim3(kScanThreads), 0, s,
+                         static_cast<const int32_t*>(d_indices), N, T, cursor, row_ptr, status);
+    return fmoe_host::check_launch(who);
+  }
+  hipLaunchKernelGGL(k_plan_zero, dim3((unsigned)((nb + kGroup - 1) / kGroup)), dim3(kGroup), 0,
+                     s, cursor, nb);
+  if (int rc = fmoe_host::check_launch(who)) return rc;
+  if (N > 0) {
+    hipLaunchKernelGGL(k_plan_count_global, dim3((unsigned)((N + kGroup - 1) / kGroup)),
+                       dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, cursor);
+    if (int rc = fmoe_host::check_launch(who)) return rc;
+  }
+  hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, cursor, T, row_ptr,
+                     status);
+  return fmoe_host::check_launch(who);
+}
+
+}  // namespace
+
 extern "C" int64_t fmoe_plan_workspace_bytes(int64_t num_rows, int64_t num_tokens) {
   if (num_rows < 0 || num_tokens < 1) return -1;
   return fmoe::plan_layout(num_rows, num_tokens).total;
@@ -353,29 +428,10 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
   Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
-  const int64_t nb = T + 1;
 
-  if (nb <= kLdsTokens && N < (int64_t(1) << 27)) {
-    if (idx_dtype == FMOE_I64)
-      hipLaunchKernelGGL(k_plan_count_scan_lds<int64_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int64_t*>(d_indices), N, T, cursor, row_ptr, status);
-    else
-      hipLaunchKernelGGL(k_plan_count_scan_lds<int32_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int32_t*>(d_indices), N, T, cursor, row_ptr, status);
-    if (int rc = fmoe_host::check_launch("fmoe_build_plan(count_scan)")) return rc;
-  } else {
-    hipLaunchKernelGGL(k_plan_zero, dim3((unsigned)((nb + kGroup - 1) / kGroup)), dim3(kGroup), 0,
-                       s, cursor, nb);
-    if (int rc = fmoe_host::check_launch("fmoe_build_plan(zero)")) return rc;
-    if (N > 0) {
-      hipLaunchKernelGGL(k_plan_count_global, dim3((unsigned)((N + kGroup - 1) / kGroup)),
-                         dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, cursor);
-      if (int rc = fmoe_host::check_launch("fmoe_build_plan(count)")) return rc;
-    }
-    hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, cursor, T, row_ptr,
-                       status);
-    if (int rc = fmoe_host::check_launch("fmoe_build_plan(scan)")) return rc;
-  }
+  if (int rc = launch_count_scan(d_indices, idx_dtype, N, T, cursor, row_ptr, status, s,
+                                 "fmoe_build_plan"))
+    return rc;
   if (N == 0) return FMOE_OK;
   const dim3 grid((unsigned)((N + kGroup - 1) / kGroup));
 #define FMOE_FILL(TI, TW)                                                                          \
@@ -444,4 +500,47 @@ extern "C" int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num
   else FMOE_FROM_SLOTS(f16_t);
 #undef FMOE_FROM_SLOTS
   return fmoe_host::check_launch("fmoe_build_plan_from_slots");
+}
+
+extern "C" int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, int64_t num_rows,
+                                         int64_t num_tokens, int32_t* d_row_ptr, int32_t* d_rows,
+                                         void* d_workspace, void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  const int64_t N = num_rows, T = num_tokens;
+  FMOE_REQUIRE(N >= 0, "fmoe_invert_scatter_index: num_rows must be >= 0");
+  FMOE_REQUIRE(T >= 1, "fmoe_invert_scatter_index: num_tokens must be >= 1");
+  if (N >= (int64_t(1) << 31) || T >= (int64_t(1) << 30)) {
+    fmoe_host::set_error("fmoe_invert_scatter_index: N=%lld / T=%lld exceed the 32-bit row counters",
+                         (long long)N, (long long)T);
+    return FMOE_ERANGE;
+  }
+  FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype), "fmoe_invert_scatter_index: bad index dtype %d",
+               idx_dtype);
+  FMOE_REQUIRE(d_row_ptr && d_workspace, "fmoe_invert_scatter_index: null device pointer");
+  FMOE_REQUIRE(N == 0 || (d_indices && d_rows), "fmoe_invert_scatter_index: null indices/rows");
+  FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
+               "fmoe_invert_scatter_index: workspace not 256B-aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const PlanLayout L = plan_layout(N, T);
+  char* ws = static_cast<char*>(d_workspace);
+  int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
+  int32_t* cursor = reinterpret_cast<int32_t*>(ws + L.cursor);
+  int32_t* tmp = reinterpret_cast<int32_t*>(ws + L.rec_tmp);
+  if (int rc = launch_count_scan(d_indices, idx_dtype, N, T, cursor, d_row_ptr, status, s,
+                                 "fmoe_invert_scatter_index"))
+    return rc;
+  if (N == 0) return FMOE_OK;
+  const dim3 grid((unsigned)((N + kGroup - 1) / kGroup));
+  if (idx_dtype == FMOE_I64)
+    hipLaunchKernelGGL(k_invert_fill<int64_t>, grid, dim3(kGroup), 0, s,
+                       static_cast<const int64_t*>(d_indices), N, T, cursor, tmp);
+  else
+    hipLaunchKernelGGL(k_invert_fill<int32_t>, grid, dim3(kGroup), 0, s,
+                       static_cast<const int32_t*>(d_indices), N, T, cursor, tmp);
+  if (int rc = fmoe_host::check_launch("fmoe_invert_scatter_index(fill)")) return rc;
+  const int64_t groups = std::min<int64_t>((T + 1 + kWavesPerGroup - 1) / kWavesPerGroup, 2048);
+  hipLaunchKernelGGL(k_invert_order, dim3((unsigned)groups), dim3(kGroup), 0, s, d_row_ptr, T, tmp,
+                     d_rows);
+  return fmoe_host::check_launch("fmoe_invert_scatter_index(order)");
 }

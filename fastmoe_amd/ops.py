@@ -282,6 +282,34 @@ def build_plan_from_slots(meta: GroupedMetadata, slot_pos: torch.Tensor, weights
     return ws
 
 
+def invert_scatter_index(indices: torch.Tensor, num_tokens: int):
+    """The token-major inverse of ``indices`` as a CSR (``fmoe_invert_scatter_index``).
+
+    Returns ``(row_ptr, rows)``, int32 device tensors of T + 2 and N entries: token t's packed
+    rows are ``rows[row_ptr[t]:row_ptr[t + 1]]`` in ascending order, and segment T holds the rows
+    whose index lies outside [0, num_tokens).  Equal to a stable argsort of ``indices`` (with
+    out-of-range indices mapped to T) and the exclusive prefix of its bincount.
+    """
+    lib = _abi.lib()
+    _require_cuda(indices, "indices")
+    if indices.dtype not in _INDEX_CODES:
+        raise TypeError(f"fastmoe_amd: indices must be int64 or int32, got {indices.dtype}")
+    if num_tokens < 1:
+        raise ValueError(f"fastmoe_amd: num_tokens must be >= 1, got {num_tokens}")
+    idx = indices.reshape(-1).contiguous()
+    N, dev = idx.numel(), idx.device
+    row_ptr = torch.empty(num_tokens + 2, dtype=torch.int32, device=dev)
+    rows = torch.empty(N, dtype=torch.int32, device=dev)
+    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev), _span("invert_scatter_index"):
+        rc = lib.fmoe_invert_scatter_index(
+            idx.data_ptr(), _INDEX_CODES[idx.dtype], N, num_tokens, row_ptr.data_ptr(),
+            rows.data_ptr(), ws.data_ptr(), _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_invert_scatter_index")
+    return row_ptr, rows
+
+
 def plan_status(plan: torch.Tensor) -> torch.Tensor:
     """The plan's int32 status words [invalid_index_count, misaligned_flag, longest_segment]
     (a device view; longest_segment counts the rows of the busiest token)."""

@@ -30,6 +30,7 @@
  *   fmoe_build_plan        <- no counterpart: the token-major inverse of the scatter index that the
  *                             deterministic combine and the backward read (ops.py:344 gathers by
  *                             scatter index on the fly instead)
+ *   fmoe_invert_scatter_index <- no counterpart either: the same inverse as a bare CSR
  *   fmoe_permute_*         <- the sort-and-gather of MoEFeedForward.gate_and_sort
  *                             src/fastmoe/models/tiny_model.py:108-138 (the combine's producer)
  */
@@ -141,6 +142,21 @@ FMOE_API int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num_t
                                const int64_t* d_ptr_table, const int64_t* d_offsets,
                                int64_t num_experts, int64_t num_rows, int64_t row_bytes,
                                void* d_workspace, void* stream);
+
+/*
+ * The token-major inverse of the scatter index as a bare CSR (no counterpart in the reference,
+ * whose backward gathers by scatter index instead, ops.py:344; this is the plan without the
+ * records, for callers that want the inverse index itself):
+ *   d_row_ptr[T + 2] int32 : token t's rows are d_rows[d_row_ptr[t] .. d_row_ptr[t + 1]); segment T
+ *                            holds the rows whose index lies outside [0, T)
+ *   d_rows[N]        int32 : row numbers g, ascending within every segment
+ * d_indices : [N] scatter index, FMOE_I64 or FMOE_I32.  Workspace: fmoe_plan_workspace_bytes(N, T)
+ * bytes, 256-byte aligned, no zero-fill.  A segment longer than 64 rows is ordered in time
+ * quadratic in its length.
+ */
+FMOE_API int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, int64_t num_rows,
+                              int64_t num_tokens, int32_t* d_row_ptr, int32_t* d_rows,
+                              void* d_workspace, void* stream);
 
 /*
  * Forward combine (replaces _launch_grouped_kernel + _grouped_weighted_scatter_add_kernel,

@@ -106,6 +106,24 @@ def test_combine_entry_points_reject_bad_arguments():
     assert rc == _abi.EINVAL
 
 
+def test_invert_scatter_index_rejects_bad_arguments():
+    lib = _abi.lib()
+    dev = 0x10000
+    ws = dev * 256
+    cases = {
+        "num_rows": (dev, _abi.I64, -1, 4, dev, dev, ws),
+        "num_tokens": (dev, _abi.I64, 4, 0, dev, dev, ws),
+        "dtype": (dev, _abi.F32, 4, 4, dev, dev, ws),
+        "null": (dev, _abi.I64, 4, 4, None, dev, ws),
+        "aligned": (dev, _abi.I64, 4, 4, dev, dev, ws + 8),
+    }
+    for word, args in cases.items():
+        rc = lib.fmoe_invert_scatter_index(*args, None)
+        assert rc == _abi.EINVAL and word.encode() in lib.fmoe_last_error(), word
+    rc = lib.fmoe_invert_scatter_index(dev, _abi.I64, 1 << 31, 4, dev, dev, ws, None)
+    assert rc == _abi.ERANGE
+
+
 def test_check_raises_with_library_message():
     lib = _abi.lib()
     rc = lib.fmoe_build_metadata(None, None, 0, None, None, None, None, None)

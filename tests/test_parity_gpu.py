@@ -443,6 +443,43 @@ def test_plan_matches_oracle(T):
     assert lib.fmoe_plan_workspace_bytes(N, T) == plan.numel()
 
 
+@pytest.mark.parametrize("case", ["topk", "long", "one_token", "invalid_i32", "empty", "bigT"])
+def test_invert_scatter_index_matches_oracle(case):
+    """fmoe_invert_scatter_index: row_ptr and the row list equal the oracle's stable inverse
+    exactly -- top-k routing, segments longer than 64 rows (one of 3000 rows), out-of-range int32
+    indices, no rows, and T above the LDS histogram (the global count path)."""
+    from oracle import cref
+
+    gen = torch.Generator().manual_seed(21)
+    if case == "topk":
+        _, T, idx, _, _ = _inputs("gigachat")
+    elif case == "long":
+        T = 40
+        idx = torch.cat([torch.randint(0, 3, (300,), generator=gen),
+                         torch.randint(0, T, (200,), generator=gen)])
+        idx = idx[torch.randperm(idx.numel(), generator=gen)]
+    elif case == "one_token":
+        T, idx = 8, torch.randint(0, 2, (3000,), generator=gen)
+    elif case == "invalid_i32":
+        T = 64
+        idx = torch.randint(0, T, (1000,), generator=gen)
+        idx[::37] = -1
+        idx[5::41] = T
+        idx = idx.to(torch.int32)
+    elif case == "empty":
+        T, idx = 16, torch.zeros(0, dtype=torch.int64)
+    else:
+        T, idx = 40000, torch.randint(0, 40000, (80000,), generator=gen)
+    row_ptr, rows = fastmoe_amd.invert_scatter_index(idx.to(DEV), T)
+    want_rp, want_rows = cref.plan(idx.to(torch.int64).numpy(), T)
+    np.testing.assert_array_equal(row_ptr.cpu().numpy(), want_rp)
+    np.testing.assert_array_equal(rows.cpu().numpy(), want_rows)
+    if case == "long":
+        assert np.diff(want_rp)[:T].max() > 64
+    if case == "invalid_i32":
+        assert want_rp[T + 1] - want_rp[T] > 0
+
+
 def test_metadata_matches_closed_forms():
     gen = torch.Generator().manual_seed(8)
     for E in (1, 7, 256, 300, 600):
