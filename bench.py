@@ -200,6 +200,62 @@ def _standard_moe_step(wl, x, ids, gates):
     return std_step, "torch GPU argsort -> x[rev] -> bincount -> * w -> index_add_, eager"
 
 
+def _verify_combine(wl, xs, idx, w, mode):
+    """The reference harness's correctness check (run_on_cloud.py:13-32): the in-place fast path
+    into fp32 zeros against cat -> * w -> index_add_ into fp32 zeros, both on the GPU, max |diff|
+    against its 1e-4 tolerance."""
+    import torch
+
+    import fastmoe_amd
+
+    with torch.no_grad():
+        weighted = torch.cat(xs, dim=0) * w.unsqueeze(-1)
+        out_std = torch.zeros((wl.T, wl.D), device=idx.device).index_add_(0, idx, weighted)
+        del weighted
+        out_fast = torch.zeros((wl.T, wl.D), device=idx.device)
+        fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (wl.T, wl.D), out=out_fast, mode=mode)
+        diff = (out_std - out_fast).abs().max().item()
+    return {"max_abs_diff": diff, "tol": 1e-4, "passed": diff <= 1e-4,
+            "against": "torch GPU cat -> * w -> index_add_ into fp32 zeros (run_on_cloud.py:13-32)"}
+
+
+def _verify_dispatch(wl, x, ids, gates):
+    """The permutation against the reference's torch sequence (tiny_model.py:108-138) with a
+    stable argsort: reverse map, sorted gates and gathered rows must be equal exactly."""
+    import torch
+
+    import fastmoe_amd
+
+    with torch.no_grad():
+        p = fastmoe_amd.permute_tokens(x, ids, gates, wl.E)
+        order = torch.argsort(ids.view(-1), stable=True)
+        rev = torch.arange(wl.T, device=x.device).repeat_interleave(wl.k)[order]
+        same = (torch.equal(p.reverse_map_indices, rev)
+                and torch.equal(p.sorted_weights, gates.view(-1)[order]))
+        diff = (p.permuted_data.float() - x[rev].float()).abs().max().item()
+    return {"max_abs_diff": diff, "tol": 0.0, "passed": same and diff == 0.0,
+            "against": "torch GPU stable argsort -> reverse map -> x[rev] (tiny_model.py:108-138)"}
+
+
+def _verify_moe(wl, x, ids, gates, out):
+    """The layer's combine against an fp32 torch sum of the same permuted products: the output
+    is that sum rounded once, so within one ulp of the output dtype (2^-7 relative in bf16)."""
+    import torch
+
+    with torch.no_grad():
+        order = torch.argsort(ids.view(-1), stable=True)
+        rev = torch.arange(wl.T, device=x.device).repeat_interleave(wl.k)[order]
+        sw = gates.view(-1)[order].type_as(x)
+        ref = torch.zeros(wl.T, wl.D, device=x.device).index_add_(
+            0, rev, x[rev].float() * sw.float().unsqueeze(-1))
+        err = (out.float().view(wl.T, wl.D) - ref).abs()
+        rel = 2.0 ** -7 if out.dtype == torch.bfloat16 else 2.0 ** -10 if out.dtype == torch.float16 else 1e-6
+        ok = bool((err <= ref.abs() * rel + 1e-30).all())
+        diff = err.max().item()
+    return {"max_abs_diff": diff, "tol": f"{rel:g} * |ref| elementwise", "passed": ok,
+            "against": "fp32 torch index_add_ of the stably permuted products (tiny_model.py:396-403)"}
+
+
 def _cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -296,6 +352,7 @@ def main() -> int:
                 return out
 
         std = lambda: _standard_combine_step(wl, xs, idx, w, grad_out, backward)  # noqa: E731
+        verify = lambda: _verify_combine(wl, xs, idx, w, args.mode)  # noqa: E731
     elif args.path == "moe":
         metric = ("MoE layer data movement GB/s & % HBM peak (permutation + grouped combine, "
                   "identity experts, forward)")
@@ -304,6 +361,7 @@ def main() -> int:
         ids, gates = ids.to(dev), gates.to(dev)
         x = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
                         generator=gen_dev.manual_seed(3)).to(wl.dtype)
+        gates = gates.type_as(x)  # the layer's gates are in the activation dtype (tiny_model.py:100)
         pf, _ = dispatch_bytes(wl.T, wl.D, wl.N, xb)
         cf, _ = algorithmic_bytes(wl.T, wl.D, wl.N, xb, xb)
         fwd_b, bwd_b = pf + cf, 0
@@ -321,6 +379,7 @@ def main() -> int:
                                              (1, wl.T), permutation=p if use_slots else None)
 
         std = lambda: _standard_moe_step(wl, x, ids, gates)  # noqa: E731
+        verify = lambda: _verify_moe(wl, x, ids, gates, step())  # noqa: E731
     else:
         metric = ("dispatch permutation fwd+bwd GB/s & % HBM peak (gate_and_sort sort + gather, "
                   "its backward)")
@@ -345,6 +404,7 @@ def main() -> int:
 
         std = lambda: _standard_dispatch_step(wl, x, ids, gates, g_rows, g_sw,  # noqa: E731
                                               backward)
+        verify = lambda: _verify_dispatch(wl, x, ids, gates)  # noqa: E731
     step_bytes = fwd_b + (bwd_b if backward else 0)
 
     if args.copy_probe:
@@ -496,6 +556,7 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_standard:
+        res["verify"] = verify()
         std_step, what = std()
         res["standard"] = _time_standard(std_step, args.steps, args.warmup, ms, what)
         res["peak_mem_gb"] = round(fast_peak / 2 ** 30, 3)
