@@ -10,7 +10,13 @@
 //                     rows is unordered (consumers that need the order rank it in registers),
 //                     a longer one is in ascending g
 //
-// Steps (all on the caller's stream, no host synchronisation):
+// Built in one launch when T + 1 <= 256 * 4096, N <= 2^20 and E <= 4096 (k_plan_tok): P
+// workgroups each own a contiguous range of token bins, stream all of idx (from L2 after the
+// first), count the rows below their range and the rows of each of their own bins, scan their bins
+// and fill their rows' records; a segment longer than 64 rows is then ordered by g by the
+// workgroup that owns it.  No workgroup waits for another and nothing needs zero-filled memory.
+//
+// Otherwise three steps (all on the caller's stream, no host synchronisation):
 //   1. count + scan   one 1024-thread workgroup histograms idx into LDS (T + 1 <= kLdsTokens) and
 //                     scans it; larger T fall back to zero / global-atomic count / one-block scan.
 //   2. fill           one thread per row: claims a slot in its segment with an atomic cursor and
@@ -18,11 +24,11 @@
 //   3. order          segments longer than 64 rows only (never for top-k routing; the kernel
 //                     exits at once otherwise): one wave per segment ranks its records by g and
 //                     writes them in order.
-//                     Shorter segments are ordered by the consumer in registers, so every result
-//                     is bit-identical run to run even though the fill order is not.
+// Segments of up to 64 rows are ordered by the consumers in registers, so every result is
+// bit-identical run to run even though the fill order is not.
 //
-// fmoe_invert_scatter_index runs the same count + scan, then writes bare row numbers (ascending
-// in every segment) instead of records.
+// fmoe_invert_scatter_index runs the three-step count + scan, then writes bare row numbers
+// (ascending in every segment) instead of records.
 #include <algorithm>
 
 #include "common.h"
@@ -264,6 +270,267 @@ __global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __rest
   }
 }
 
+// ---- one-launch plan: token-sliced count + scan + fill (+ ordering of long segments) --------
+// P workgroups; workgroup s owns the token bins [s * bins, (s + 1) * bins) of the T + 1 (bin T:
+// out-of-range rows), so every segment belongs to exactly one workgroup and the workgroups never
+// communicate.  Each streams all of idx (from L2 after the first) and
+//   * counts the rows whose bin lies below its range (a register sum: row_ptr of its first bin),
+//   * counts its own bins' rows with LDS atomics and stashes those rows' (g, bin) in LDS,
+// scans its bins into row_ptr and the fill cursors, and writes one record per stashed row.  A
+// wave whose stash region overflows (a heavily skewed index) makes the workgroup fill from a
+// second pass over idx instead.  Within a segment the slot order is arbitrary; a segment longer
+// than 64 rows is then ordered by g by the workgroup that owns it.
+constexpr int kTokBins = 4096;                         // bins per workgroup at most
+constexpr int kTokWaves = kScanThreads / kWave;        // 16
+constexpr int kTokStash = 8192;                        // stashed rows per workgroup
+constexpr int kTokWaveStash = kTokStash / kTokWaves;   // 512 per wave
+constexpr int kTokRows = 2048;                         // rows per workgroup aimed at
+constexpr int kTokGroups = 256;
+constexpr int kTokExperts = 4096;                      // int32 expert offsets staged in LDS
+constexpr int64_t kTokMaxRows = int64_t(1) << 20;      // every workgroup streams all of idx
+constexpr int32_t kLongBit = 1 << 30;                  // cursor flag: segment longer than 64 rows
+
+__device__ __forceinline__ int expert_of_row32(const int* __restrict__ off, int E, int g) {
+  int lo = 0, hi = E;  // invariant: off[lo] <= g < off[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (off[mid] <= g) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// Record of row g for the slot `v` (cursor value: slot | long flag); gate already loaded.
+__device__ __forceinline__ void tok_write_rec(int v, int g, float wg, const int* __restrict__ off32,
+                                              const uint64_t* __restrict__ ptr_lds, int ne,
+                                              int64_t row_bytes, Rec* __restrict__ rec_tmp,
+                                              Rec* __restrict__ rec) {
+  const int e = expert_of_row32(off32, ne, g);
+  Rec r;
+  r.src = ptr_lds[e] + (uint64_t)((int64_t)(g - off32[e]) * row_bytes);
+  r.w = wg;
+  r.g = g;
+  ((v & kLongBit) ? rec_tmp : rec)[v & (kLongBit - 1)] = r;
+}
+
+// Index vector of one 16-byte load: 2 int64 or 4 int32 scatter indices.
+template <typename TI> struct IdxVec {
+  static constexpr int kCount = 16 / (int)sizeof(TI);
+  static __device__ __forceinline__ int64_t get(const u32x4& v, int q) {
+    if constexpr (sizeof(TI) == 8)
+      return (int64_t)((uint64_t)v[2 * q] | ((uint64_t)v[2 * q + 1] << 32));
+    else
+      return (int64_t)(int32_t)v[q];
+  }
+};
+
+template <typename TI, typename TW>
+__global__ __launch_bounds__(kScanThreads) void k_plan_tok(
+    const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T, int bins,
+    const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
+    int64_t row_bytes, int32_t* __restrict__ row_ptr, Rec* __restrict__ rec_tmp,
+    Rec* __restrict__ rec, int32_t* __restrict__ status) {
+  using IV = IdxVec<TI>;
+  constexpr int kQ = IV::kCount;
+  __shared__ int cnt[kTokBins];         // rows per bin, then the fill cursors
+  __shared__ int2 stash[kTokStash];     // (g, local bin) of this range's rows; later the long list
+  __shared__ int off32[kTokExperts + 1];
+  __shared__ uint64_t ptr_lds[kTokExperts];
+  __shared__ int red[3][kTokWaves];
+  __shared__ int overflow, misaligned, n_long;
+  const int nb = (int)T + 1;
+  const int ne = (int)E;
+  const int lo = (int)blockIdx.x * bins;  // the host makes every range non-empty
+  const int hi = min(nb, lo + bins);
+  const int nloc = hi - lo;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int i = threadIdx.x; i < nloc; i += kScanThreads) cnt[i] = 0;
+  for (int i = threadIdx.x; i <= ne; i += kScanThreads) {
+    off32[i] = (int)offsets[i];
+    if (i < ne) ptr_lds[i] = (uint64_t)ptr_table[i];
+  }
+  if (threadIdx.x == 0) {
+    overflow = 0;
+    misaligned = 0;
+    n_long = 0;
+  }
+  __syncthreads();
+
+  // 1. one pass over idx, 16 bytes per lane per load, software-pipelined: the loads of the next
+  //    batch are in flight while this one is counted.  Only whole vectors are loaded (a vector
+  //    past the end gets the offset of the end, which the range check turns into zeros); the
+  //    N % kQ rows after the last whole vector are loaded one by one by wave 0.
+  const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));
+  int2* wstash = stash + wave * kTokWaveStash;
+  int below = 0;   // rows whose bin precedes this range
+  int wcount = 0;  // rows of this range seen by this wave (wave-uniform)
+  const int n32 = (int)N;
+  const int nfull = n32 - n32 % kQ;
+  const uint32_t end_off = (uint32_t)n32 * (uint32_t)sizeof(TI);
+  auto count_row = [&](bool valid, int g, int64_t t) {
+    // (unsigned) t < T covers 0 <= t < T; nb marks rows that are not counted here
+    const int b = valid ? ((uint64_t)t < (uint64_t)T ? (int)t : (int)T) : nb;
+    below += b < lo ? 1 : 0;
+    const bool in = b >= lo && b < hi;
+    const uint64_t m = __ballot(in);
+    if (in) {
+      atomicAdd(&cnt[b - lo], 1);
+      const int slot = wcount + (int)__builtin_amdgcn_mbcnt_hi(
+                                    (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      if (slot < kTokWaveStash) wstash[slot] = make_int2(g, b - lo);
+    }
+    wcount += __popcll(m);
+  };
+  constexpr int kLoads = 8 / kQ;  // 8 rows per thread per batch
+  constexpr int kStep = kScanThreads * kQ;
+  constexpr int kBatchRows = kStep * kLoads;
+  auto load_batch = [&](int base, u32x4* v) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int g0 = base + i * kStep + (int)threadIdx.x * kQ;
+      v[i] = Raw<16>::ld<kCPolCached>(ri, g0 < nfull ? (uint32_t)g0 * (uint32_t)sizeof(TI) : end_off);
+    }
+  };
+  u32x4 cur[kLoads], nxt[kLoads];
+  load_batch(0, cur);
+  for (int base = 0; base < nfull; base += kBatchRows) {
+    load_batch(base + kBatchRows, nxt);  // past the end: zeros, no memory traffic
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) {
+        const int g = base + i * kStep + (int)threadIdx.x * kQ + q;
+        count_row(g < nfull, g, IV::get(cur[i], q));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) cur[i] = nxt[i];
+  }
+  if (nfull < n32 && wave == 0) {  // wave-uniform
+    const int g = nfull + lane;
+    const bool valid = g < n32;
+    int64_t t = 0;
+    if (valid) t = (int64_t)__builtin_bit_cast(
+        TI, Raw<sizeof(TI)>::template ld<kCPolCached>(ri, (uint32_t)g * (uint32_t)sizeof(TI)));
+    count_row(valid, g, t);
+  }
+  if (lane == 0 && wcount > kTokWaveStash) overflow = 1;
+  if (blockIdx.x == 0) {
+    // a source row is misaligned iff its expert's base is, or the expert has two or more rows
+    // and the row length is not a multiple of 16 bytes
+    int mis = 0;
+    for (int e = threadIdx.x; e < ne; e += kScanThreads) {
+      const int n = off32[e + 1] - off32[e];
+      if (n > 0 && ((ptr_lds[e] & 15) || (n > 1 && (row_bytes & 15)))) mis = 1;
+    }
+    if (mis) misaligned = 1;
+  }
+  __syncthreads();
+
+  // 2. scan of this range's bins (at most 4 per thread), the rows below it and the longest
+  //    segment, in one barrier round
+  constexpr int kPer = kTokBins / kScanThreads;
+  const int per = (nloc + kScanThreads - 1) / kScanThreads;
+  const int b0 = min(nloc, (int)threadIdx.x * per);
+  const int b1 = min(nloc, b0 + per);
+  int c[kPer];
+  int local = 0, longest = 0;
+#pragma unroll
+  for (int p = 0; p < kPer; ++p) {
+    c[p] = b0 + p < b1 ? cnt[b0 + p] : 0;
+    local += c[p];
+    if (lo + b0 + p < nb - 1) longest = max(longest, c[p]);  // token bins only
+  }
+  int incl = local;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) {
+    below += __shfl_xor(below, d, kWave);
+    longest = max(longest, __shfl_xor(longest, d, kWave));
+  }
+  if (lane == kWave - 1) {
+    red[0][wave] = incl;
+    red[1][wave] = below;
+    red[2][wave] = longest;
+  }
+  __syncthreads();  // also: every count read above precedes the cursor writes below
+  int run = incl - local, range_rows = 0, rows_below = 0;
+#pragma unroll
+  for (int i = 0; i < kTokWaves; ++i) {
+    run += i < wave ? red[0][i] : 0;
+    range_rows += red[0][i];
+    rows_below += red[1][i];
+    longest = max(longest, red[2][i]);
+  }
+  int first[kPer];
+#pragma unroll
+  for (int p = 0; p < kPer; ++p) {
+    const int lb = b0 + p;
+    first[p] = rows_below + run;
+    if (lb < b1) {
+      const bool tok = lo + lb < nb - 1;  // a token bin (not the out-of-range bin T)
+      row_ptr[lo + lb] = first[p];
+      cnt[lb] = first[p] | ((tok && c[p] > kWave) ? kLongBit : 0);
+      if (!tok) status[kStatusInvalid] = c[p];
+    }
+    run += c[p];
+  }
+  if (hi == nb && threadIdx.x == 0) row_ptr[nb] = rows_below + range_rows;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    status[kStatusMisaligned] = misaligned;
+    status[kStatusLongest] = -1;  // not recorded: no workgroup sees every segment
+  }
+  __syncthreads();  // the cursors
+
+  // 3. fill: each wave its own stashed rows, two at a time; or all rows from a second pass
+  if (!overflow) {
+    const int n = wcount;  // <= kTokWaveStash here
+    for (int j = lane; j < n; j += 2 * kWave) {
+      const bool two = j + kWave < n;
+      const int2 a = wstash[j];
+      const int2 bb = two ? wstash[j + kWave] : a;
+      const float wa = ld1(w + a.x);
+      const float wb = ld1(w + bb.x);
+      const int va = atomicAdd(&cnt[a.y], 1);
+      const int vb = two ? atomicAdd(&cnt[bb.y], 1) : 0;
+      tok_write_rec(va, a.x, wa, off32, ptr_lds, ne, row_bytes, rec_tmp, rec);
+      if (two) tok_write_rec(vb, bb.x, wb, off32, ptr_lds, ne, row_bytes, rec_tmp, rec);
+    }
+  } else {
+    for (int64_t g = threadIdx.x; g < N; g += kScanThreads) {
+      const int64_t t = (int64_t)idx[g];
+      const int b = (t >= 0 && t < T) ? (int)t : (int)T;
+      if (b >= lo && b < hi)
+        tok_write_rec(atomicAdd(&cnt[b - lo], 1), (int)g, ld1(w + g), off32, ptr_lds, ne,
+                      row_bytes, rec_tmp, rec);
+    }
+  }
+  if (longest <= kWave) return;  // workgroup-uniform
+
+  // 4. order the segments longer than 64 rows (non-top-k routing only), one wave per segment
+  __syncthreads();  // the fill's records are visible to the workgroup; the stash is free
+  int2* list = stash;  // at most nloc <= kTokStash entries
+#pragma unroll
+  for (int p = 0; p < kPer; ++p)
+    if (b0 + p < b1 && lo + b0 + p < nb - 1 && c[p] > kWave)
+      list[atomicAdd(&n_long, 1)] = make_int2(first[p], c[p]);
+  __syncthreads();
+  const int nl = n_long;
+  for (int i = wave; i < nl; i += kTokWaves) {
+    const int beg = list[i].x, cn = list[i].y;
+    for (int j = lane; j < cn; j += kWave) {
+      const Rec r = rec_tmp[beg + j];
+      int rank = 0;
+      for (int m = 0; m < cn; ++m) rank += (rec_tmp[beg + m].g < r.g) ? 1 : 0;
+      rec[beg + rank] = r;
+    }
+  }
+}
+
 // ---- the bare CSR inverse (fmoe_invert_scatter_index) ---------------------------------------
 // Same count + scan as the plan.  The fill writes bare row numbers; then one wave per segment
 // writes its rows in ascending order.  Row numbers are distinct, so a row's place in its segment
@@ -428,6 +695,30 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
   Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
+
+  // One token-sliced launch when its limits hold; otherwise count + scan, fill and order as
+  // three launches.  FMOE_PLAN_SPLIT=1 forces the latter (tests compare the two).
+  const int64_t nb = T + 1;
+  int64_t groups = std::max<int64_t>((N + kTokRows - 1) / kTokRows, (nb + kTokBins - 1) / kTokBins);
+  groups = std::min<int64_t>(std::min<int64_t>(groups, kTokGroups), nb);
+  const int64_t bins = (nb + groups - 1) / groups;
+  groups = (nb + bins - 1) / bins;  // every workgroup gets a non-empty bin range
+  const char* split_env = getenv("FMOE_PLAN_SPLIT");
+  if (!(split_env && *split_env && atoi(split_env) != 0) && E <= kTokExperts &&
+      N <= kTokMaxRows && bins <= kTokBins) {
+#define FMOE_TOK(TI, TW)                                                                           \
+  hipLaunchKernelGGL((k_plan_tok<TI, TW>), dim3((unsigned)groups), dim3(kScanThreads), 0, s,       \
+                     static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
+                     (int)bins, d_ptr_table, d_offsets, E, row_bytes, row_ptr, rec_tmp, rec, status)
+#define FMOE_TOK_W(TI)                                           \
+  if (w_dtype == FMOE_F32) FMOE_TOK(TI, float);                  \
+  else if (w_dtype == FMOE_BF16) FMOE_TOK(TI, bf16_t);           \
+  else FMOE_TOK(TI, f16_t)
+    if (idx_dtype == FMOE_I64) { FMOE_TOK_W(int64_t); } else { FMOE_TOK_W(int32_t); }
+#undef FMOE_TOK_W
+#undef FMOE_TOK
+    return fmoe_host::check_launch("fmoe_build_plan(one launch)");
+  }
 
   if (int rc = launch_count_scan(d_indices, idx_dtype, N, T, cursor, row_ptr, status, s,
                                  "fmoe_build_plan"))

@@ -396,18 +396,42 @@ def test_dtype_combinations(xdt, wdt, idt, odt):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
-@pytest.mark.parametrize("T", [512, 40])
-def test_plan_matches_oracle(T):
+def _plan_case(case: str):
+    """(T, idx, w, experts, D) of a plan test case.  The fused plan gives each workgroup a slice
+    of 2048 rows (fewer groups than rows / 2048 only above 256 groups), so N decides how many
+    workgroups split a segment; N >= 65536 selects its 64-bit histogram."""
+    gen = torch.Generator().manual_seed(17)
+    if case in ("topk512", "long40"):
+        wl, T, idx, w, experts = _inputs("skewed", T=512 if case == "topk512" else 40)
+        if case == "long40":  # pile 200 extra rows onto tokens 0..2 through one more expert
+            experts = experts + [torch.randn(200, wl.D, generator=gen).to(wl.dtype)]
+            idx = torch.cat([idx, torch.randint(0, 3, (200,), generator=gen)])
+            w = torch.cat([w, torch.rand(200, generator=gen)])
+        return T, idx, w, experts, wl.D
+    # randint routing over ragged experts of 8 fp32 columns
+    T, N, hot = {"long_pieces_short": (50, 4096, 50),   # 2 groups, ~41-row pieces of 82-row segments
+                 "long_pieces_long": (40, 10000, 3),    # 5 groups, pieces of ~650 rows
+                 "wide_hist": (512, 70000, 512)}[case]  # 35 groups, 64-bit histogram words
+    idx = torch.randint(0, hot, (N,), generator=gen)
+    cuts = torch.sort(torch.randint(0, N + 1, (23,), generator=gen)).values.tolist()
+    sizes = [b - a for a, b in zip([0] + cuts, cuts + [N])]
+    experts = [torch.randn(n, 8, generator=gen) for n in sizes]
+    return T, idx, torch.rand(N, generator=gen), experts, 8
+
+
+@pytest.mark.parametrize("path", ["fused", "split"])
+@pytest.mark.parametrize("case", ["topk512", "long40", "long_pieces_short", "long_pieces_long",
+                                  "wide_hist"])
+def test_plan_matches_oracle(case, path, monkeypatch):
     """row_ptr, the records (source address, gate bits, g) and the status words equal the
-    oracle's inverse.  At T=40, 200 extra rows on tokens 0..2 make segments longer than 64."""
+    oracle's inverse, for the one-launch fused plan and the split count/fill/order plan.  Segments
+    longer than 64 rows must come out in ascending g, including when several workgroups each fill
+    a piece of one segment."""
     from oracle import cref
 
-    wl, T, idx, w, experts = _inputs("skewed", T=T)
-    if T == 40:  # pile 200 extra rows onto tokens 0..2 through one more expert
-        gen = torch.Generator().manual_seed(3)
-        experts = experts + [torch.randn(200, wl.D, generator=gen).to(wl.dtype)]
-        idx = torch.cat([idx, torch.randint(0, 3, (200,), generator=gen)])
-        w = torch.cat([w, torch.rand(200, generator=gen)])
+    if path == "split":
+        monkeypatch.setenv("FMOE_PLAN_SPLIT", "1")
+    T, idx, w, experts, D = _plan_case(case)
     xd, idd, wd = _to_dev(experts, idx, w)
     meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
     plan = fastmoe_amd.build_plan(meta, idd, wd, T)
@@ -425,9 +449,13 @@ def test_plan_matches_oracle(T):
         if seg_len[b] > 64:
             assert np.all(np.diff(g[want_rp[b]:want_rp[b + 1]]) > 0), b
     st = ops.plan_status(plan).cpu().numpy()
-    assert st[0] == 0 and st[1] == 0 and st[2] == seg_len[:T].max()
-    if T == 40:
-        assert st[2] > 64
+    misaligned = int((D * experts[0].element_size()) % 16 != 0)
+    # the longest segment is recorded by the split plan only (no workgroup of the one-launch plan
+    # sees every segment)
+    assert st[0] == 0 and st[1] == misaligned
+    assert st[2] == (seg_len[:T].max() if path == "split" else -1)
+    if case != "topk512":
+        assert seg_len[:T].max() > 64
     # short segments may be unordered: order each segment by g before comparing
     order = np.concatenate([np.arange(want_rp[b], want_rp[b + 1])[np.argsort(g[want_rp[b]:want_rp[b + 1]])]
                             for b in range(T + 1)])
@@ -438,9 +466,14 @@ def test_plan_matches_oracle(T):
     np.testing.assert_array_equal(wbits, w.numpy()[want_g].view(np.uint32))
     off, _ = cref.metadata(meta.sizes)
     e_of = np.searchsorted(off, want_g, side="right") - 1
-    src = np.array([meta.ptrs[e] for e in e_of], dtype=np.int64) + (want_g - off[e_of]) * wl.D * 2
+    src = (np.array([meta.ptrs[e] for e in e_of], dtype=np.int64)
+           + (want_g - off[e_of]) * D * experts[0].element_size())
     np.testing.assert_array_equal(rec[:, 0].numpy(), src)
     assert lib.fmoe_plan_workspace_bytes(N, T) == plan.numel()
+    # and the forward that reads this plan is bit-exact
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), mode="det")
+    want, _, _ = oracle_fwd(experts, idx, w, T, experts[0].dtype)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
 @pytest.mark.parametrize("case", ["topk", "long", "one_token", "invalid_i32", "empty", "bigT"])
