@@ -286,6 +286,20 @@ __device__ __forceinline__ typename Vec<TX, V>::raw_t load_x(rsrc_t r, uint32_t 
   }
 }
 
+// The (address, rows) table of up to 256 expert buffers as a kernel argument: the metadata kernel
+// and the one-launch metadata + plan kernel read it straight from their arguments, so building
+// the metadata needs no host staging buffer and no copy.
+constexpr int kMetaChunk = 256;  // experts per launch: 256*8 + 256*4 + 16 bytes of arguments
+struct MetaChunk {
+  int64_t ptr[kMetaChunk];
+  int32_t rows[kMetaChunk];
+  int32_t count;  // experts in this chunk
+  int32_t base;   // index of the first expert of this chunk
+  int32_t scan;   // 1: this launch also scans (only when the whole table fits one chunk)
+  int32_t pad;
+};
+static_assert(sizeof(MetaChunk) <= 3200, "kernel-argument table too large");
+
 // Plan status words (int32, at the start of the plan workspace).
 constexpr int kStatusInvalid = 0;    // rows whose scatter index is outside [0, T)
 constexpr int kStatusMisaligned = 1; // nonzero if any source row is not 16-byte aligned

@@ -9,18 +9,6 @@
 
 namespace fmoe {
 
-constexpr int kMetaChunk = 256;  // experts per launch: 256*8 + 256*4 + 16 bytes of arguments
-
-struct MetaChunk {
-  int64_t ptr[kMetaChunk];
-  int32_t rows[kMetaChunk];
-  int32_t count;  // experts in this chunk
-  int32_t base;   // index of the first expert of this chunk
-  int32_t scan;   // 1: this launch also scans (only when the whole table fits one chunk)
-  int32_t pad;
-};
-static_assert(sizeof(MetaChunk) <= 3200, "kernel-argument table too large");
-
 // Block-wide exclusive scan of one int64 per thread (256 threads); returns the total.
 __device__ int64_t block_exclusive_scan_256(int64_t v, int64_t* out_excl) {
   __shared__ int64_t wave_tot[kWavesPerGroup];

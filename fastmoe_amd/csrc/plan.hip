@@ -312,6 +312,53 @@ __device__ __forceinline__ void tok_write_rec(int v, int g, float wg, const int*
   ((v & kLongBit) ? rec_tmp : rec)[v & (kLongBit - 1)] = r;
 }
 
+// Where the one-launch plan gets the expert table from.  TokMetaGlobal: the device arrays of
+// fmoe_build_metadata.  TokMetaArgs: the (address, rows) pairs in the kernel arguments (at most 256
+// experts); every workgroup scans the row counts itself and workgroup 0 also writes the
+// metadata outputs, so metadata and plan take one launch.
+struct TokMetaGlobal {
+  const int64_t* ptr_table;
+  const int64_t* offsets;
+};
+struct TokMetaArgs {
+  MetaChunk a;  // a.count experts from a.base = 0
+  int64_t* ptr_table;
+  int32_t* chunk_sizes;
+  int64_t* offsets;
+  int32_t* max_rows;
+};
+
+__device__ __forceinline__ void tok_load_meta(const TokMetaGlobal& m, int ne, int* off32,
+                                              uint64_t* ptr_lds) {
+  for (int i = threadIdx.x; i <= ne; i += kScanThreads) {
+    off32[i] = (int)m.offsets[i];
+    if (i < ne) ptr_lds[i] = (uint64_t)m.ptr_table[i];
+  }
+}
+__device__ __forceinline__ void tok_load_meta(const TokMetaArgs& m, int ne, int* off32,
+                                              uint64_t* ptr_lds) {
+  const int e = threadIdx.x;  // ne <= 256 < kScanThreads: one expert per thread
+  const int rows = e < ne ? m.a.rows[e] : 0;
+  const int64_t ptr = e < ne ? m.a.ptr[e] : 0;
+  int total;
+  const int excl = block_exclusive_scan_1024(rows, &total);
+  if (e < ne) {
+    off32[e] = excl;
+    ptr_lds[e] = (uint64_t)ptr;
+  }
+  if (e == 0) off32[ne] = total;
+  if (blockIdx.x == 0) {  // workgroup-uniform: the metadata outputs (fmoe_build_metadata's)
+    if (e < ne) {
+      m.ptr_table[e] = ptr;
+      m.chunk_sizes[e] = rows;
+      m.offsets[e] = excl;
+    }
+    if (e == 0) m.offsets[ne] = total;
+    const int mx = block_max_1024(rows);
+    if (e == 0) *m.max_rows = mx;
+  }
+}
+
 // Index vector of one 16-byte load: 2 int64 or 4 int32 scatter indices.
 template <typename TI> struct IdxVec {
   static constexpr int kCount = 16 / (int)sizeof(TI);
@@ -323,12 +370,11 @@ template <typename TI> struct IdxVec {
   }
 };
 
-template <typename TI, typename TW>
+template <typename TI, typename TW, typename Meta>
 __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T, int bins,
-    const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
-    int64_t row_bytes, int32_t* __restrict__ row_ptr, Rec* __restrict__ rec_tmp,
-    Rec* __restrict__ rec, int32_t* __restrict__ status) {
+    const Meta meta, int64_t E, int64_t row_bytes, int32_t* __restrict__ row_ptr,
+    Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, int32_t* __restrict__ status) {
   using IV = IdxVec<TI>;
   constexpr int kQ = IV::kCount;
   __shared__ int cnt[kTokBins];         // rows per bin, then the fill cursors
@@ -345,10 +391,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   for (int i = threadIdx.x; i < nloc; i += kScanThreads) cnt[i] = 0;
-  for (int i = threadIdx.x; i <= ne; i += kScanThreads) {
-    off32[i] = (int)offsets[i];
-    if (i < ne) ptr_lds[i] = (uint64_t)ptr_table[i];
-  }
+  tok_load_meta(meta, ne, off32, ptr_lds);
   if (threadIdx.x == 0) {
     overflow = 0;
     misaligned = 0;
@@ -650,6 +693,41 @@ int launch_count_scan(const void* d_indices, int idx_dtype, int64_t N, int64_t T
   return fmoe_host::check_launch(who);
 }
 
+// Grid of the one-launch plan, or false when its limits do not hold (or FMOE_PLAN_SPLIT=1).
+bool tok_grid(int64_t N, int64_t T, int64_t E, int64_t* groups_out, int64_t* bins_out) {
+  using namespace fmoe;
+  const char* split_env = getenv("FMOE_PLAN_SPLIT");
+  if (split_env && *split_env && atoi(split_env) != 0) return false;
+  const int64_t nb = T + 1;
+  int64_t groups = std::max<int64_t>((N + kTokRows - 1) / kTokRows, (nb + kTokBins - 1) / kTokBins);
+  groups = std::min<int64_t>(std::min<int64_t>(groups, kTokGroups), nb);
+  const int64_t bins = (nb + groups - 1) / groups;
+  groups = (nb + bins - 1) / bins;  // every workgroup gets a non-empty bin range
+  *groups_out = groups;
+  *bins_out = bins;
+  return E <= kTokExperts && N <= kTokMaxRows && bins <= kTokBins;
+}
+
+template <typename Meta>
+int launch_plan_tok(const Meta& meta, const void* d_indices, int idx_dtype, const void* d_weights,
+                    int w_dtype, int64_t N, int64_t T, int64_t E, int64_t row_bytes,
+                    int64_t groups, int64_t bins, int32_t* row_ptr, fmoe::Rec* rec_tmp,
+                    fmoe::Rec* rec, int32_t* status, hipStream_t s) {
+  using namespace fmoe;
+#define FMOE_TOK(TI, TW)                                                                           \
+  hipLaunchKernelGGL((k_plan_tok<TI, TW, Meta>), dim3((unsigned)groups), dim3(kScanThreads), 0, s, \
+                     static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
+                     (int)bins, meta, E, row_bytes, row_ptr, rec_tmp, rec, status)
+#define FMOE_TOK_W(TI)                                 \
+  if (w_dtype == FMOE_F32) FMOE_TOK(TI, float);        \
+  else if (w_dtype == FMOE_BF16) FMOE_TOK(TI, bf16_t); \
+  else FMOE_TOK(TI, f16_t)
+  if (idx_dtype == FMOE_I64) { FMOE_TOK_W(int64_t); } else { FMOE_TOK_W(int32_t); }
+#undef FMOE_TOK_W
+#undef FMOE_TOK
+  return fmoe_host::check_launch("fmoe_build_plan(one launch)");
+}
+
 }  // namespace
 
 extern "C" int64_t fmoe_plan_workspace_bytes(int64_t num_rows, int64_t num_tokens) {
@@ -698,26 +776,11 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
 
   // One token-sliced launch when its limits hold; otherwise count + scan, fill and order as
   // three launches.  FMOE_PLAN_SPLIT=1 forces the latter (tests compare the two).
-  const int64_t nb = T + 1;
-  int64_t groups = std::max<int64_t>((N + kTokRows - 1) / kTokRows, (nb + kTokBins - 1) / kTokBins);
-  groups = std::min<int64_t>(std::min<int64_t>(groups, kTokGroups), nb);
-  const int64_t bins = (nb + groups - 1) / groups;
-  groups = (nb + bins - 1) / bins;  // every workgroup gets a non-empty bin range
-  const char* split_env = getenv("FMOE_PLAN_SPLIT");
-  if (!(split_env && *split_env && atoi(split_env) != 0) && E <= kTokExperts &&
-      N <= kTokMaxRows && bins <= kTokBins) {
-#define FMOE_TOK(TI, TW)                                                                           \
-  hipLaunchKernelGGL((k_plan_tok<TI, TW>), dim3((unsigned)groups), dim3(kScanThreads), 0, s,       \
-                     static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
-                     (int)bins, d_ptr_table, d_offsets, E, row_bytes, row_ptr, rec_tmp, rec, status)
-#define FMOE_TOK_W(TI)                                           \
-  if (w_dtype == FMOE_F32) FMOE_TOK(TI, float);                  \
-  else if (w_dtype == FMOE_BF16) FMOE_TOK(TI, bf16_t);           \
-  else FMOE_TOK(TI, f16_t)
-    if (idx_dtype == FMOE_I64) { FMOE_TOK_W(int64_t); } else { FMOE_TOK_W(int32_t); }
-#undef FMOE_TOK_W
-#undef FMOE_TOK
-    return fmoe_host::check_launch("fmoe_build_plan(one launch)");
+  int64_t groups, bins;
+  if (tok_grid(N, T, E, &groups, &bins)) {
+    const TokMetaGlobal meta{d_ptr_table, d_offsets};
+    return launch_plan_tok(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
+                           groups, bins, row_ptr, rec_tmp, rec, status, s);
   }
 
   if (int rc = launch_count_scan(d_indices, idx_dtype, N, T, cursor, row_ptr, status, s,
@@ -744,6 +807,74 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   hipLaunchKernelGGL(k_plan_sort_long, dim3((unsigned)sort_groups), dim3(kGroup), 0, s, row_ptr, T,
                      status, rec_tmp, rec);
   return fmoe_host::check_launch("fmoe_build_plan(sort)");
+}
+
+extern "C" int fmoe_build_metadata_and_plan(
+    const int64_t* host_ptrs, const int64_t* host_rows, int64_t num_experts, int64_t* d_ptr_table,
+    int32_t* d_chunk_sizes, int64_t* d_offsets, int32_t* d_max_rows, const void* d_indices,
+    int idx_dtype, const void* d_weights, int w_dtype, int64_t num_tokens, int64_t row_bytes,
+    void* d_workspace, void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  const int64_t E = num_experts, T = num_tokens;
+  FMOE_REQUIRE(E >= 1 && E < (int64_t(1) << 30),
+               "fmoe_build_metadata_and_plan: num_experts must be in [1, 2^30) (got %lld)",
+               (long long)E);
+  FMOE_REQUIRE(host_ptrs && host_rows, "fmoe_build_metadata_and_plan: null host table");
+  int64_t N = 0;
+  for (int64_t e = 0; e < E; ++e) {
+    if (host_rows[e] < 0 || host_rows[e] >= (int64_t(1) << 31)) break;  // reported below
+    N += host_rows[e];
+  }
+  const bool small_table = E <= kMetaChunk;
+  int64_t groups = 0, bins = 0;
+  if (!small_table || T < 1 || T >= (int64_t(1) << 30) || !tok_grid(N, T, E, &groups, &bins)) {
+    // the two calls (each validates its own arguments)
+    if (int rc = fmoe_build_metadata(host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes,
+                                     d_offsets, d_max_rows, stream))
+      return rc;
+    return fmoe_build_plan(d_indices, idx_dtype, d_weights, w_dtype, N, T, d_ptr_table, d_offsets,
+                           E, row_bytes, d_workspace, stream);
+  }
+  // one launch: the checks of fmoe_build_metadata and fmoe_build_plan
+  for (int64_t e = 0; e < E; ++e) {
+    FMOE_REQUIRE(host_rows[e] >= 0 && host_rows[e] < (int64_t(1) << 31),
+                 "fmoe_build_metadata_and_plan: expert %lld has invalid row count %lld",
+                 (long long)e, (long long)host_rows[e]);
+    FMOE_REQUIRE(host_rows[e] == 0 || host_ptrs[e] != 0,
+                 "fmoe_build_metadata_and_plan: expert %lld has rows but a null address",
+                 (long long)e);
+  }
+  FMOE_REQUIRE(d_ptr_table && d_chunk_sizes && d_offsets && d_max_rows && d_workspace,
+               "fmoe_build_metadata_and_plan: null device output");
+  FMOE_REQUIRE(N == 0 || (d_indices && d_weights),
+               "fmoe_build_metadata_and_plan: null indices/weights");
+  FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype),
+               "fmoe_build_metadata_and_plan: bad index dtype %d", idx_dtype);
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_build_metadata_and_plan: bad weight dtype %d",
+               w_dtype);
+  FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
+               "fmoe_build_metadata_and_plan: workspace not 256B-aligned");
+  FMOE_REQUIRE(row_bytes > 0, "fmoe_build_metadata_and_plan: row_bytes must be > 0");
+  TokMetaArgs meta;
+  meta.a.count = (int32_t)E;
+  meta.a.base = 0;
+  meta.a.scan = 1;
+  meta.a.pad = 0;
+  for (int i = 0; i < kMetaChunk; ++i) {
+    meta.a.ptr[i] = i < E ? host_ptrs[i] : 0;
+    meta.a.rows[i] = i < E ? (int32_t)host_rows[i] : 0;
+  }
+  meta.ptr_table = d_ptr_table;
+  meta.chunk_sizes = d_chunk_sizes;
+  meta.offsets = d_offsets;
+  meta.max_rows = d_max_rows;
+  const PlanLayout L = plan_layout(N, T);
+  char* ws = static_cast<char*>(d_workspace);
+  return launch_plan_tok(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
+                         groups, bins, reinterpret_cast<int32_t*>(ws + L.row_ptr),
+                         reinterpret_cast<Rec*>(ws + L.rec_tmp), reinterpret_cast<Rec*>(ws + L.rec),
+                         reinterpret_cast<int32_t*>(ws + L.status), static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num_tokens,

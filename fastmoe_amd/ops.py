@@ -47,6 +47,7 @@ __all__ = [
     "build_plan_from_slots",
     "grouped_weighted_scatter_add",
     "prepare_grouped_metadata",
+    "prepare_metadata_and_plan",
     "weighted_scatter_add",
 ]
 
@@ -179,9 +180,14 @@ def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None
     the device by one kernel launch whose arguments carry the (address, rows) pairs
     (``fmoe_build_metadata``): no host staging buffer and no synchronous copy.
     """
-    dtype, dev, hidden, sizes, ptrs = _check_experts(expert_tensors)
+    checked = _check_experts(expert_tensors)
     if device is not None:
         _require_cuda(_DeviceProbe(device), "device")
+    return _metadata(expert_tensors, checked)
+
+
+def _metadata(expert_tensors, checked) -> GroupedMetadata:
+    dtype, dev, hidden, sizes, ptrs = checked
     lib = _abi.lib()
     E = len(expert_tensors)
     ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
@@ -249,6 +255,49 @@ def build_plan(meta: GroupedMetadata, indices: torch.Tensor, weights: torch.Tens
                 f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})"
             )
     return ws
+
+
+def prepare_metadata_and_plan(expert_tensors: Sequence[torch.Tensor], indices: torch.Tensor,
+                              weights: torch.Tensor, num_tokens: int,
+                              validate: Optional[bool] = None):
+    """``prepare_grouped_metadata`` followed by ``build_plan`` in one C-ABI call
+    (``fmoe_build_metadata_and_plan``: one kernel launch for up to 256 experts); returns
+    ``(metadata, plan)``, each exactly what the two calls return."""
+    return _metadata_and_plan(expert_tensors, _check_experts(expert_tensors), indices, weights,
+                              num_tokens, validate)
+
+
+def _metadata_and_plan(expert_tensors, checked, indices, weights, num_tokens, validate):
+    dtype, dev, hidden, sizes, ptrs = checked
+    lib = _abi.lib()
+    E, N = len(expert_tensors), sum(sizes)
+    idx, w = _routing_args(indices, weights, N, dev)
+    nbytes = lib.fmoe_plan_workspace_bytes(N, num_tokens)
+    if nbytes <= 0:
+        raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
+    ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
+    chunk_sizes = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
+    max_rows_dev = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev), _span("metadata_plan"):
+        rc = lib.fmoe_build_metadata_and_plan(
+            (ctypes.c_int64 * E)(*ptrs), (ctypes.c_int64 * E)(*sizes), E, ptr_table.data_ptr(),
+            chunk_sizes.data_ptr(), offsets.data_ptr(), max_rows_dev.data_ptr(), idx.data_ptr(),
+            _INDEX_CODES[idx.dtype], w.data_ptr(), _FLOAT_CODES[w.dtype], num_tokens,
+            hidden * expert_tensors[0].element_size(), ws.data_ptr(), _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_build_metadata_and_plan")
+    meta = GroupedMetadata(
+        ptr_table, chunk_sizes, offsets, max(sizes), E,
+        max_rows_device=max_rows_dev, tensors=expert_tensors, sizes=sizes, ptrs=ptrs,
+        hidden=hidden, dtype=dtype, device=dev,
+    )
+    if _validate_default(validate):
+        bad = int(plan_status(ws)[0])
+        if bad:
+            raise IndexError(f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})")
+    return meta, ws
 
 
 def build_plan_from_slots(meta: GroupedMetadata, slot_pos: torch.Tensor, weights: torch.Tensor,
@@ -357,18 +406,25 @@ def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
 def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None, *, mode=None,
                            validate=None):
     """In-place combine into ``out`` (accumulates; mirrors ops.py:277-310)."""
+    code = _mode_code(mode)
+    T = out.shape[0]
+    plan = None
     if metadata is None or not isinstance(metadata, GroupedMetadata) or not metadata.matches(
         expert_tensors
     ):
-        metadata = prepare_grouped_metadata(expert_tensors, indices.device)
+        checked = _check_experts(expert_tensors)
+        if code == _abi.MODE_DET and sum(checked[3]) > 0:
+            metadata, plan = _metadata_and_plan(expert_tensors, checked, indices, weights, T,
+                                                validate)
+        else:
+            metadata = _metadata(expert_tensors, checked)
     _check_out(out, None, metadata.hidden, metadata.device)
     idx, w = _routing_args(indices, weights, metadata.num_rows, metadata.device)
     if metadata.max_rows == 0:  # ops.py:286: nothing to add
         return out
-    code = _mode_code(mode)
-    T = out.shape[0]
     if code == _abi.MODE_DET:
-        plan = build_plan(metadata, idx, w, T, validate)
+        if plan is None:
+            plan = build_plan(metadata, idx, w, T, validate)
         _launch_fwd(metadata, code, plan, None, None, out, accumulate=True)
     else:
         if _validate_default(validate):
@@ -379,19 +435,24 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
 
 def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices, weights,
                      out_shape, expert_tensors, slots=None):
-    meta = prepare_grouped_metadata(expert_tensors, indices.device)
+    checked = _check_experts(expert_tensors)
+    hidden, sizes = checked[2], checked[3]
     shape = tuple(int(s) for s in out_shape)
-    if len(shape) != 2 or shape[1] != meta.hidden:
-        raise ValueError(f"fastmoe_amd: out_shape {shape} must be [T, {meta.hidden}]")
+    if len(shape) != 2 or shape[1] != hidden:
+        raise ValueError(f"fastmoe_amd: out_shape {shape} must be [T, {hidden}]")
     T, D = shape
-    idx, w = _routing_args(indices, weights, meta.num_rows, meta.device)
     code = _mode_code(mode)
-    if meta.num_rows == 0:
-        plan = None
-    elif slots is not None and meta.num_rows == T * slots[1] and slots[1] <= 64:
-        plan = build_plan_from_slots(meta, slots[0], w, T, slots[1])
+    rows = sum(sizes)
+    if rows > 0 and not (slots is not None and rows == T * slots[1] and slots[1] <= 64):
+        # metadata and plan in one call (one launch for up to 256 experts)
+        meta, plan = _metadata_and_plan(expert_tensors, checked, indices, weights, T, validate)
     else:
-        plan = build_plan(meta, idx, w, T, validate)
+        meta = _metadata(expert_tensors, checked)
+        plan = None
+        if rows > 0:
+            _, w0 = _routing_args(indices, weights, meta.num_rows, meta.device)
+            plan = build_plan_from_slots(meta, slots[0], w0, T, slots[1])
+    idx, w = _routing_args(indices, weights, meta.num_rows, meta.device)
     if plan is None:
         out = torch.zeros(shape, dtype=meta.dtype, device=meta.device)
     elif code == _abi.MODE_DET:

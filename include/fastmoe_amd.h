@@ -129,6 +129,21 @@ FMOE_API int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d
                     void* d_workspace, void* stream);
 
 /*
+ * fmoe_build_metadata followed by fmoe_build_plan on the same experts, in one call (no counterpart
+ * in the reference, which builds metadata per call in prepare_grouped_metadata, ops.py:200-271,
+ * and needs no inverse).  Outputs and workspace exactly as those two calls; num_rows is the sum
+ * of host_rows.  With at most 256 experts and the one-launch plan's limits (N <= 2^20, T < 2^20)
+ * a single kernel launch writes both, the (address, rows) table riding in its arguments;
+ * otherwise it makes the two calls.
+ */
+FMOE_API int fmoe_build_metadata_and_plan(const int64_t* host_ptrs, const int64_t* host_rows,
+                                 int64_t num_experts, int64_t* d_ptr_table,
+                                 int32_t* d_chunk_sizes, int64_t* d_offsets, int32_t* d_max_rows,
+                                 const void* d_indices, int idx_dtype, const void* d_weights,
+                                 int w_dtype, int64_t num_tokens, int64_t row_bytes,
+                                 void* d_workspace, void* stream);
+
+/*
  * Plan of a combine fed by fmoe_permute_build (no counterpart in the reference; it replaces
  * fmoe_build_plan when the scatter index is that permutation's reverse map): token t's rows are
  * d_slot_pos[t * top_k + j], j < top_k, so the plan is written by one thread per slot with no

@@ -52,6 +52,14 @@ class FakeLib:
         self.calls.append(("plan", N, T, E, row_bytes, idt, wdt))
         return 0
 
+    def fmoe_build_metadata_and_plan(self, host_ptrs, host_rows, E, ptr_table, chunk, offsets,
+                                     max_rows, idx, idt, w, wdt, T, row_bytes, ws, stream):
+        assert isinstance(E, int) and E >= 1 and len(host_ptrs) == E and len(host_rows) == E
+        assert idt in (_abi.I64, _abi.I32) and wdt in (_abi.F32, _abi.BF16, _abi.F16)
+        assert all(isinstance(p, int) for p in (ptr_table, chunk, offsets, max_rows, idx, w, ws))
+        self.calls.append(("metadata_plan", E, list(host_rows), T, row_bytes, idt, wdt))
+        return 0
+
     def fmoe_combine_fwd(self, mode, plan, idx, idt, w, wdt, ptr_table, offsets, E, N, T, D, xdt,
                          out, odt, ostride, acc, stream):
         if mode == _abi.MODE_DET:
@@ -90,13 +98,12 @@ def test_autograd_forward_and_backward_calls(fake):
     assert out.shape == (4, 16) and out.dtype == torch.bfloat16
     grads = torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
     kinds = [c[0] for c in fake.calls]
-    assert kinds == ["metadata", "plan", "fwd", "bwd", "bwd"]
-    assert fake.calls[0] == ("metadata", 3, [3, 0, 5])
-    assert fake.calls[1] == ("plan", 8, 4, 3, 32, _abi.I64, _abi.F32)
-    assert fake.calls[2] == ("fwd", _abi.MODE_DET, 8, 4, 16, _abi.BF16, _abi.BF16, 16, 0)
+    assert kinds == ["metadata_plan", "fwd", "bwd", "bwd"]
+    assert fake.calls[0] == ("metadata_plan", 3, [3, 0, 5], 4, 32, _abi.I64, _abi.F32)
+    assert fake.calls[1] == ("fwd", _abi.MODE_DET, 8, 4, 16, _abi.BF16, _abi.BF16, 16, 0)
     # grad_X pass, then grad_w pass
-    assert fake.calls[3] == ("bwd", 8, 4, 16, _abi.BF16, 16, True, False, _abi.F32)
-    assert fake.calls[4] == ("bwd", 8, 4, 16, _abi.BF16, 16, False, True, _abi.F32)
+    assert fake.calls[2] == ("bwd", 8, 4, 16, _abi.BF16, 16, True, False, _abi.F32)
+    assert fake.calls[3] == ("bwd", 8, 4, 16, _abi.BF16, 16, False, True, _abi.F32)
     assert grads[0].shape == (N,) and grads[0].dtype == torch.float32
     assert [g.shape[0] for g in grads[1:]] == [3, 0, 5]
 
@@ -107,8 +114,8 @@ def test_fused_backward_is_one_call(fake, monkeypatch):
     w = torch.rand(8, requires_grad=True)
     out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, 4, (8,)), w, (4, 16))
     torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
-    assert [c[0] for c in fake.calls] == ["metadata", "plan", "fwd", "bwd"]
-    assert fake.calls[3][6:8] == (True, True)
+    assert [c[0] for c in fake.calls] == ["metadata_plan", "fwd", "bwd"]
+    assert fake.calls[2][6:8] == (True, True)
 
 
 def test_backward_skips_unneeded_outputs(fake):
@@ -143,7 +150,7 @@ def test_atomic_mode_zero_fills_and_skips_plan_in_place(fake):
     out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
                                                    torch.rand(8), (4, 16), mode="atomic")
     assert torch.all(out == 0)
-    assert [c[0] for c in fake.calls] == ["metadata", "plan", "fwd"]
+    assert [c[0] for c in fake.calls] == ["metadata_plan", "fwd"]
 
 
 def test_stale_metadata_is_rebuilt(fake):
@@ -153,7 +160,9 @@ def test_stale_metadata_is_rebuilt(fake):
     fake.calls.clear()
     fastmoe_amd.grouped_weighted_scatter_add(other, torch.zeros(8, dtype=torch.long), torch.rand(8),
                                              (4, 16), out=torch.zeros(4, 16), metadata=meta)
-    assert fake.calls[0][0] == "metadata"  # the passed table does not describe `other`
+    # the passed table does not describe `other`: metadata and plan are rebuilt in one call
+    assert [c[0] for c in fake.calls] == ["metadata_plan", "fwd"]
+    assert fake.calls[0][2] == [3, 0, 5]
 
 
 def test_argument_validation(fake):
@@ -180,4 +189,4 @@ def test_weighted_scatter_add_single_tensor(fake):
     src = torch.randn(10, 4)
     out = fastmoe_amd.weighted_scatter_add(src, torch.randint(0, 5, (10,)), torch.rand(10), (5, 4))
     assert out.shape == (5, 4)
-    assert fake.calls[0] == ("metadata", 1, [10])
+    assert fake.calls[0] == ("metadata_plan", 1, [10], 5, 16, _abi.I64, _abi.F32)

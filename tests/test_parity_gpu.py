@@ -476,6 +476,67 @@ def test_plan_matches_oracle(case, path, monkeypatch):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
+def _sorted_plan(plan, N, T):
+    """row_ptr, records ordered by g within every segment, and status words 0-1 of a plan."""
+    lib = fastmoe_amd._abi.lib()
+    h = plan.cpu()
+    rp = h[lib.fmoe_plan_row_ptr_offset(N, T):][: 4 * (T + 2)].view(torch.int32).numpy()
+    rec = h[lib.fmoe_plan_records_offset(N, T):][: 16 * N].view(torch.int64).view(N, 2).numpy()
+    g = (rec[:, 1] >> 32).astype(np.int32)
+    order = np.concatenate([np.arange(rp[b], rp[b + 1])[np.argsort(g[rp[b]:rp[b + 1]])]
+                            for b in range(T + 1)]) if N else np.zeros(0, dtype=np.int64)
+    return rp, rec[order], ops.plan_status(plan).cpu().numpy()[:2]
+
+
+@pytest.mark.parametrize("case", ["e256", "e300", "e1", "empty_experts", "long", "i32_bf16w",
+                                  "big_n"])
+def test_metadata_and_plan_in_one_call_equals_two_calls(case):
+    """fmoe_build_metadata_and_plan writes exactly what fmoe_build_metadata + fmoe_build_plan
+    write: one launch for up to 256 experts (within the one-launch plan's limits), the two calls
+    otherwise (300 experts, N > 2^20)."""
+    gen = torch.Generator().manual_seed(31)
+    D, dtype, idt, wdt = 8, torch.float32, torch.int64, torch.float32
+    if case == "big_n":
+        E, T, N, D = 16, 4096, (1 << 20) + 5, 1
+    else:
+        E, T, N = {"e256": (256, 512, 4096), "e300": (300, 512, 4096), "e1": (1, 64, 500),
+                   "empty_experts": (40, 100, 700), "long": (8, 40, 3000),
+                   "i32_bf16w": (64, 256, 2048)}[case]
+    if case == "i32_bf16w":
+        idt, wdt, dtype = torch.int32, torch.bfloat16, torch.bfloat16
+    cuts = torch.sort(torch.randint(0, N + 1, (E - 1,), generator=gen)).values.tolist()
+    sizes = [b - a for a, b in zip([0] + cuts, cuts + [N])]
+    if case == "empty_experts":
+        sizes = [0] * 20 + sizes[20:-1] + [sizes[-1] + sum(sizes[:20])]
+    hot = 3 if case == "long" else T
+    idx = torch.randint(0, hot, (N,), generator=gen).to(idt)
+    w = torch.rand(N, generator=gen).to(wdt)
+    xs = [torch.randn(n, D, generator=gen).to(dtype).to(DEV) for n in sizes]
+    idd, wd = idx.to(DEV), w.to(DEV)
+    meta1, plan1 = ops.prepare_metadata_and_plan(xs, idd, wd, T)
+    meta2 = fastmoe_amd.prepare_grouped_metadata(xs, DEV)
+    plan2 = fastmoe_amd.build_plan(meta2, idd, wd, T)
+    torch.cuda.synchronize()
+    assert meta1.sizes == meta2.sizes and meta1.max_rows == meta2.max_rows
+    for a, b in [(meta1.ptr_table, meta2.ptr_table), (meta1.chunk_sizes, meta2.chunk_sizes),
+                 (meta1.offsets_full, meta2.offsets_full),
+                 (meta1.max_rows_device, meta2.max_rows_device)]:
+        assert torch.equal(a, b)
+    rp1, rec1, st1 = _sorted_plan(plan1, N, T)
+    rp2, rec2, st2 = _sorted_plan(plan2, N, T)
+    np.testing.assert_array_equal(rp1, rp2)
+    np.testing.assert_array_equal(rec1, rec2)
+    np.testing.assert_array_equal(st1, st2)
+    if case == "long":  # segments over 64 rows come out in ascending g
+        g = (rec1[:, 1] >> 32).astype(np.int32)
+        lib = fastmoe_amd._abi.lib()
+        raw = plan1.cpu()[lib.fmoe_plan_records_offset(N, T):][: 16 * N].view(torch.int64)
+        graw = (raw.view(N, 2)[:, 1].numpy() >> 32).astype(np.int32)
+        for b in range(T):
+            if rp1[b + 1] - rp1[b] > 64:
+                assert np.array_equal(graw[rp1[b]:rp1[b + 1]], g[rp1[b]:rp1[b + 1]])
+
+
 @pytest.mark.parametrize("case", ["topk", "long", "one_token", "invalid_i32", "empty", "bigT"])
 def test_invert_scatter_index_matches_oracle(case):
     """fmoe_invert_scatter_index: row_ptr and the row list equal the oracle's stable inverse
