@@ -30,7 +30,7 @@ import torch
 
 from . import _abi
 from .ops import (_FLOAT_CODES, _INDEX_CODES, _launch_fwd, _require_cuda, _span, _stream_handle,
-                  _validate_default, build_plan, prepare_grouped_metadata)
+                  _validate_default, prepare_metadata_and_plan)
 
 __all__ = ["PermutedTokens", "permute_tokens"]
 
@@ -51,9 +51,8 @@ def _unit_gate_combine(rows: torch.Tensor, rev: torch.Tensor, num_tokens: int) -
     out = torch.empty((num_tokens, rows.shape[1]), dtype=rows.dtype, device=rows.device)
     if rows.shape[0] == 0:
         return out.zero_()
-    meta = prepare_grouped_metadata([rows], rows.device)
     ones = torch.ones(rows.shape[0], dtype=torch.float32, device=rows.device)
-    plan = build_plan(meta, rev, ones, num_tokens, validate=False)
+    meta, plan = prepare_metadata_and_plan([rows], rev, ones, num_tokens, validate=False)
     _launch_fwd(meta, _abi.MODE_DET, plan, None, None, out, accumulate=False)
     return out
 
