@@ -592,8 +592,38 @@ def test_metadata_matches_closed_forms():
         assert int(meta.max_rows_device.item()) == max(sizes)
 
 
-def test_large_token_count_uses_global_plan_path():
-    """T + 1 above the LDS histogram capacity (33792 bins): zero / count / scan in global memory."""
+def test_many_experts_beyond_the_lds_tables():
+    """5000 experts (0-2 rows each): more than the one-launch plan's LDS expert tables (4096) and
+    the metadata's kernel-argument table (256), so metadata and plan take their multi-launch
+    paths; forward bits, grad_X bits and grad_w against the oracle."""
+    gen = torch.Generator().manual_seed(41)
+    E, T, D = 5000, 700, 24
+    sizes = torch.randint(0, 3, (E,), generator=gen).tolist()
+    N = sum(sizes)
+    idx = torch.randint(0, T, (N,), generator=gen)
+    w = torch.rand(N, generator=gen)
+    experts = [torch.randn(n, D, generator=gen).to(torch.bfloat16) for n in sizes]
+    xs = [x.to(DEV).requires_grad_(True) for x in experts]
+    wd = w.to(DEV).requires_grad_(True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx.to(DEV), wd, (T, D))
+    go = torch.randn(T, D, generator=gen).to(torch.bfloat16)
+    grads = torch.autograd.grad(out, [wd, *xs], go.to(DEV), allow_unused=True)
+    torch.cuda.synchronize()
+    want, _, _ = oracle_fwd(experts, idx, w, T, torch.bfloat16)
+    np.testing.assert_array_equal(bits(out), want)
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, go)
+    got_gx = np.concatenate([to_np(g) for g, n in zip(grads[1:], sizes) if n])
+    np.testing.assert_array_equal(got_gx, want_gx)
+    scale = abs_dot(experts, idx, go, T)
+    assert np.all(np.abs(grads[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
+@pytest.mark.parametrize("path", ["split", "one_launch"])
+def test_large_token_count_plan_paths(path, monkeypatch):
+    """T = 40000: the split plan's histogram exceeds its LDS (33792 bins), so it counts and scans
+    in global memory; the one-launch plan spreads the 40001 bins over 40 workgroups."""
+    if path == "split":
+        monkeypatch.setenv("FMOE_PLAN_SPLIT", "1")
     D, T, k = 16, 40000, 2
     wl = Workload("bigT", T, D, 16, k, torch.float32, 13, False)
     idx, w, counts = make_routing(wl)
