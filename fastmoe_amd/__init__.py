@@ -13,6 +13,7 @@ from .ops import (
     grouped_weighted_scatter_add,
     invert_scatter_index,
     prepare_grouped_metadata,
+    prepare_metadata_and_plan,
     weighted_scatter_add,
 )
 
@@ -30,5 +31,6 @@ __all__ = [
     "grouped_weighted_scatter_add",
     "invert_scatter_index",
     "prepare_grouped_metadata",
+    "prepare_metadata_and_plan",
     "weighted_scatter_add",
 ]
