@@ -48,6 +48,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_vp, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp],
     ),
+    "fmoe_build_metadata_and_plan_from_slots": (
+        _c_int,
+        [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+         _c_i64, _c_i64, _c_vp, _c_int, _c_i64, _c_vp, _c_vp],
+    ),
     "fmoe_invert_scatter_index": (
         _c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp],
     ),

@@ -623,15 +623,72 @@ __global__ __launch_bounds__(kGroup) void k_invert_order(const int32_t* __restri
 // registers and the ordering pass is not needed.  A slot_pos entry outside [0, N) (an
 // inconsistent caller) yields a zero-gate record on packed row 0, so nothing is ever addressed
 // outside the expert buffers.
-template <typename TW>
+// Expert offsets (and, from kernel arguments, base addresses) of the slot-map plan in LDS.
+__device__ __forceinline__ void slots_load_meta(const TokMetaGlobal& m, int64_t E,
+                                                int64_t* off_lds, uint64_t*) {
+  for (int i = threadIdx.x; i <= E; i += kGroup) off_lds[i] = m.offsets[i];
+}
+__device__ __forceinline__ uint64_t slots_ptr(const TokMetaGlobal& m, const uint64_t*, int64_t e) {
+  return (uint64_t)m.ptr_table[e];
+}
+// E <= 256 == kGroup: one expert per thread; a workgroup scan of the row counts gives the
+// offsets, and workgroup 0 writes the metadata outputs (fmoe_build_metadata's).
+__device__ __forceinline__ void slots_load_meta(const TokMetaArgs& m, int64_t E, int64_t* off_lds,
+                                                uint64_t* ptr_lds) {
+  __shared__ int wave_tot[kWavesPerGroup], wave_max[kWavesPerGroup];
+  const int e = threadIdx.x, lane = e & (kWave - 1), wv = e / kWave;
+  const int rows = e < E ? m.a.rows[e] : 0;
+  const int64_t ptr = e < E ? m.a.ptr[e] : 0;
+  int incl = rows, mx = rows;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) mx = max(mx, __shfl_xor(mx, d, kWave));
+  if (lane == kWave - 1) wave_tot[wv] = incl;
+  if (lane == 0) wave_max[wv] = mx;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < kWavesPerGroup; ++i) {
+    before += i < wv ? wave_tot[i] : 0;
+    total += wave_tot[i];
+    mx = max(mx, wave_max[i]);
+  }
+  const int excl = before + incl - rows;
+  if (e < E) {
+    off_lds[e] = excl;
+    ptr_lds[e] = (uint64_t)ptr;
+  }
+  if (e == 0) off_lds[E] = total;
+  if (blockIdx.x == 0) {
+    if (e < E) {
+      m.ptr_table[e] = ptr;
+      m.chunk_sizes[e] = rows;
+      m.offsets[e] = excl;
+    }
+    if (e == 0) {
+      m.offsets[E] = total;
+      *m.max_rows = mx;
+    }
+  }
+}
+__device__ __forceinline__ uint64_t slots_ptr(const TokMetaArgs&, const uint64_t* ptr_lds,
+                                              int64_t e) {
+  return ptr_lds[e];
+}
+
+template <typename TW, typename Meta>
 __global__ __launch_bounds__(kGroup) void k_plan_from_slots(
     const int32_t* __restrict__ slot_pos, int64_t T, int64_t k, const TW* __restrict__ w,
-    const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
-    int64_t row_bytes, int32_t* __restrict__ row_ptr, Rec* __restrict__ rec,
-    int32_t* __restrict__ status) {
+    const Meta meta, int64_t E, int64_t row_bytes, int32_t* __restrict__ row_ptr,
+    Rec* __restrict__ rec, int32_t* __restrict__ status) {
   __shared__ int64_t off_lds[kLdsExperts + 1];
+  __shared__ uint64_t ptr_lds[kMetaChunk];  // used when the table comes in the arguments
   __shared__ int misaligned;
-  for (int i = threadIdx.x; i <= E; i += kGroup) off_lds[i] = offsets[i];
+  slots_load_meta(meta, E, off_lds, ptr_lds);
   if (threadIdx.x == 0) misaligned = 0;
   __syncthreads();
   const int64_t N = T * k;  // == off_lds[E], checked on the host
@@ -642,7 +699,7 @@ __global__ __launch_bounds__(kGroup) void k_plan_from_slots(
     const int64_t g = ok ? p : 0;
     const int64_t e = expert_of_row(off_lds, E, g);
     Rec r;
-    r.src = (uint64_t)ptr_table[e] + (uint64_t)((g - off_lds[e]) * row_bytes);
+    r.src = slots_ptr(meta, ptr_lds, e) + (uint64_t)((g - off_lds[e]) * row_bytes);
     r.w = ok ? ld1(w + g) : 0.f;
     r.g = (int32_t)g;
     rec[i] = r;
@@ -652,7 +709,8 @@ __global__ __launch_bounds__(kGroup) void k_plan_from_slots(
   // is misaligned iff its expert's base or the row length is not a multiple of 16 bytes.
   if (blockIdx.x == 0) {
     for (int64_t x = threadIdx.x; x < E; x += kGroup)
-      if (off_lds[x + 1] > off_lds[x] && ((ptr_table[x] & 15) || (row_bytes & 15))) misaligned = 1;
+      if (off_lds[x + 1] > off_lds[x] && ((slots_ptr(meta, ptr_lds, x) & 15) || (row_bytes & 15)))
+        misaligned = 1;
     __syncthreads();
     if (threadIdx.x == 0) {
       status[kStatusInvalid] = 0;
@@ -877,35 +935,36 @@ extern "C" int fmoe_build_metadata_and_plan(
                          reinterpret_cast<int32_t*>(ws + L.status), static_cast<hipStream_t>(stream));
 }
 
-extern "C" int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num_tokens,
-                                          int64_t top_k, const void* d_weights, int w_dtype,
-                                          const int64_t* d_ptr_table, const int64_t* d_offsets,
-                                          int64_t num_experts, int64_t num_rows,
-                                          int64_t row_bytes, void* d_workspace, void* stream) {
+namespace {
+
+// Checks of the slot-map plan's arguments (the expert table's pointers are checked by callers).
+int check_slots_args(const char* who, const int32_t* d_slot_pos, int64_t T, int64_t K,
+                     const void* d_weights, int w_dtype, int64_t E, int64_t N, int64_t row_bytes,
+                     void* d_workspace) {
   using namespace fmoe;
-  fmoe_host::clear_error();
-  const int64_t T = num_tokens, K = top_k, E = num_experts, N = num_rows;
-  FMOE_REQUIRE(T >= 1 && K >= 1 && K <= kWave,
-               "fmoe_build_plan_from_slots: need T >= 1 and 1 <= top_k <= %d (T=%lld k=%lld)",
-               kWave, (long long)T, (long long)K);
-  FMOE_REQUIRE(E >= 1 && E <= kLdsExperts, "fmoe_build_plan_from_slots: num_experts not in [1, %d]",
-               kLdsExperts);
+  FMOE_REQUIRE(T >= 1 && K >= 1 && K <= kWave, "%s: need T >= 1 and 1 <= top_k <= %d (T=%lld k=%lld)",
+               who, kWave, (long long)T, (long long)K);
+  FMOE_REQUIRE(E >= 1 && E <= kLdsExperts, "%s: num_experts not in [1, %d]", who, kLdsExperts);
   if (T >= (int64_t(1) << 30) || T * K >= (int64_t(1) << 31)) {
-    fmoe_host::set_error("fmoe_build_plan_from_slots: T*k exceeds the 32-bit row counters");
+    fmoe_host::set_error("%s: T*k exceeds the 32-bit row counters", who);
     return FMOE_ERANGE;
   }
   FMOE_REQUIRE(N == T * K,
-               "fmoe_build_plan_from_slots: every slot must be a row of the combine (rows %lld != "
-               "T*k %lld); build the plan from the scatter index instead",
-               (long long)N, (long long)(T * K));
-  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_build_plan_from_slots: bad weight dtype %d",
-               w_dtype);
-  FMOE_REQUIRE(d_slot_pos && d_weights && d_ptr_table && d_offsets && d_workspace,
-               "fmoe_build_plan_from_slots: null device pointer");
-  FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
-               "fmoe_build_plan_from_slots: workspace not 256B-aligned");
-  FMOE_REQUIRE(row_bytes > 0, "fmoe_build_plan_from_slots: row_bytes must be > 0");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+               "%s: every slot must be a row of the combine (rows %lld != T*k %lld); build the plan "
+               "from the scatter index instead",
+               who, (long long)N, (long long)(T * K));
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "%s: bad weight dtype %d", who, w_dtype);
+  FMOE_REQUIRE(d_slot_pos && d_weights && d_workspace, "%s: null device pointer", who);
+  FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0, "%s: workspace not 256B-aligned", who);
+  FMOE_REQUIRE(row_bytes > 0, "%s: row_bytes must be > 0", who);
+  return FMOE_OK;
+}
+
+template <typename Meta>
+int launch_from_slots(const Meta& meta, const int32_t* d_slot_pos, int64_t T, int64_t K,
+                      const void* d_weights, int w_dtype, int64_t E, int64_t N, int64_t row_bytes,
+                      void* d_workspace, hipStream_t s, const char* who) {
+  using namespace fmoe;
   const PlanLayout L = plan_layout(N, T);
   char* ws = static_cast<char*>(d_workspace);
   int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
@@ -914,14 +973,86 @@ extern "C" int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num
   const int64_t threads = std::max<int64_t>(N, T + 2);
   const dim3 grid((unsigned)((threads + kGroup - 1) / kGroup));
 #define FMOE_FROM_SLOTS(TW)                                                                        \
-  hipLaunchKernelGGL((k_plan_from_slots<TW>), grid, dim3(kGroup), 0, s, d_slot_pos, T, K,          \
-                     static_cast<const TW*>(d_weights), d_ptr_table, d_offsets, E, row_bytes,      \
-                     row_ptr, rec, status)
+  hipLaunchKernelGGL((k_plan_from_slots<TW, Meta>), grid, dim3(kGroup), 0, s, d_slot_pos, T, K,    \
+                     static_cast<const TW*>(d_weights), meta, E, row_bytes, row_ptr, rec, status)
   if (w_dtype == FMOE_F32) FMOE_FROM_SLOTS(float);
   else if (w_dtype == FMOE_BF16) FMOE_FROM_SLOTS(bf16_t);
   else FMOE_FROM_SLOTS(f16_t);
 #undef FMOE_FROM_SLOTS
-  return fmoe_host::check_launch("fmoe_build_plan_from_slots");
+  return fmoe_host::check_launch(who);
+}
+
+}  // namespace
+
+extern "C" int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num_tokens,
+                                          int64_t top_k, const void* d_weights, int w_dtype,
+                                          const int64_t* d_ptr_table, const int64_t* d_offsets,
+                                          int64_t num_experts, int64_t num_rows,
+                                          int64_t row_bytes, void* d_workspace, void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  const char* who = "fmoe_build_plan_from_slots";
+  if (int rc = check_slots_args(who, d_slot_pos, num_tokens, top_k, d_weights, w_dtype,
+                                num_experts, num_rows, row_bytes, d_workspace))
+    return rc;
+  FMOE_REQUIRE(d_ptr_table && d_offsets, "%s: null device pointer", who);
+  const TokMetaGlobal meta{d_ptr_table, d_offsets};
+  return launch_from_slots(meta, d_slot_pos, num_tokens, top_k, d_weights, w_dtype, num_experts,
+                           num_rows, row_bytes, d_workspace, static_cast<hipStream_t>(stream), who);
+}
+
+extern "C" int fmoe_build_metadata_and_plan_from_slots(
+    const int64_t* host_ptrs, const int64_t* host_rows, int64_t num_experts, int64_t* d_ptr_table,
+    int32_t* d_chunk_sizes, int64_t* d_offsets, int32_t* d_max_rows, const int32_t* d_slot_pos,
+    int64_t num_tokens, int64_t top_k, const void* d_weights, int w_dtype, int64_t row_bytes,
+    void* d_workspace, void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  const char* who = "fmoe_build_metadata_and_plan_from_slots";
+  const int64_t E = num_experts;
+  FMOE_REQUIRE(E >= 1 && E < (int64_t(1) << 30), "%s: num_experts must be in [1, 2^30) (got %lld)",
+               who, (long long)E);
+  FMOE_REQUIRE(host_ptrs && host_rows, "%s: null host table", who);
+  int64_t N = 0;
+  for (int64_t e = 0; e < E; ++e) {
+    if (host_rows[e] < 0 || host_rows[e] >= (int64_t(1) << 31)) break;  // reported below
+    N += host_rows[e];
+  }
+  if (E > kMetaChunk) {  // the two calls (each validates its own arguments)
+    if (int rc = fmoe_build_metadata(host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes,
+                                     d_offsets, d_max_rows, stream))
+      return rc;
+    return fmoe_build_plan_from_slots(d_slot_pos, num_tokens, top_k, d_weights, w_dtype,
+                                      d_ptr_table, d_offsets, E, N, row_bytes, d_workspace,
+                                      stream);
+  }
+  for (int64_t e = 0; e < E; ++e) {
+    FMOE_REQUIRE(host_rows[e] >= 0 && host_rows[e] < (int64_t(1) << 31),
+                 "%s: expert %lld has invalid row count %lld", who, (long long)e,
+                 (long long)host_rows[e]);
+    FMOE_REQUIRE(host_rows[e] == 0 || host_ptrs[e] != 0,
+                 "%s: expert %lld has rows but a null address", who, (long long)e);
+  }
+  FMOE_REQUIRE(d_ptr_table && d_chunk_sizes && d_offsets && d_max_rows,
+               "%s: null device output", who);
+  if (int rc = check_slots_args(who, d_slot_pos, num_tokens, top_k, d_weights, w_dtype, E, N,
+                                row_bytes, d_workspace))
+    return rc;
+  TokMetaArgs meta;
+  meta.a.count = (int32_t)E;
+  meta.a.base = 0;
+  meta.a.scan = 1;
+  meta.a.pad = 0;
+  for (int i = 0; i < kMetaChunk; ++i) {
+    meta.a.ptr[i] = i < E ? host_ptrs[i] : 0;
+    meta.a.rows[i] = i < E ? (int32_t)host_rows[i] : 0;
+  }
+  meta.ptr_table = d_ptr_table;
+  meta.chunk_sizes = d_chunk_sizes;
+  meta.offsets = d_offsets;
+  meta.max_rows = d_max_rows;
+  return launch_from_slots(meta, d_slot_pos, num_tokens, top_k, d_weights, w_dtype, E, N,
+                           row_bytes, d_workspace, static_cast<hipStream_t>(stream), who);
 }
 
 extern "C" int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, int64_t num_rows,

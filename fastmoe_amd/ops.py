@@ -48,6 +48,7 @@ __all__ = [
     "grouped_weighted_scatter_add",
     "prepare_grouped_metadata",
     "prepare_metadata_and_plan",
+    "prepare_metadata_and_plan_from_slots",
     "weighted_scatter_add",
 ]
 
@@ -331,6 +332,50 @@ def build_plan_from_slots(meta: GroupedMetadata, slot_pos: torch.Tensor, weights
     return ws
 
 
+def prepare_metadata_and_plan_from_slots(expert_tensors: Sequence[torch.Tensor],
+                                         slot_pos: torch.Tensor, weights: torch.Tensor,
+                                         num_tokens: int, top_k: int):
+    """``prepare_grouped_metadata`` followed by ``build_plan_from_slots`` in one C-ABI call
+    (``fmoe_build_metadata_and_plan_from_slots``: one kernel launch for up to 256 experts);
+    returns ``(metadata, plan)``."""
+    return _metadata_and_plan_from_slots(expert_tensors, _check_experts(expert_tensors), slot_pos,
+                                         weights, num_tokens, top_k)
+
+
+def _metadata_and_plan_from_slots(expert_tensors, checked, slot_pos, weights, num_tokens, top_k):
+    dtype, dev, hidden, sizes, ptrs = checked
+    lib = _abi.lib()
+    E, N = len(expert_tensors), sum(sizes)
+    if N != num_tokens * top_k or not (1 <= top_k <= 64):
+        raise ValueError(f"fastmoe_amd: a slot plan needs rows == T*k and k <= 64 "
+                         f"(rows {N}, T {num_tokens}, k {top_k})")
+    if slot_pos.dtype != torch.int32 or slot_pos.numel() != N or slot_pos.device != dev:
+        raise ValueError("fastmoe_amd: slot_pos must be int32 [T*k] on the experts' device")
+    w = weights.reshape(-1).contiguous()
+    if w.dtype not in _FLOAT_CODES or w.numel() != N:
+        raise ValueError("fastmoe_amd: weights must be a float [T*k] tensor")
+    ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
+    chunk_sizes = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
+    max_rows_dev = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev), _span("metadata_plan"):
+        rc = lib.fmoe_build_metadata_and_plan_from_slots(
+            (ctypes.c_int64 * E)(*ptrs), (ctypes.c_int64 * E)(*sizes), E, ptr_table.data_ptr(),
+            chunk_sizes.data_ptr(), offsets.data_ptr(), max_rows_dev.data_ptr(),
+            slot_pos.contiguous().data_ptr(), num_tokens, top_k, w.data_ptr(),
+            _FLOAT_CODES[w.dtype], hidden * expert_tensors[0].element_size(), ws.data_ptr(),
+            _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_build_metadata_and_plan_from_slots")
+    meta = GroupedMetadata(
+        ptr_table, chunk_sizes, offsets, max(sizes), E,
+        max_rows_device=max_rows_dev, tensors=expert_tensors, sizes=sizes, ptrs=ptrs,
+        hidden=hidden, dtype=dtype, device=dev,
+    )
+    return meta, ws
+
+
 def invert_scatter_index(indices: torch.Tensor, num_tokens: int):
     """The token-major inverse of ``indices`` as a CSR (``fmoe_invert_scatter_index``).
 
@@ -443,15 +488,15 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
     T, D = shape
     code = _mode_code(mode)
     rows = sum(sizes)
-    if rows > 0 and not (slots is not None and rows == T * slots[1] and slots[1] <= 64):
-        # metadata and plan in one call (one launch for up to 256 experts)
-        meta, plan = _metadata_and_plan(expert_tensors, checked, indices, weights, T, validate)
+    # metadata and plan in one call (one launch for up to 256 experts)
+    if rows == 0:
+        meta, plan = _metadata(expert_tensors, checked), None
+    elif slots is not None and rows == T * slots[1] and slots[1] <= 64:
+        _, w0 = _routing_args(indices, weights, rows, checked[1])
+        meta, plan = _metadata_and_plan_from_slots(expert_tensors, checked, slots[0], w0, T,
+                                                   slots[1])
     else:
-        meta = _metadata(expert_tensors, checked)
-        plan = None
-        if rows > 0:
-            _, w0 = _routing_args(indices, weights, meta.num_rows, meta.device)
-            plan = build_plan_from_slots(meta, slots[0], w0, T, slots[1])
+        meta, plan = _metadata_and_plan(expert_tensors, checked, indices, weights, T, validate)
     idx, w = _routing_args(indices, weights, meta.num_rows, meta.device)
     if plan is None:
         out = torch.zeros(shape, dtype=meta.dtype, device=meta.device)

@@ -159,6 +159,18 @@ FMOE_API int fmoe_build_plan_from_slots(const int32_t* d_slot_pos, int64_t num_t
                                void* d_workspace, void* stream);
 
 /*
+ * fmoe_build_metadata followed by fmoe_build_plan_from_slots on the same experts, in one call (no
+ * counterpart in the reference).  Outputs and workspace exactly as those two calls; num_rows is the
+ * sum of host_rows.  With at most 256 experts a single kernel launch writes both, the (address,
+ * rows) table riding in its arguments; otherwise it makes the two calls.
+ */
+FMOE_API int fmoe_build_metadata_and_plan_from_slots(
+    const int64_t* host_ptrs, const int64_t* host_rows, int64_t num_experts, int64_t* d_ptr_table,
+    int32_t* d_chunk_sizes, int64_t* d_offsets, int32_t* d_max_rows, const int32_t* d_slot_pos,
+    int64_t num_tokens, int64_t top_k, const void* d_weights, int w_dtype, int64_t row_bytes,
+    void* d_workspace, void* stream);
+
+/*
  * The token-major inverse of the scatter index as a bare CSR (no counterpart in the reference,
  * whose backward gathers by scatter index instead, ops.py:344; this is the plan without the
  * records, for callers that want the inverse index itself):

@@ -216,6 +216,32 @@ def test_plan_from_slots_equals_plan_from_scatter_index():
     assert st_b[0] == 0 and st_b[2] == k and st_a[0] == 0
 
 
+@pytest.mark.parametrize("E", [32, 300])
+def test_metadata_and_slot_plan_in_one_call_equals_two_calls(E):
+    """fmoe_build_metadata_and_plan_from_slots writes exactly what fmoe_build_metadata +
+    fmoe_build_plan_from_slots write: one launch for up to 256 experts, the two calls above."""
+    T, D, k = 300, 40, 4
+    ids, w = _routing(T, E, k, seed=23)
+    x = torch.randn(T, D).to(DEV)
+    p = fastmoe_amd.permute_tokens(x, ids.to(DEV), w.to(DEV), E)
+    experts = [c.contiguous() for c in p.permuted_data.split(p.expert_counts.tolist())]
+    N = T * k
+    meta1, plan1 = fastmoe_amd.ops.prepare_metadata_and_plan_from_slots(
+        experts, p.slot_pos, p.sorted_weights, T, k)
+    meta2 = fastmoe_amd.prepare_grouped_metadata(experts, DEV)
+    plan2 = fastmoe_amd.ops.build_plan_from_slots(meta2, p.slot_pos, p.sorted_weights, T, k)
+    torch.cuda.synchronize()
+    for a, b in [(meta1.ptr_table, meta2.ptr_table), (meta1.chunk_sizes, meta2.chunk_sizes),
+                 (meta1.offsets_full, meta2.offsets_full),
+                 (meta1.max_rows_device, meta2.max_rows_device)]:
+        assert torch.equal(a, b)
+    rp1, seg1, st1 = _plan_segments(plan1, N, T)
+    rp2, seg2, st2 = _plan_segments(plan2, N, T)
+    np.testing.assert_array_equal(rp1, rp2)
+    assert seg1 == seg2
+    np.testing.assert_array_equal(st1[:3], st2[:3])
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_unpermute_with_permutation_is_bit_identical(dtype):
     T, D, E, k = 256, 192, 32, 6

@@ -60,6 +60,15 @@ class FakeLib:
         self.calls.append(("metadata_plan", E, list(host_rows), T, row_bytes, idt, wdt))
         return 0
 
+    def fmoe_build_metadata_and_plan_from_slots(self, host_ptrs, host_rows, E, ptr_table, chunk,
+                                                offsets, max_rows, slot_pos, T, k, w, wdt,
+                                                row_bytes, ws, stream):
+        assert isinstance(E, int) and E >= 1 and len(host_ptrs) == E and len(host_rows) == E
+        assert wdt in (_abi.F32, _abi.BF16, _abi.F16) and 1 <= k <= 64
+        assert all(isinstance(p, int) for p in (ptr_table, chunk, offsets, max_rows, slot_pos, w, ws))
+        self.calls.append(("metadata_plan_slots", E, list(host_rows), T, k, row_bytes, wdt))
+        return 0
+
     def fmoe_combine_fwd(self, mode, plan, idx, idt, w, wdt, ptr_table, offsets, E, N, T, D, xdt,
                          out, odt, ostride, acc, stream):
         if mode == _abi.MODE_DET:
