@@ -735,6 +735,25 @@ def test_full_size_forward_parity(name):
     np.testing.assert_array_equal(bits(out), want)
 
 
+def test_full_size_properties_gigachat():
+    """Size-independent properties at the headline size: doubling every gate doubles every output
+    bit pattern exactly (a power-of-two scale is exact through the fp32 products and sum and the
+    bf16 rounding), and the same rows given as one concatenated expert tensor give the same bits
+    as the 256 separate buffers."""
+    wl = WORKLOADS["gigachat"]
+    idx, w, counts = make_routing(wl)
+    xd = make_experts(counts, wl.D, wl.dtype, DEV, wl.seed)
+    idd, wd = idx.to(DEV), w.to(DEV)
+    shape = (wl.T, wl.D)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, shape)
+    out2 = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, 2 * wd, shape)
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out2, out * 2)
+    del out2
+    one = fastmoe_amd.grouped_weighted_scatter_add([torch.cat(xd)], idd, wd, shape)
+    assert torch.equal(one.view(torch.int16), out.view(torch.int16))
+
+
 def test_full_size_det_repeatable_and_atomic_bounded():
     """BASELINE config 5 at its full size (T=32768, D=16384, E=256, top-2, bf16): ten
     deterministic runs are bit-identical; ten atomic runs each stay within the packed-bf16
@@ -750,6 +769,10 @@ def test_full_size_det_repeatable_and_atomic_bounded():
     for _ in range(9):
         again = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, shape, mode="det")
         assert torch.equal(again.view(torch.int16), det_bits)
+    want, _, bad = oracle_fwd([x.cpu() for x in xd], idx, w, wl.T, wl.dtype)
+    assert bad == 0
+    np.testing.assert_array_equal(bits(det), want)  # and bit-exact against the oracle
+    del want
     # sum|terms| per output element, torch fp32 ops on the GPU (a tolerance scale only)
     scale = torch.zeros(shape, device=DEV)
     scale.index_add_(0, idd, torch.cat(xd).float().abs() * wd.abs()[:, None])
