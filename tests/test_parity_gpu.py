@@ -476,6 +476,41 @@ def test_plan_matches_oracle(case, path, monkeypatch):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
+@pytest.mark.parametrize("T,N", [(1, 1), (1, 5000), (2, 3), (2, 4500)])
+def test_plan_few_tokens(T, N):
+    """One or two tokens: one or two workgroups, a segment of thousands of rows (stash overflow
+    and the long-segment ordering), and out-of-range indices mixed in; the plan and the forward
+    against the oracle."""
+    from oracle import cref
+
+    gen = torch.Generator().manual_seed(43 + N)
+    D = 12
+    idx = torch.randint(0, T, (N,), generator=gen)
+    idx[::7] = T          # out of range, both sides
+    idx[3::11] = -2
+    w = torch.rand(N, generator=gen)
+    sizes = [N // 3, N - 2 * (N // 3), N // 3]
+    experts = [torch.randn(n, D, generator=gen) for n in sizes]
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta, plan = ops.prepare_metadata_and_plan(xd, idd, wd, T)
+    lib = fastmoe_amd._abi.lib()
+    rp = plan[lib.fmoe_plan_row_ptr_offset(N, T):][: 4 * (T + 2)].view(torch.int32).cpu().numpy()
+    rec = plan[lib.fmoe_plan_records_offset(N, T):][: 16 * N].view(torch.int64).view(N, 2).cpu()
+    want_rp, want_g = cref.plan(idx.numpy(), T)
+    np.testing.assert_array_equal(rp, want_rp)
+    g = (rec[:, 1] >> 32).numpy().astype(np.int32)
+    for b in range(T + 1):
+        seg = g[want_rp[b]:want_rp[b + 1]]
+        if b < T and seg.size > 64:
+            assert np.all(np.diff(seg) > 0)  # long segments in ascending g
+        np.testing.assert_array_equal(np.sort(seg), want_g[want_rp[b]:want_rp[b + 1]])
+    assert int(ops.plan_status(plan)[0]) == int((want_rp[T + 1] - want_rp[T]))
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
+    want, _, bad = oracle_fwd(experts, idx, w, T, torch.float32)
+    assert bad == want_rp[T + 1] - want_rp[T]
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+
+
 def _sorted_plan(plan, N, T):
     """row_ptr, records ordered by g within every segment, and status words 0-1 of a plan."""
     lib = fastmoe_amd._abi.lib()
