@@ -95,7 +95,13 @@ def lib() -> ctypes.CDLL:
         )
     handle = ctypes.CDLL(str(path))
     for name, (restype, argtypes) in SIGNATURES.items():
-        fn = getattr(handle, name)
+        try:
+            fn = getattr(handle, name)
+        except AttributeError:
+            raise FastMoEError(
+                f"fastmoe_amd: {path} does not export {name} (a library built from other sources); "
+                "rebuild it with `python -m fastmoe_amd.build`"
+            ) from None
         fn.restype = restype
         fn.argtypes = argtypes
     ver = handle.fmoe_abi_version()

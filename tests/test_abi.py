@@ -137,3 +137,23 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     with pytest.raises(_abi.FastMoEError, match="no non-HIP fallback"):
         _abi.lib()
     monkeypatch.setattr(_abi, "_LIB", None)
+
+
+def test_library_missing_a_symbol_fails_loudly(monkeypatch, tmp_path):
+    """A library built from other sources (here: one exporting only the version) is refused with
+    FastMoEError naming the missing entry point, not an AttributeError from ctypes."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "stub.c"
+    src.write_text("int fmoe_abi_version(void) { return %d; }\n" % _abi.ABI_VERSION)
+    so = tmp_path / "libstub.so"
+    subprocess.run([cc, "-shared", "-fPIC", str(src), "-o", str(so)], check=True)
+    monkeypatch.setattr(_abi, "_LIB", None)
+    monkeypatch.setenv("FASTMOE_AMD_LIB", str(so))
+    with pytest.raises(_abi.FastMoEError, match="does not export fmoe_last_error"):
+        _abi.lib()
+    monkeypatch.setattr(_abi, "_LIB", None)
