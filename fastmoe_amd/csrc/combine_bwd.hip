@@ -133,7 +133,13 @@ __device__ __forceinline__ void bwd_row_body(uint64_t src, float wt, uint32_t t,
           float go[V], y[V];
           VX::cvt(gr[h][u], go);
 #pragma unroll
-          for (int v = 0; v < V; ++v) y[v] = go[v] * wt;
+          for (int v = 0; v < V; ++v) {
+            y[v] = go[v] * wt;
+            // f16: keep the fp32 product in a register.  Otherwise the multiply and the
+            // conversion to f16 fuse into v_fma_mixlo_f16, which rounds once where the reference
+            // (index_select * w in fp32, then the cast to f16) rounds twice.
+            if constexpr (std::is_same<TX, f16_t>::value) __asm__("" : "+v"(y[v]));
+          }
           VX::template st<FMOE_GX_CPOL>(rgx, off[h][u], y);
         }
         if constexpr (GW) part += dot_partial<TX, V>(xr[h][u], gr[h][u]);

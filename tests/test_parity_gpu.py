@@ -476,6 +476,74 @@ def test_plan_matches_oracle(case, path, monkeypatch):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
+def test_bwd_f16_grad_x_rounds_twice_like_the_reference():
+    """f16 experts, fp32 gates: grad_X is the fp32 product rounded to fp32 and then to f16
+    (index_select * w, then autograd's cast; ops.py:344-353).  The inputs include elements where
+    rounding the exact product once to f16 gives another value, so a kernel that fuses the
+    multiply and the conversion (one rounding) fails here."""
+    gen = torch.Generator().manual_seed(47)
+    T, D, k, E = 1000, 1024, 2, 64
+    N = T * k
+    idx = torch.arange(T).repeat_interleave(k)[torch.randperm(N, generator=gen)]
+    w = torch.rand(N, generator=gen)
+    sizes = [N // E] * (E - 1) + [N - (N // E) * (E - 1)]
+    experts = [torch.randn(n, D, generator=gen).to(torch.float16) for n in sizes]
+    go = torch.randn(T, D, generator=gen).to(torch.float16)
+    # sensitivity: some products differ between one rounding and two
+    prod = go.double().numpy()[idx.numpy()] * w.double().numpy()[:, None]
+    once = prod.astype(np.float16)
+    twice = prod.astype(np.float32).astype(np.float16)
+    assert np.count_nonzero(once != twice) > 0
+    xs = [x.to(DEV).requires_grad_(True) for x in experts]
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx.to(DEV), w.to(DEV), (T, D))
+    grads = torch.autograd.grad(out, xs, go.to(DEV))
+    want_gx, _ = oracle_bwd(experts, idx, w, T, go)
+    np.testing.assert_array_equal(np.concatenate([to_np(g) for g in grads]), want_gx)
+    np.testing.assert_array_equal(want_gx.view(np.float16), twice)  # the oracle rounds twice
+
+
+def test_random_shapes_against_oracle():
+    """40 seeded random cases: tokens, experts (some empty), rows, D, every dtype combination,
+    int32/int64 indices, and out-of-range indices mixed in; forward bits, grad_X bits and grad_w
+    (1e-6 of sum|terms|) against the oracle, through the autograd path."""
+    rng = np.random.default_rng(2026)
+    dts = [torch.float32, torch.bfloat16, torch.float16]
+    for case in range(40):
+        T = int(rng.choice([1, 2, 7, 64, 300, 1000, 2500]))
+        E = int(rng.integers(1, 300))
+        N = int(rng.integers(1, 6000))
+        D = int(rng.choice([1, 7, 8, 64, 200, 1024]))
+        xdt = dts[int(rng.integers(3))]
+        wdt = [torch.float32, torch.bfloat16][int(rng.integers(2))]
+        idt = [torch.int64, torch.int32][int(rng.integers(2))]
+        gen = torch.Generator().manual_seed(case)
+        cuts = np.sort(rng.integers(0, N + 1, E - 1))
+        sizes = np.diff(np.concatenate([[0], cuts, [N]])).tolist()
+        idx = torch.from_numpy(rng.integers(0, T, N)).to(idt)
+        if case % 3 == 0:
+            idx[:: int(rng.integers(5, 50))] = T + 1  # out of range
+        w = torch.rand(N, generator=gen).to(wdt)
+        experts = [torch.randn(n, D, generator=gen).to(xdt) for n in sizes]
+        xs = [x.to(DEV).requires_grad_(True) for x in experts]
+        wd = w.to(DEV).requires_grad_(True)
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx.to(DEV), wd, (T, D))
+        go = torch.randn(T, D, generator=gen).to(xdt)
+        grads = torch.autograd.grad(out, [wd, *xs], go.to(DEV))
+        torch.cuda.synchronize()
+        label = f"case {case}: T={T} E={E} N={N} D={D} {xdt} {wdt} {idt}"
+        want, _, _ = oracle_fwd(experts, idx, w, T, xdt)
+        np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32
+                                      else want, err_msg=label)
+        want_gx, want_gw = oracle_bwd(experts, idx, w, T, go)
+        got_gx = np.concatenate([to_np(g).reshape(-1, D) for g in grads[1:]])
+        np.testing.assert_array_equal(got_gx.view(want_gx.dtype), want_gx, err_msg=label)
+        scale = abs_dot(experts, idx, go, T)
+        err = np.abs(grads[0].double().cpu().numpy() - want_gw)
+        # grad_w is stored in the gates' dtype: add its rounding (2^-8 for bf16)
+        rtol = 1e-6 if wdt == torch.float32 else 2.0 ** -8
+        assert np.all(err <= 1e-6 * scale + rtol * np.abs(want_gw) + 1e-30), label
+
+
 @pytest.mark.parametrize("T,N", [(1, 1), (1, 5000), (2, 3), (2, 4500)])
 def test_plan_few_tokens(T, N):
     """One or two tokens: one or two workgroups, a segment of thousands of rows (stash overflow
