@@ -502,10 +502,14 @@ def test_bwd_f16_grad_x_rounds_twice_like_the_reference():
     np.testing.assert_array_equal(want_gx.view(np.float16), twice)  # the oracle rounds twice
 
 
-def test_random_shapes_against_oracle():
+@pytest.mark.parametrize("plan", ["one_launch", "split"])
+def test_random_shapes_against_oracle(plan, monkeypatch):
     """40 seeded random cases: tokens, experts (some empty), rows, D, every dtype combination,
     int32/int64 indices, and out-of-range indices mixed in; forward bits, grad_X bits and grad_w
-    (1e-6 of sum|terms|) against the oracle, through the autograd path."""
+    (1e-6 of sum|terms|) against the oracle, through the autograd path, with the one-launch
+    and the three-launch plan."""
+    if plan == "split":
+        monkeypatch.setenv("FMOE_PLAN_SPLIT", "1")
     rng = np.random.default_rng(2026)
     dts = [torch.float32, torch.bfloat16, torch.float16]
     for case in range(40):
@@ -542,6 +546,47 @@ def test_random_shapes_against_oracle():
         # grad_w is stored in the gates' dtype: add its rounding (2^-8 for bf16)
         rtol = 1e-6 if wdt == torch.float32 else 2.0 ** -8
         assert np.all(err <= 1e-6 * scale + rtol * np.abs(want_gw) + 1e-30), label
+
+
+def test_random_inplace_against_oracle():
+    """30 seeded random in-place calls (ops.py:389-390: accumulate into the given out): out in
+    fp32, bf16 or f16 with random prior contents and sometimes a padded row stride; the
+    deterministic mode bit-exact against the oracle started from out's values, the atomic mode
+    (fp32 out) within the reordering bound."""
+    rng = np.random.default_rng(77)
+    dts = [torch.float32, torch.bfloat16, torch.float16]
+    for case in range(30):
+        T = int(rng.choice([1, 5, 64, 700, 2000]))
+        E = int(rng.integers(1, 100))
+        N = int(rng.integers(1, 4000))
+        D = int(rng.choice([8, 24, 256, 1000, 2048]))
+        pad = int(rng.choice([0, 0, 8, 40]))
+        xdt, odt = dts[int(rng.integers(3))], dts[int(rng.integers(3))]
+        mode = "atomic" if (odt == torch.float32 and case % 4 == 1) else "det"
+        gen = torch.Generator().manual_seed(100 + case)
+        cuts = np.sort(rng.integers(0, N + 1, E - 1))
+        sizes = np.diff(np.concatenate([[0], cuts, [N]])).tolist()
+        idx = torch.from_numpy(rng.integers(0, T, N))
+        w = torch.rand(N, generator=gen)
+        experts = [torch.randn(n, D, generator=gen).to(xdt) for n in sizes]
+        init = torch.randn(T, D, generator=gen).to(odt)
+        big = torch.zeros(T, D + pad, dtype=odt, device=DEV)
+        out = big[:, :D]
+        out.copy_(init.to(DEV))
+        xd, idd, wd = _to_dev(experts, idx, w)
+        fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), out=out, mode=mode)
+        torch.cuda.synchronize()
+        label = f"case {case}: T={T} E={E} N={N} D={D} pad={pad} {xdt} out {odt} {mode}"
+        want, acc, _ = oracle_fwd(experts, idx, w, T, odt, acc_init=init.float().numpy())
+        if mode == "det":
+            np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32
+                                          else want, err_msg=label)
+        else:
+            kmax = max(2, int(np.bincount(idx.numpy(), minlength=T).max()))
+            scale = abs_sum(experts, idx, w, T) + np.abs(init.float().numpy())
+            assert np.all(np.abs(out.cpu().numpy() - acc) <= kmax * 2.0 ** -24 * scale + 1e-30), label
+        if pad:
+            assert not bool(big[:, D:].any()), label  # the padding columns are never written
 
 
 @pytest.mark.parametrize("T,N", [(1, 1), (1, 5000), (2, 3), (2, 4500)])
