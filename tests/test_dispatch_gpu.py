@@ -80,6 +80,29 @@ def test_permute_many_experts_uses_large_variant():
     _check_permute(torch.randn(300, 32), ids, w, 3000)
 
 
+def test_permute_random_shapes():
+    """30 seeded random permutations against the oracle: tokens, top-k, experts (including more
+    than 1024, the small-block ranking), row bytes (16-, 4- and 2-byte copies), id and gate
+    dtypes, ids with repeats within a token, and out-of-range ids."""
+    rng = np.random.default_rng(5150)
+    dts = [torch.float32, torch.bfloat16, torch.float16]
+    for case in range(30):
+        T = int(rng.choice([1, 3, 64, 500, 2000]))
+        E = int(rng.choice([1, 2, 17, 256, 1500, 4096]))
+        k = int(rng.integers(1, 9))
+        D = int(rng.choice([1, 7, 16, 100, 1024]))
+        gen = torch.Generator().manual_seed(200 + case)
+        ids = torch.from_numpy(rng.integers(0, E, (T, k)))
+        if case % 4 == 0:
+            ids[torch.from_numpy(rng.random((T, k)) < 0.05)] = E   # out of range
+        if case % 4 == 2:
+            ids = ids.to(torch.int32)
+        w = torch.rand(T, k, generator=gen).to([torch.float32, torch.bfloat16][case % 2])
+        x = torch.randn(T, D, generator=gen).to(dts[int(rng.integers(3))])
+        p, bad = _check_permute(x, ids, w, E)
+        assert bad == int(((ids < 0) | (ids >= E)).sum()), f"case {case}"
+
+
 def test_permute_invalid_ids_go_last_and_validate_raises():
     ids, w = _routing(100, 8, 2, seed=5)
     ids[3, 0] = 8
