@@ -532,9 +532,16 @@ def test_random_shapes_against_oracle(plan, monkeypatch):
         wd = w.to(DEV).requires_grad_(True)
         out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx.to(DEV), wd, (T, D))
         go = torch.randn(T, D, generator=gen).to(xdt)
-        grads = torch.autograd.grad(out, [wd, *xs], go.to(DEV))
+        if case % 5 == 3:    # grad_out rows with a padded stride (read in place)
+            god = torch.zeros(T, D + 24, dtype=xdt, device=DEV)[:, :D]
+            god.copy_(go.to(DEV))
+        elif case % 5 == 4:  # a transposed grad_out (made contiguous by the backward)
+            god = go.t().contiguous().to(DEV).t()
+        else:
+            god = go.to(DEV)
+        grads = torch.autograd.grad(out, [wd, *xs], god)
         torch.cuda.synchronize()
-        label = f"case {case}: T={T} E={E} N={N} D={D} {xdt} {wdt} {idt}"
+        label = f"case {case}: T={T} E={E} N={N} D={D} {xdt} {wdt} {idt} go strides {god.stride()}"
         want, _, _ = oracle_fwd(experts, idx, w, T, xdt)
         np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32
                                       else want, err_msg=label)
