@@ -174,11 +174,13 @@ def test_gate_and_sort_matches_reference_formulation():
     assert torch.equal(permuted, want_perm)
 
 
+@pytest.mark.parametrize("shape", [(2, 40, 64, 96, 8, 2), (3, 50, 128, 64, 32, 4)])
 @pytest.mark.parametrize("impl", [MoEImplementation.FAST, MoEImplementation.STANDARD])
-def test_moe_layer_forward_backward(impl):
+def test_moe_layer_forward_backward(impl, shape):
+    B, T, dim, ff, E, k = shape
     torch.manual_seed(1)
-    layer = fastmoe_amd.MoEFeedForward(64, 96, 8, 2, implementation=impl).to(DEV)
-    x = torch.randn(2, 40, 64, device=DEV, requires_grad=True)
+    layer = fastmoe_amd.MoEFeedForward(dim, ff, E, k, implementation=impl).to(DEV)
+    x = torch.randn(B, T, dim, device=DEV, requires_grad=True)
     y = layer(x)
     go = torch.randn_like(y)
     params = [x, layer.router.weight, *[p for e in layer.experts for p in e.parameters()]]
