@@ -156,6 +156,31 @@ def test_backward_matches_torch(dtype):
     assert np.all(np.abs(gw - want_gw) <= 1e-12 * scale + 1e-300)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_backward_16bit_rounds_the_fp32_product_twice_like_torch(dtype):
+    """grad_X of 16-bit experts is the fp32 product rounded to fp32, then cast (two roundings):
+    torch's index_select * w then .to(dtype) (ops.py:344-353 + autograd's cast).  The inputs hold
+    elements where rounding the exact product once would give another value, so an oracle that
+    rounded once would fail here."""
+    T, D, E, k = 300, 256, 8, 2
+    xs, idx, w, counts = _routed(13, T=T, D=D, E=E, k=k, dtype=dtype)
+    go = torch.randn(T, D, generator=torch.Generator().manual_seed(14)).to(dtype)
+    code = cref.F16 if dtype == torch.float16 else cref.BF16
+    gx, _ = cref.combine_bwd([to_np(x) for x in xs], idx.numpy(), w.numpy(), T, D, to_np(go), code,
+                             want_w=False)
+    want = torch.cat(torch_ref.bwd_grad_x(go, idx, w, counts, dtype))
+    np.testing.assert_array_equal(gx, to_np(want))
+    # one rounding of the exact (fp64) product, straight to the 16-bit format (torch's own
+    # fp64 -> 16-bit cast goes through fp32, i.e. rounds twice itself)
+    exact = (go.double()[idx] * w.double()[:, None]).numpy()
+    if dtype == torch.float16:
+        once = exact.astype(np.float16).view(np.uint16)
+    else:  # 8 significant bits, half to even; the result is exact in bf16
+        m, e = np.frexp(exact)
+        once = to_np(torch.from_numpy(np.ldexp(np.round(m * 256) / 256, e)).to(dtype))
+    assert np.count_nonzero(once != to_np(want)) > 0  # the double rounding is exercised
+
+
 def test_backward_invalid_rows_get_zero():
     x = torch.randn(3, 4)
     idx = torch.tensor([1, 9, 0])
