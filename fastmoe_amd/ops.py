@@ -122,6 +122,7 @@ class GroupedMetadata(tuple):
         self.hidden = extra["hidden"]
         self.dtype = extra["dtype"]
         self.device = extra["device"]
+        self.device_index = self.tensors[0].get_device()
         self.num_rows = sum(self.sizes)
         return self
 
@@ -133,11 +134,16 @@ class GroupedMetadata(tuple):
     num_experts = property(lambda self: self[4])
 
     def matches(self, expert_tensors: Sequence[torch.Tensor]) -> bool:
-        """True if this metadata describes exactly these buffers (same addresses and rows)."""
+        """True if this metadata describes exactly these buffers: same addresses, rows, dtype,
+        device and hidden size, each row-contiguous (a strided view of the same memory does not
+        match)."""
         if len(expert_tensors) != len(self.ptrs):
             return False
+        dev_index = self.device_index
         return all(
-            t.shape[0] == n and (t.data_ptr() if n else 0) == p
+            t.shape[0] == n and (t.data_ptr() if n else 0) == p and t.dtype == self.dtype
+            and t.dim() == 2 and t.shape[1] == self.hidden and t.get_device() == dev_index
+            and t.is_contiguous()
             for t, p, n in zip(expert_tensors, self.ptrs, self.sizes)
         )
 

@@ -174,6 +174,29 @@ def test_stale_metadata_is_rebuilt(fake):
     assert fake.calls[0][2] == [3, 0, 5]
 
 
+def test_metadata_of_the_same_memory_under_another_view_does_not_match(fake):
+    wide = torch.randn(3, 32)
+    packed = wide.reshape(-1)[:48].view(3, 16)   # same address and rows as wide[:, :16]
+    meta = fastmoe_amd.prepare_grouped_metadata([packed], "cuda")
+    assert meta.matches([packed])
+    strided = wide[:, :16]
+    assert strided.data_ptr() == packed.data_ptr() and not meta.matches([strided])
+    with pytest.raises(ValueError, match="row-contiguous"):
+        fastmoe_amd.grouped_weighted_scatter_add([strided], torch.zeros(3, dtype=torch.long),
+                                                 torch.rand(3), (2, 16), out=torch.zeros(2, 16),
+                                                 metadata=meta)
+    half = torch.randn(3, 16).to(torch.bfloat16)
+    meta = fastmoe_amd.prepare_grouped_metadata([half], "cuda")
+    as_f16 = half.view(torch.float16)
+    assert not meta.matches([as_f16])
+    fake.calls.clear()
+    fastmoe_amd.grouped_weighted_scatter_add([as_f16], torch.zeros(3, dtype=torch.long),
+                                             torch.rand(3), (2, 16),
+                                             out=torch.zeros(2, 16, dtype=torch.float16),
+                                             metadata=meta)
+    assert fake.calls[0][0] == "metadata_plan" and fake.calls[1][5] == _abi.F16
+
+
 def test_argument_validation(fake):
     xs = _experts(torch.float32)
     with pytest.raises(ValueError, match="total expert rows"):

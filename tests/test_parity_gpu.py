@@ -175,6 +175,32 @@ def test_bwd_without_gate_grad_and_without_expert_grad():
     assert np.all(np.abs(gw.double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
+@pytest.mark.parametrize("form", ["row_broadcast", "sum"])
+def test_bwd_broadcast_grad_out(form):
+    """Broadcast gradients: one row expanded over the tokens (row stride 0, read in place by the
+    backward) and the all-zero-stride gradient of out.sum().  Both equal the oracle on the
+    materialised grad_out."""
+    wl, T, idx, w, experts = _inputs("gigachat", T=64)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    xd = [x.requires_grad_(True) for x in xd]
+    wd.requires_grad_(True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D))
+    if form == "row_broadcast":
+        row = torch.randn(1, wl.D, generator=torch.Generator().manual_seed(3)).to(wl.dtype)
+        god = row.to(DEV).expand(T, wl.D)
+        assert god.stride() == (0, 1)
+        grads = torch.autograd.grad(out, [wd, *xd], god)
+        grad_out = row.expand(T, wl.D).contiguous()
+    else:
+        grads = torch.autograd.grad(out.sum(), [wd, *xd])
+        grad_out = torch.ones(T, wl.D, dtype=wl.dtype)
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, grad_out)
+    got_gx = np.concatenate([to_np(g) for g in grads[1:]], 0)
+    np.testing.assert_array_equal(got_gx, want_gx)
+    scale = abs_dot(experts, idx, grad_out, T)
+    assert np.all(np.abs(grads[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
 def test_inplace_accumulates_into_out():
     """ops.py:389-390 contract: the kernel adds into the given out (here non-zero)."""
     wl, T, idx, w, experts = _inputs("mid", T=256)
@@ -553,6 +579,70 @@ def test_random_shapes_against_oracle(plan, monkeypatch):
         # grad_w is stored in the gates' dtype: add its rounding (2^-8 for bf16)
         rtol = 1e-6 if wdt == torch.float32 else 2.0 ** -8
         assert np.all(err <= 1e-6 * scale + rtol * np.abs(want_gw) + 1e-30), label
+
+
+@pytest.mark.parametrize("bwd", ["split", "fused"])
+def test_random_misaligned_buffers_against_oracle(bwd, monkeypatch):
+    """16 seeded random cases whose buffers sit at arbitrary element offsets of shared pools:
+    every expert (some empty) a contiguous view at a random offset, grad_out and an in-place out
+    at odd offsets with padded row strides.  Forward (autograd and in place, det) bit-exact,
+    grad_X bit-exact and grad_w within 1e-6 of sum|terms|, with the backward's two passes or its
+    fused pass."""
+    monkeypatch.setenv("FMOE_BWD_FUSED", "1" if bwd == "fused" else "0")
+    rng = np.random.default_rng(4242)
+    dts = [torch.float32, torch.bfloat16, torch.float16]
+    for case in range(16):
+        T = int(rng.choice([1, 3, 64, 500]))
+        E = int(rng.integers(1, 40))
+        N = int(rng.integers(1, 3000))
+        D = int(rng.choice([1, 5, 8, 33, 256, 1000]))
+        xdt = dts[int(rng.integers(3))]
+        gen = torch.Generator().manual_seed(900 + case)
+        cuts = np.sort(rng.integers(0, N + 1, E - 1))
+        sizes = np.diff(np.concatenate([[0], cuts, [N]])).tolist()
+        # one pool for every expert, each at a random element offset after the previous one
+        offs, cur = [], 0
+        for n in sizes:
+            cur += int(rng.integers(0, 9))
+            offs.append(cur)
+            cur += n * D
+        pool = torch.randn(cur + 1, generator=gen).to(xdt).to(DEV)
+        views = [pool[o: o + n * D].view(n, D) for o, n in zip(offs, sizes)]
+        experts = [v.cpu() for v in views]
+        idx = torch.from_numpy(rng.integers(0, T, N))
+        w = torch.rand(N, generator=gen)
+        idd, wd = idx.to(DEV), w.to(DEV).requires_grad_(True)
+        leaf = pool.clone()
+        xs = [leaf[o: o + n * D].view(n, D).requires_grad_(True) for o, n in zip(offs, sizes)]
+        label = f"case {case}: T={T} E={E} N={N} D={D} {xdt} offsets {offs[:4]}"
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idd, wd, (T, D))
+        want, acc, _ = oracle_fwd(experts, idx, w, T, xdt)
+        np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32
+                                      else want, err_msg=label)
+        # grad_out at an odd element offset with an odd row padding
+        go = torch.randn(T, D, generator=gen).to(xdt)
+        pad, o = int(rng.integers(1, 6)), int(rng.integers(1, 8))
+        gpool = torch.zeros(o + T * (D + pad), dtype=xdt, device=DEV)
+        god = gpool[o:].as_strided((T, D), (D + pad, 1))
+        god.copy_(go.to(DEV))
+        grads = torch.autograd.grad(out, [wd, *xs], god)
+        want_gx, want_gw = oracle_bwd(experts, idx, w, T, go)
+        got_gx = np.concatenate([to_np(g).reshape(-1, D) for g in grads[1:]])
+        np.testing.assert_array_equal(got_gx.view(want_gx.dtype), want_gx, err_msg=label)
+        scale = abs_dot(experts, idx, go, T)
+        err = np.abs(grads[0].double().cpu().numpy() - want_gw)
+        assert np.all(err <= 1e-6 * scale + 1e-30), label
+        # in place into an out view at an odd offset with padded rows: accumulates
+        odt = dts[int(rng.integers(3))]
+        prior = torch.randn(T, D, generator=gen).to(odt)
+        opool = torch.zeros(o + T * (D + pad), dtype=odt, device=DEV)
+        oview = opool[o:].as_strided((T, D), (D + pad, 1))
+        oview.copy_(prior.to(DEV))
+        fastmoe_amd.grouped_weighted_scatter_add(views, idd, wd.detach(), (T, D), out=oview,
+                                                 mode="det")
+        want_ip, _, _ = oracle_fwd(experts, idx, w, T, odt, acc_init=to_np(prior.float()).copy())
+        np.testing.assert_array_equal(bits(oview), want_ip.view(np.uint32)
+                                      if want_ip.dtype == np.float32 else want_ip, err_msg=label)
 
 
 def test_random_inplace_against_oracle():
