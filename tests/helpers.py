@@ -53,6 +53,17 @@ def abs_dot(experts, idx, grad_out, T):
     return out.numpy()
 
 
+def reorder_tol(n_terms: int, scale):
+    """Largest gap between two fp32 sums of the same n_terms values added in different orders.
+
+    Recursive summation of n terms in fp32 lies within (n-1) * u * sum|terms| of the exact sum,
+    u = 2^-24, to first order (Higham, Accuracy and Stability of Numerical Algorithms, 2nd ed.,
+    section 4.2); two different orders can therefore differ by twice that.  ``scale`` is
+    sum|terms| per element; the factor (1 + 2^-20) covers the second-order term.
+    """
+    return 2.0 * max(n_terms - 1, 1) * 2.0 ** -24 * (1.0 + 2.0 ** -20) * scale + 1e-30
+
+
 def abs_sum(experts, idx, w, T):
     """sum_g |w[g] * X[g, d]| per output element (scale of reordering error of a fp32 sum)."""
     D = experts[0].shape[1]

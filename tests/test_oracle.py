@@ -267,3 +267,28 @@ def test_pinning_checks_reject_planted_mistakes(mistake):
     np.testing.assert_array_equal(ok.view(np.uint32), good.view(np.uint32))
     bad = _Mutant.fwd(np_xs, idx.numpy(), w.numpy(), T, D, mistake)
     assert not np.array_equal(bad.view(np.uint32), good.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [3, 4, 8])
+def test_reorder_tolerance_covers_two_summation_orders(n):
+    """The tolerance the GPU tests allow between the atomic forward and the oracle: two fp32
+    sums of the same n terms in different orders.  Each order lies within (n-1) u sum|terms| of
+    the exact sum (u = 2^-24), so their gap can exceed that one-sided bound -- it does here for
+    3 terms -- and never exceeds twice it (reorder_tol)."""
+    from tests.helpers import reorder_tol
+
+    rng = np.random.default_rng(n)
+    M = 100_000
+    x = rng.standard_normal((M, n)).astype(np.float32)
+    perm = rng.permuted(np.tile(np.arange(n), (M, 1)), axis=1)
+    xp = np.take_along_axis(x, perm, 1)
+    s1 = np.zeros(M, np.float32)
+    s2 = np.zeros(M, np.float32)
+    for i in range(n):
+        s1 = s1 + x[:, i]
+        s2 = s2 + xp[:, i]
+    scale = np.abs(x.astype(np.float64)).sum(1)
+    gap = np.abs(s1.astype(np.float64) - s2.astype(np.float64))
+    assert np.all(gap <= reorder_tol(n, scale))
+    if n == 3:
+        assert np.any(gap > (n - 1) * 2.0 ** -24 * scale)
