@@ -284,7 +284,7 @@ constexpr int kTokBins = 4096;                         // bins per workgroup at 
 constexpr int kTokWaves = kScanThreads / kWave;        // 16
 constexpr int kTokStash = 8192;                        // stashed rows per workgroup
 constexpr int kTokWaveStash = kTokStash / kTokWaves;   // 512 per wave
-constexpr int kTokRows = 2048;                         // rows per workgroup aimed at
+constexpr int kTokRows = 256;                          // rows per workgroup aimed at
 constexpr int kTokGroups = 256;
 constexpr int kTokExperts = 4096;                      // int32 expert offsets staged in LDS
 constexpr int64_t kTokMaxRows = int64_t(1) << 20;      // every workgroup streams all of idx
