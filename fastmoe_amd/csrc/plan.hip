@@ -313,20 +313,50 @@ __device__ __forceinline__ void tok_write_rec(int v, int g, float wg, const int*
 }
 
 // Where the one-launch plan gets the expert table from.  TokMetaGlobal: the device arrays of
-// fmoe_build_metadata.  TokMetaArgs: the (address, rows) pairs in the kernel arguments (at most 256
-// experts); every workgroup scans the row counts itself and workgroup 0 also writes the
-// metadata outputs, so metadata and plan take one launch.
+// fmoe_build_metadata.  TokMetaArgs: the table in the kernel arguments (at most 256 experts),
+// prefixed on the host -- each expert's address and first packed row, and the largest row count --
+// so a workgroup only copies it into LDS; workgroup 0 also writes the metadata outputs, so
+// metadata and plan take one launch.
 struct TokMetaGlobal {
   const int64_t* ptr_table;
   const int64_t* offsets;
 };
+struct HostTable {
+  int64_t ptr[kMetaChunk];
+  int32_t off[kMetaChunk + 1];  // exclusive prefix of the row counts; off[count] = N < 2^31
+  int32_t count;
+  int32_t max_rows;
+};
 struct TokMetaArgs {
-  MetaChunk a;  // a.count experts from a.base = 0
+  HostTable a;
   int64_t* ptr_table;
   int32_t* chunk_sizes;
   int64_t* offsets;
   int32_t* max_rows;
 };
+static_assert(sizeof(TokMetaArgs) <= 3200, "kernel-argument table too large");
+
+// The host side of TokMetaArgs: E <= kMetaChunk (address, rows) pairs, rows in [0, 2^31) and
+// summing below 2^31 (checked by the callers).
+inline void fill_host_table(TokMetaArgs* m, const int64_t* host_ptrs, const int64_t* host_rows,
+                            int64_t E, int64_t* ptr_table, int32_t* chunk_sizes, int64_t* offsets,
+                            int32_t* max_rows) {
+  int64_t run = 0, mx = 0;
+  for (int i = 0; i < kMetaChunk; ++i) {
+    const int64_t n = i < E ? host_rows[i] : 0;
+    m->a.ptr[i] = i < E ? host_ptrs[i] : 0;
+    m->a.off[i] = (int32_t)run;
+    run += n;
+    mx = std::max(mx, n);
+  }
+  m->a.off[kMetaChunk] = (int32_t)run;
+  m->a.count = (int32_t)E;
+  m->a.max_rows = (int32_t)mx;
+  m->ptr_table = ptr_table;
+  m->chunk_sizes = chunk_sizes;
+  m->offsets = offsets;
+  m->max_rows = max_rows;
+}
 
 __device__ __forceinline__ void tok_load_meta(const TokMetaGlobal& m, int ne, int* off32,
                                               uint64_t* ptr_lds) {
@@ -338,24 +368,15 @@ __device__ __forceinline__ void tok_load_meta(const TokMetaGlobal& m, int ne, in
 __device__ __forceinline__ void tok_load_meta(const TokMetaArgs& m, int ne, int* off32,
                                               uint64_t* ptr_lds) {
   const int e = threadIdx.x;  // ne <= 256 < kScanThreads: one expert per thread
-  const int rows = e < ne ? m.a.rows[e] : 0;
-  const int64_t ptr = e < ne ? m.a.ptr[e] : 0;
-  int total;
-  const int excl = block_exclusive_scan_1024(rows, &total);
-  if (e < ne) {
-    off32[e] = excl;
-    ptr_lds[e] = (uint64_t)ptr;
-  }
-  if (e == 0) off32[ne] = total;
+  if (e <= ne) off32[e] = m.a.off[e];
+  if (e < ne) ptr_lds[e] = (uint64_t)m.a.ptr[e];
   if (blockIdx.x == 0) {  // workgroup-uniform: the metadata outputs (fmoe_build_metadata's)
     if (e < ne) {
-      m.ptr_table[e] = ptr;
-      m.chunk_sizes[e] = rows;
-      m.offsets[e] = excl;
+      m.ptr_table[e] = m.a.ptr[e];
+      m.chunk_sizes[e] = m.a.off[e + 1] - m.a.off[e];
     }
-    if (e == 0) m.offsets[ne] = total;
-    const int mx = block_max_1024(rows);
-    if (e == 0) *m.max_rows = mx;
+    if (e <= ne) m.offsets[e] = m.a.off[e];
+    if (e == 0) *m.max_rows = m.a.max_rows;
   }
 }
 
@@ -631,47 +652,25 @@ __device__ __forceinline__ void slots_load_meta(const TokMetaGlobal& m, int64_t 
 __device__ __forceinline__ uint64_t slots_ptr(const TokMetaGlobal& m, const uint64_t*, int64_t e) {
   return (uint64_t)m.ptr_table[e];
 }
-// E <= 256 == kGroup: one expert per thread; a workgroup scan of the row counts gives the
-// offsets, and workgroup 0 writes the metadata outputs (fmoe_build_metadata's).
+// E <= 256 == kGroup: one expert per thread copies the host-prefixed table into LDS, and
+// workgroup 0 writes the metadata outputs (fmoe_build_metadata's).
 __device__ __forceinline__ void slots_load_meta(const TokMetaArgs& m, int64_t E, int64_t* off_lds,
                                                 uint64_t* ptr_lds) {
-  __shared__ int wave_tot[kWavesPerGroup], wave_max[kWavesPerGroup];
-  const int e = threadIdx.x, lane = e & (kWave - 1), wv = e / kWave;
-  const int rows = e < E ? m.a.rows[e] : 0;
-  const int64_t ptr = e < E ? m.a.ptr[e] : 0;
-  int incl = rows, mx = rows;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) mx = max(mx, __shfl_xor(mx, d, kWave));
-  if (lane == kWave - 1) wave_tot[wv] = incl;
-  if (lane == 0) wave_max[wv] = mx;
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int i = 0; i < kWavesPerGroup; ++i) {
-    before += i < wv ? wave_tot[i] : 0;
-    total += wave_tot[i];
-    mx = max(mx, wave_max[i]);
-  }
-  const int excl = before + incl - rows;
+  const int e = threadIdx.x;
   if (e < E) {
-    off_lds[e] = excl;
-    ptr_lds[e] = (uint64_t)ptr;
+    off_lds[e] = m.a.off[e];
+    ptr_lds[e] = (uint64_t)m.a.ptr[e];
   }
-  if (e == 0) off_lds[E] = total;
+  if (e == 0) off_lds[E] = m.a.off[E];
   if (blockIdx.x == 0) {
     if (e < E) {
-      m.ptr_table[e] = ptr;
-      m.chunk_sizes[e] = rows;
-      m.offsets[e] = excl;
+      m.ptr_table[e] = m.a.ptr[e];
+      m.chunk_sizes[e] = m.a.off[e + 1] - m.a.off[e];
+      m.offsets[e] = m.a.off[e];
     }
     if (e == 0) {
-      m.offsets[E] = total;
-      *m.max_rows = mx;
+      m.offsets[E] = m.a.off[E];
+      *m.max_rows = m.a.max_rows;
     }
   }
 }
@@ -915,18 +914,8 @@ extern "C" int fmoe_build_metadata_and_plan(
                "fmoe_build_metadata_and_plan: workspace not 256B-aligned");
   FMOE_REQUIRE(row_bytes > 0, "fmoe_build_metadata_and_plan: row_bytes must be > 0");
   TokMetaArgs meta;
-  meta.a.count = (int32_t)E;
-  meta.a.base = 0;
-  meta.a.scan = 1;
-  meta.a.pad = 0;
-  for (int i = 0; i < kMetaChunk; ++i) {
-    meta.a.ptr[i] = i < E ? host_ptrs[i] : 0;
-    meta.a.rows[i] = i < E ? (int32_t)host_rows[i] : 0;
-  }
-  meta.ptr_table = d_ptr_table;
-  meta.chunk_sizes = d_chunk_sizes;
-  meta.offsets = d_offsets;
-  meta.max_rows = d_max_rows;
+  fill_host_table(&meta, host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes, d_offsets,
+                  d_max_rows);
   const PlanLayout L = plan_layout(N, T);
   char* ws = static_cast<char*>(d_workspace);
   return launch_plan_tok(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
@@ -1039,18 +1028,8 @@ extern "C" int fmoe_build_metadata_and_plan_from_slots(
                                 row_bytes, d_workspace))
     return rc;
   TokMetaArgs meta;
-  meta.a.count = (int32_t)E;
-  meta.a.base = 0;
-  meta.a.scan = 1;
-  meta.a.pad = 0;
-  for (int i = 0; i < kMetaChunk; ++i) {
-    meta.a.ptr[i] = i < E ? host_ptrs[i] : 0;
-    meta.a.rows[i] = i < E ? (int32_t)host_rows[i] : 0;
-  }
-  meta.ptr_table = d_ptr_table;
-  meta.chunk_sizes = d_chunk_sizes;
-  meta.offsets = d_offsets;
-  meta.max_rows = d_max_rows;
+  fill_host_table(&meta, host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes, d_offsets,
+                  d_max_rows);
   return launch_from_slots(meta, d_slot_pos, num_tokens, top_k, d_weights, w_dtype, E, N,
                            row_bytes, d_workspace, static_cast<hipStream_t>(stream), who);
 }
