@@ -106,6 +106,37 @@ def test_combine_entry_points_reject_bad_arguments():
     assert rc == _abi.EINVAL
 
 
+def test_metadata_and_plan_entry_points_reject_bad_arguments():
+    """The one-call metadata + plan entry points check every argument on the host, including row
+    totals that the kernel-argument table (32-bit offsets) cannot hold."""
+    lib = _abi.lib()
+    dev, ws = 0x10000, 0x10000 * 256
+    ptrs = (ctypes.c_int64 * 2)(0x1000, 0x2000)
+
+    def from_slots(rows, T, k):
+        r = (ctypes.c_int64 * 2)(*rows)
+        return lib.fmoe_build_metadata_and_plan_from_slots(ptrs, r, 2, dev, dev, dev, dev, dev, T,
+                                                           k, dev, _abi.F32, 32, ws, None)
+
+    # rows that each fit but sum to 2^31: not the T*k rows of the slot map
+    assert from_slots([1 << 30, 1 << 30], 4, 2) == _abi.EINVAL
+    assert b"slot" in lib.fmoe_last_error()
+    assert from_slots([4, 4], 4, 65) == _abi.EINVAL            # top_k above 64
+    assert from_slots([1 << 30, 1 << 30], 1 << 29, 4) == _abi.ERANGE   # T*k of 2^31
+    assert from_slots([4, -1], 4, 2) == _abi.EINVAL
+
+    def meta_plan(rows, idx_dtype=_abi.I64, p0=0x1000):
+        r = (ctypes.c_int64 * 2)(*rows)
+        pp = (ctypes.c_int64 * 2)(p0, 0x2000)
+        return lib.fmoe_build_metadata_and_plan(pp, r, 2, dev, dev, dev, dev, dev, idx_dtype, dev,
+                                                _abi.F32, 8, 32, ws, None)
+
+    assert meta_plan([3, 4], p0=0) == _abi.EINVAL               # rows at a null address
+    assert b"null address" in lib.fmoe_last_error()
+    assert meta_plan([3, 4], idx_dtype=_abi.F32) == _abi.EINVAL  # float indices
+    assert meta_plan([3, -4]) == _abi.EINVAL
+
+
 def test_invert_scatter_index_rejects_bad_arguments():
     lib = _abi.lib()
     dev = 0x10000
