@@ -153,6 +153,85 @@ __device__ __forceinline__ void bwd_row_body(uint64_t src, float wt, uint32_t t,
 }
 
 constexpr int kBwdWaves = FMOE_BWD_WAVES;
+#ifndef FMOE_GW_STAGE_STEPS
+#define FMOE_GW_STAGE_STEPS 4  // column steps of grad_out per LDS slice (one barrier per slice)
+#endif
+
+// grad_w pass of a token with at most kBwdWaves rows, grad_out staged in LDS: per slice of
+// FMOE_GW_STAGE_STEPS column steps the workgroup reads that part of grad_out[t] once (one 16-byte
+// vector per thread per step), and every wave takes it from LDS instead of fetching the same bytes
+// from L2 (the per-wave path reads grad_out once per row).  Double-buffered: the next slice's
+// loads are in flight while a slice is consumed, and one barrier per slice both publishes a slice
+// and frees the other buffer.  The products and their accumulation order are those of
+// bwd_row_body, so grad_w is bit-identical to it.
+template <typename TX, int V, int U>
+__device__ __forceinline__ void bwd_gw_staged(const Rec* __restrict__ rec, int beg, int cnt,
+                                              uint32_t t, const TX* __restrict__ gout,
+                                              int64_t gstride, void* __restrict__ gw,
+                                              int gw_dtype, uint32_t D) {
+  using VX = Vec<TX, V>;
+  using raw_t = typename VX::raw_t;
+  constexpr int CW = kWave * V * U;
+  constexpr int kStepVecs = 2 * U * kWave;  // 16-byte vectors of grad_out per column step
+  static_assert(kStepVecs == kBwdWaves * kWave, "one staging vector per thread per step");
+  constexpr int S = FMOE_GW_STAGE_STEPS;  // column steps per slice
+  __shared__ raw_t stage[2][S * kStepVecs];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = uniform(tid / kWave);
+  const bool has = wave < cnt;  // wave-uniform
+  const uint32_t rowb = D * (uint32_t)sizeof(TX);
+  const rsrc_t rg = make_rsrc(gout + (int64_t)t * gstride, rowb);
+  Rec r{};
+  if (has) r = rec[beg + wave];
+  const rsrc_t rx = make_rsrc(has ? r.src : (uint64_t)(uintptr_t)gout, rowb);
+  constexpr uint32_t kStepBytes = (uint32_t)kStepVecs * 16;
+  constexpr uint32_t kSliceBytes = S * kStepBytes;
+  const uint32_t slices = (D + S * 2 * CW - 1) / (S * 2 * CW);
+#pragma unroll
+  for (int q = 0; q < S; ++q)
+    stage[0][q * kStepVecs + tid] =
+        VX::template ld<FMOE_GOUT_CPOL>(rg, (uint32_t)(q * kStepVecs + tid) * 16);
+  // X of column step q of slice sl, for this wave's row
+  auto load_step = [&](uint32_t sl, int q, raw_t (&xr)[2][U]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        xr[h][u] = load_x<TX, V, true>(rx, sl * kSliceBytes + (uint32_t)q * kStepBytes +
+                                               (uint32_t)((h * U + u) * kWave + lane) * 16);
+  };
+  double part = 0.0;
+  for (uint32_t sl = 0; sl < slices; ++sl) {
+    raw_t xr[S][2][U];
+    if (has) load_step(sl, 0, xr[0]);  // in flight across the barrier
+    // the next slice (past the row: zeros from the range check, no memory traffic)
+    raw_t nxt[S];
+#pragma unroll
+    for (int q = 0; q < S; ++q)
+      nxt[q] = VX::template ld<FMOE_GOUT_CPOL>(
+          rg, (sl + 1) * kSliceBytes + (uint32_t)(q * kStepVecs + tid) * 16);
+    __syncthreads();  // slice sl is in LDS; every wave is done with the other buffer
+#pragma unroll
+    for (int q = 0; q < S; ++q) {
+      if (has) {
+        if (q + 1 < S) load_step(sl, q + 1, xr[(q + 1) % S]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            part += dot_partial<TX, V>(xr[q][h][u],
+                                       stage[sl & 1][q * kStepVecs + (h * U + u) * kWave + lane]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < S; ++q) stage[(sl + 1) & 1][q * kStepVecs + tid] = nxt[q];
+  }
+  if (has) {
+    const double tot = wave_sum(part);
+    if (lane == 0) store_gate(gw, gw_dtype, r.g, tot);
+  }
+}
 
 // Workgroup per plan segment: token t = blockIdx.x; segment T holds the out-of-range rows.
 template <typename TX, int V, int U, bool GX, bool GW>
@@ -169,6 +248,12 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_bwd_tok(const int32_t* __
   const bool al = !(V > 1 && status[kStatusMisaligned] != 0);
   const int beg = row_ptr[t];
   const int end = row_ptr[t + 1];
+  if constexpr (GW && !GX && V > 1 && 2 * U == kBwdWaves) {
+    if (t < T && al && end - beg <= kBwdWaves) {  // workgroup-uniform
+      if (end > beg) bwd_gw_staged<TX, V, U>(rec, beg, end - beg, t, gout, gstride, gw, gw_dtype, D);
+      return;
+    }
+  }
   for (int j = beg + wave; j < end; j += kBwdWaves) {
     const Rec r = rec[j];
     if (t == T) {
