@@ -242,14 +242,14 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_bwd_tok(const int32_t* __
                                                                int64_t gstride,
                                                                TX* __restrict__ gx,
                                                                void* __restrict__ gw, int gw_dtype,
-                                                               uint32_t D, uint32_t T) {
+                                                               uint32_t D, uint32_t T, int staged) {
   const uint32_t t = blockIdx.x;
   const int wave = uniform(threadIdx.x / kWave);
   const bool al = !(V > 1 && status[kStatusMisaligned] != 0);
   const int beg = row_ptr[t];
   const int end = row_ptr[t + 1];
   if constexpr (GW && !GX && V > 1 && 2 * U == kBwdWaves) {
-    if (t < T && al && end - beg <= kBwdWaves) {  // workgroup-uniform
+    if (staged && t < T && al && end - beg <= kBwdWaves) {  // workgroup-uniform
       if (end > beg) bwd_gw_staged<TX, V, U>(rec, beg, end - beg, t, gout, gstride, gw, gw_dtype, D);
       return;
     }
@@ -282,6 +282,7 @@ struct BwdArgs {
   void* gx;
   void* gw;
   int gw_dtype;
+  int gw_staged;  // grad_w pass: grad_out shared through LDS (FMOE_GW_STAGED=0 turns it off)
   int64_t D, T;
   hipStream_t s;
 };
@@ -291,7 +292,7 @@ static int launch_bwd_k(const BwdArgs& a) {
   hipLaunchKernelGGL((k_bwd_tok<TX, V, U, GX, GW>), dim3((unsigned)(a.T + 1)),
                      dim3(kBwdWaves * kWave), 0, a.s, a.status, a.row_ptr, a.rec,
                      static_cast<const TX*>(a.gout), a.gstride, static_cast<TX*>(a.gx), a.gw,
-                     a.gw_dtype, (uint32_t)a.D, (uint32_t)a.T);
+                     a.gw_dtype, (uint32_t)a.D, (uint32_t)a.T, a.gw_staged);
   return fmoe_host::check_launch("fmoe_combine_bwd");
 }
 
@@ -363,6 +364,7 @@ extern "C" int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t nu
   a.gx = d_grad_x;
   a.gw = d_grad_w;
   a.gw_dtype = gw_dtype;
+  a.gw_staged = env_int_b("FMOE_GW_STAGED", 1) != 0;
   a.D = D;
   a.T = T;
   a.s = static_cast<hipStream_t>(stream);

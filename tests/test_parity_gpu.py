@@ -131,6 +131,37 @@ def test_bwd_grad_x_bitexact_grad_w_close(name, variant, monkeypatch):
     assert gw.dtype == wd.dtype
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 16384), (torch.float32, 4104),
+                                     (torch.float16, 8200)])
+def test_bwd_grad_w_staged_equals_per_wave(dtype, D, monkeypatch):
+    """The grad_w pass shares grad_out through LDS for tokens of 1-8 rows and reads it per wave
+    otherwise (longer segments, the out-of-range segment, or FMOE_GW_STAGED=0): both give the same
+    bits, and both meet the oracle's 1e-6 bar.  Row lengths are not multiples of the LDS slice."""
+    rng = np.random.default_rng(17)
+    T, E = 300, 37
+    per_token = rng.integers(0, 13, T)          # 0..12 rows: both paths occur
+    idx = np.repeat(np.arange(T), per_token)
+    idx[:: 29] = T + 3                           # out of range: the per-wave zero path
+    idx = torch.from_numpy(idx[rng.permutation(idx.size)])
+    N = idx.numel()
+    gen = torch.Generator().manual_seed(18)
+    sizes = np.diff(np.concatenate([[0], np.sort(rng.integers(0, N + 1, E - 1)), [N]])).tolist()
+    experts = [torch.randn(n, D, generator=gen).to(dtype) for n in sizes]
+    w = torch.rand(N, generator=gen)
+    go = torch.randn(T, D, generator=gen).to(dtype)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    got = {}
+    for staged in ("1", "0"):
+        monkeypatch.setenv("FMOE_GW_STAGED", staged)
+        wg = wd.clone().requires_grad_(True)
+        out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wg, (T, D))
+        (got[staged],) = torch.autograd.grad(out, [wg], go.to(DEV))
+    np.testing.assert_array_equal(bits(got["1"]), bits(got["0"]))
+    _, want_gw = oracle_bwd(experts, idx, w, T, go)
+    scale = abs_dot(experts, idx, go, T)
+    assert np.all(np.abs(got["1"].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
 @pytest.mark.parametrize("fused", ["0", "1"])
 def test_bwd_abi_both_outputs_in_one_call(fused, monkeypatch):
     """fmoe_combine_bwd given both outputs (the call a C-ABI binding makes): grad_X and grad_w
