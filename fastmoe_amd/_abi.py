@@ -61,6 +61,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_int, _c_vp, _c_int, _c_i64, _c_int, _c_vp],
     ),
+    "fmoe_combine_fwd_noalloc": (
+        _c_int,
+        [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_int, _c_vp, _c_int,
+         _c_i64, _c_i64, _c_int, _c_vp, _c_int, _c_i64, _c_int, _c_vp],
+    ),
     "fmoe_combine_bwd": (
         _c_int,
         [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _c_int, _c_i64, _c_vp, _c_vp, _c_int, _c_vp],

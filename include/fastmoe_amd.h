@@ -205,6 +205,29 @@ FMOE_API int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indice
                      int64_t out_row_stride, int accumulate, void* stream);
 
 /*
+ * Allocation-free deterministic forward.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  It computes what fmoe_build_metadata_and_plan followed by
+ * fmoe_combine_fwd(FMOE_MODE_DET, ...) compute, bit for bit, but the metadata arrays and the plan
+ * live in a static device buffer of FMOE_NOALLOC_SCRATCH_BYTES that the library holds on every
+ * GPU it runs on until the process ends; the caller passes only inputs and the output, and the
+ * call allocates nothing.
+ *
+ * Limits: 1 <= num_experts <= 4096 and fmoe_plan_workspace_bytes(N, T) <= 16 MiB - 128 KiB, i.e.
+ * roughly 32 * N + 8 * T bytes (N = sum of host_rows; e.g. N = 2^18 rows with T = 2^18 tokens).
+ * Larger calls return FMOE_ERANGE before touching the GPU.
+ * Calls on one GPU share its buffer: calls that overlap on one GPU (two streams, two threads)
+ * race; calls on one stream are ordered.  Arguments as in fmoe_build_metadata_and_plan and
+ * fmoe_combine_fwd.
+ */
+#define FMOE_NOALLOC_SCRATCH_BYTES (16 << 20)
+FMOE_API int fmoe_combine_fwd_noalloc(const int64_t* host_ptrs, const int64_t* host_rows,
+                             int64_t num_experts, const void* d_indices, int idx_dtype,
+                             const void* d_weights, int w_dtype, int64_t num_tokens,
+                             int64_t hidden, int x_dtype, void* d_out, int out_dtype,
+                             int64_t out_row_stride, int accumulate, void* stream);
+
+/*
  * Backward combine (replaces GroupedWeightedScatterAdd.backward, src/fastmoe/kernels/ops.py:333-359,
  * and adds the gate gradient that the reference leaves out at :358-359).
  *

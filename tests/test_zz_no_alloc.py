@@ -1,0 +1,149 @@
+"""fmoe_combine_fwd_noalloc (the allocation-free deterministic forward) against the entry points it
+stands for, fmoe_build_metadata_and_plan + fmoe_combine_fwd(det), called through the C ABI.
+
+The bar is bit equality (the same kernels on the same inputs), and the oracle on top.  Two calls
+in a row, the second smaller, check that nothing left in the shared static buffer by the first call
+leaks into the second.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from fastmoe_amd import _abi
+from fastmoe_amd.workloads import Workload, make_experts, make_routing
+from tests.helpers import bits, oracle_fwd
+
+CODE = {torch.float32: _abi.F32, torch.bfloat16: _abi.BF16, torch.float16: _abi.F16}
+ICODE = {torch.int64: _abi.I64, torch.int32: _abi.I32}
+SCRATCH_BYTES = 16 << 20
+
+
+def _case(T, D, E, k, dtype, seed, idx_dtype=torch.int64):
+    wl = Workload(f"noalloc{seed}", T, D, E, k, dtype, seed, False)
+    idx, w, counts = make_routing(wl)
+    xs_cpu = make_experts(counts, D, dtype, "cpu", seed)
+    dev = torch.device("cuda:0")
+    return dict(T=T, D=D, xs_cpu=xs_cpu, idx_cpu=idx, w_cpu=w,
+                xs=[x.to(dev) for x in xs_cpu], idx=idx.to(idx_dtype).to(dev), w=w.to(dev))
+
+
+def _as_bits(a: np.ndarray) -> np.ndarray:
+    """Oracle output as bit patterns (fp32 values -> uint32; 16-bit outputs are bits already)."""
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def _table(xs):
+    E = len(xs)
+    ptrs = (ctypes.c_int64 * E)(*[x.data_ptr() if x.shape[0] else 0 for x in xs])
+    rows = (ctypes.c_int64 * E)(*[x.shape[0] for x in xs])
+    return ptrs, rows, E
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _noalloc(c, out, accumulate):
+    lib = _abi.lib()
+    ptrs, rows, E = _table(c["xs"])
+    rc = lib.fmoe_combine_fwd_noalloc(
+        ptrs, rows, E, c["idx"].data_ptr(), ICODE[c["idx"].dtype], c["w"].data_ptr(),
+        CODE[c["w"].dtype], c["T"], c["D"], CODE[c["xs"][0].dtype], out.data_ptr(),
+        CODE[out.dtype], out.stride(0), accumulate, _stream())
+    _abi.check(rc, "fmoe_combine_fwd_noalloc")
+
+
+def _with_workspace(c, out, accumulate):
+    """The existing entry points, with caller-allocated metadata arrays and plan workspace."""
+    lib = _abi.lib()
+    dev = out.device
+    ptrs, rows, E = _table(c["xs"])
+    N = sum(x.shape[0] for x in c["xs"])
+    T, D = c["T"], c["D"]
+    ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
+    chunk = torch.empty(E, dtype=torch.int32, device=dev)
+    offs = torch.empty(E + 1, dtype=torch.int64, device=dev)
+    mx = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, T), dtype=torch.uint8, device=dev)
+    xdt = c["xs"][0].dtype
+    rc = lib.fmoe_build_metadata_and_plan(
+        ptrs, rows, E, ptr_table.data_ptr(), chunk.data_ptr(), offs.data_ptr(), mx.data_ptr(),
+        c["idx"].data_ptr(), ICODE[c["idx"].dtype], c["w"].data_ptr(), CODE[c["w"].dtype], T,
+        D * c["xs"][0].element_size(), ws.data_ptr(), _stream())
+    _abi.check(rc, "fmoe_build_metadata_and_plan")
+    rc = lib.fmoe_combine_fwd(_abi.MODE_DET, ws.data_ptr(), None, _abi.I64, None, _abi.F32,
+                              ptr_table.data_ptr(), offs.data_ptr(), E, N, T, D, CODE[xdt],
+                              out.data_ptr(), CODE[out.dtype], out.stride(0), accumulate,
+                              _stream())
+    _abi.check(rc, "fmoe_combine_fwd")
+    return ws  # kept alive until the caller synchronises
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_equals_workspace_entry_points_two_calls_second_smaller(out_dtype):
+    print(f"noalloc: two calls, out {out_dtype}", flush=True)
+    big = _case(1024, 2048, 64, 6, torch.bfloat16, 11)
+    small = _case(96, 520, 8, 2, torch.bfloat16, 12)  # D % 8 == 0, narrower rows, fewer experts
+    dev = big["xs"][0].device
+    want = []
+    keep = []
+    for c in (big, small):
+        o = torch.full((c["T"], c["D"]), 7.0, dtype=out_dtype, device=dev)
+        keep.append(_with_workspace(c, o, 0))
+        want.append(o)
+    got = []
+    for c in (big, small):  # back to back on one stream: the second reuses the first's scratch
+        o = torch.full((c["T"], c["D"]), -3.0, dtype=out_dtype, device=dev)
+        _noalloc(c, o, 0)
+        got.append(o)
+    torch.cuda.synchronize()
+    for c, g, wnt in zip((big, small), got, want):
+        assert np.array_equal(bits(g), bits(wnt))
+        exp, _, _ = oracle_fwd(c["xs_cpu"], c["idx_cpu"], c["w_cpu"], c["T"], out_dtype)
+        assert np.array_equal(bits(g), _as_bits(exp))
+
+
+@pytest.mark.gpu
+def test_noalloc_accumulates_into_padded_out_with_int32_indices():
+    print("noalloc: accumulate, padded fp32 out, int32 indices", flush=True)
+    big = _case(700, 1000, 40, 4, torch.bfloat16, 13, torch.int32)
+    small = _case(33, 1000, 5, 3, torch.bfloat16, 14, torch.int32)
+    dev = big["xs"][0].device
+    gen = torch.Generator(device=dev).manual_seed(5)
+    for c in (big, small):
+        base = torch.randn(c["T"], c["D"] + 24, device=dev, generator=gen)
+        a = base.clone()[:, : c["D"]]
+        b = base.clone()[:, : c["D"]]
+        ws = _with_workspace(c, a, 1)
+        _noalloc(c, b, 1)
+        torch.cuda.synchronize()
+        del ws
+        assert np.array_equal(bits(a), bits(b))
+        init = base[:, : c["D"]].contiguous().cpu().numpy()
+        exp, _, _ = oracle_fwd(c["xs_cpu"], c["idx_cpu"], c["w_cpu"], c["T"], torch.float32,
+                               acc_init=init)
+        assert np.array_equal(bits(b), _as_bits(exp))
+
+
+def test_noalloc_rejects_sizes_beyond_the_static_buffer():
+    """Host-side checks only: they return before any HIP call (no GPU needed)."""
+    lib = _abi.lib()
+    E = 4
+    ptrs = (ctypes.c_int64 * E)(0x1000, 0x2000, 0x3000, 0x4000)
+    n = 300_000  # 4 * 300k rows: ~38 MB of plan records, beyond the 16 MiB buffer
+    rows = (ctypes.c_int64 * E)(n, n, n, n)
+    dev = 0x10000  # never dereferenced
+    rc = lib.fmoe_combine_fwd_noalloc(ptrs, rows, E, dev, _abi.I64, dev, _abi.F32, 1000, 64,
+                                      _abi.F32, dev, _abi.F32, 64, 0, None)
+    assert rc == _abi.ERANGE
+    msg = lib.fmoe_last_error().decode()
+    assert "static scratch" in msg and str(4 * n) in msg
+    assert lib.fmoe_plan_workspace_bytes(4 * n, 1000) > SCRATCH_BYTES
+    rc = lib.fmoe_combine_fwd_noalloc(ptrs, rows, 5000, dev, _abi.I64, dev, _abi.F32, 1000, 64,
+                                      _abi.F32, dev, _abi.F32, 64, 0, None)
+    assert rc == _abi.EINVAL
