@@ -6,6 +6,7 @@ but the gfx950 kernels.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 from pathlib import Path
@@ -27,6 +28,8 @@ _c_vp = ctypes.c_void_p
 SIGNATURES: dict[str, tuple] = {
     "fmoe_abi_version": (_c_int, []),
     "fmoe_last_error": (ctypes.c_char_p, []),
+    "fmoe_set_option": (_c_int, [ctypes.c_char_p, _c_i64, ctypes.POINTER(_c_i64)]),
+    "fmoe_get_option": (_c_int, [ctypes.c_char_p, ctypes.POINTER(_c_i64)]),
     "fmoe_build_metadata": (
         _c_int,
         [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp],
@@ -124,3 +127,38 @@ def check(rc: int, what: str) -> None:
         if kind is FastMoEError:
             raise FastMoEError(f"{what}: status {rc}: {msg}")
         raise kind(f"{what}: {msg}")
+
+
+# Mirror of the library's kernel-variant options (fmoe_set_option), so that host code can read an
+# option without a library call.  Filled on first read; kept in step by set_option().
+_OPTS: dict[str, int] = {}
+
+
+def option(name: str) -> int:
+    """Current value of a kernel-variant option (see fmoe_set_option in the header)."""
+    if name not in _OPTS:
+        v = ctypes.c_int64()
+        check(lib().fmoe_get_option(name.encode(), ctypes.byref(v)), "fmoe_get_option")
+        _OPTS[name] = v.value
+    return _OPTS[name]
+
+
+def set_option(name: str, value: int) -> int:
+    """Set a kernel-variant option; returns its previous value."""
+    prev = ctypes.c_int64()
+    check(lib().fmoe_set_option(name.encode(), int(value), ctypes.byref(prev)), "fmoe_set_option")
+    _OPTS[name] = int(value)
+    return prev.value
+
+
+@contextlib.contextmanager
+def options(**values):
+    """Set kernel-variant options for the duration of a ``with`` block (e.g. ``plan=1``)."""
+    prev = {}
+    try:
+        for k, v in values.items():
+            prev[k] = set_option(k, v)
+        yield
+    finally:
+        for k, v in prev.items():
+            set_option(k, v)

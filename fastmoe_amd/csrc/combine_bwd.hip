@@ -268,11 +268,6 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_bwd_tok(const int32_t* __
   }
 }
 
-static int env_int_b(const char* name, int dflt) {
-  const char* s = getenv(name);
-  return (s && *s) ? atoi(s) : dflt;
-}
-
 struct BwdArgs {
   const int32_t* status;
   const int32_t* row_ptr;
@@ -282,7 +277,7 @@ struct BwdArgs {
   void* gx;
   void* gw;
   int gw_dtype;
-  int gw_staged;  // grad_w pass: grad_out shared through LDS (FMOE_GW_STAGED=0 turns it off)
+  int gw_staged;  // grad_w pass: grad_out shared through LDS (option "gw_staged" = 0 turns it off)
   int64_t D, T;
   hipStream_t s;
 };
@@ -296,11 +291,11 @@ static int launch_bwd_k(const BwdArgs& a) {
   return fmoe_host::check_launch("fmoe_combine_bwd");
 }
 
-// FMOE_BWD_FUSED=1 runs both gradients in one pass (kept for measurement).
+// The "bwd_fused" option runs both gradients in one pass (kept for measurement).
 template <typename TX, int V, int U>
 static int launch_bwd_u(const BwdArgs& a) {
   if (a.gx && a.gw) {
-    if (env_int_b("FMOE_BWD_FUSED", 0)) return launch_bwd_k<TX, V, U, true, true>(a);
+    if (fmoe_host::opt(fmoe_host::kOptBwdFused)) return launch_bwd_k<TX, V, U, true, true>(a);
     if (int rc = launch_bwd_k<TX, V, U, true, false>(a)) return rc;  // grad_X: write pass
     return launch_bwd_k<TX, V, U, false, true>(a);                   // grad_w: read pass
   }
@@ -308,16 +303,17 @@ static int launch_bwd_u(const BwdArgs& a) {
   return launch_bwd_k<TX, V, U, false, true>(a);
 }
 
-// U 16-byte vectors per lane per column step: 4 unless D is small (FMOE_BWD_U=1|2|4 overrides).
+// U 16-byte vectors per lane per column step: 4 unless D is small (option "bwd_u" = 1|2|4
+// overrides).
 template <typename TX>
 static int launch_bwd_x(const BwdArgs& a) {
   constexpr int V = vec16<TX>();
   const int eb = (int)sizeof(TX);
   const bool vec_ok = (a.D % V == 0) && ((uintptr_t)a.gout % 16 == 0) &&
                       ((a.gstride * eb) % 16 == 0) && ((uintptr_t)a.gx % 16 == 0) &&
-                      env_int_b("FMOE_FORCE_SCALAR", 0) == 0;
+                      fmoe_host::opt(fmoe_host::kOptForceScalar) == 0;
   if (!vec_ok) return launch_bwd_u<TX, 1, 4>(a);
-  int U = env_int_b("FMOE_BWD_U", 0);
+  int U = (int)fmoe_host::opt(fmoe_host::kOptBwdU);
   if (U != 1 && U != 2 && U != 4)
     U = a.D >= (int64_t)kWave * V * 4 * 2 ? 4 : (a.D >= (int64_t)kWave * V * 2 * 2 ? 2 : 1);
   if (U == 4) return launch_bwd_u<TX, V, 4>(a);
@@ -364,7 +360,7 @@ extern "C" int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t nu
   a.gx = d_grad_x;
   a.gw = d_grad_w;
   a.gw_dtype = gw_dtype;
-  a.gw_staged = env_int_b("FMOE_GW_STAGED", 1) != 0;
+  a.gw_staged = fmoe_host::opt(fmoe_host::kOptGwStaged) != 0;
   a.D = D;
   a.T = T;
   a.s = static_cast<hipStream_t>(stream);

@@ -217,15 +217,10 @@ __global__ __launch_bounds__(kGroup) void k_fwd_atomic(
 }
 
 // ---- host dispatch ---------------------------------------------------------------------------
-static int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  return (s && *s) ? atoi(s) : dflt;
-}
-
 // Vectors per lane per row: several 16-byte loads in flight per row, and preferably a chunk
 // width that divides D (no tail predication), while small D still spreads over many waves.
-static int pick_u(int64_t D, int V, const char* env) {
-  const int forced = env_int(env, 0);
+static int pick_u(int64_t D, int V) {
+  const int forced = (int)fmoe_host::opt(fmoe_host::kOptFwdDetU);
   if (forced == 1 || forced == 2 || forced == 4) return forced;
   for (int u = 4; u >= 1; u >>= 1) {
     const int64_t cw = (int64_t)kWave * V * u;
@@ -269,7 +264,7 @@ static int launch_fwd_k(const FwdArgs& a, int64_t chunks) {
   unsigned blocks;
   if (a.mode == FMOE_MODE_DET) {
     if (int rc = grid_for(a.T * chunks, "fmoe_combine_fwd(det)", &blocks)) return rc;
-    const int persist = env_int("FMOE_FWD_GRID", 0);  // workgroups; 0 = one wave per unit
+    const int persist = (int)fmoe_host::opt(fmoe_host::kOptFwdGrid);  // 0 = one wave per unit
     if (persist > 0 && (unsigned)persist < blocks) blocks = (unsigned)persist;
     hipLaunchKernelGGL((k_fwd_det<TX, TO, V, U, RB>), dim3(blocks), dim3(kGroup), 0, a.s, a.status,
                        a.row_ptr, a.rec, static_cast<TO*>(a.out), a.out_stride, (uint32_t)a.D,
@@ -299,17 +294,18 @@ static int launch_fwd_u(const FwdArgs& a) {
   return launch_fwd_k<TX, TO, V, U, RB>(a, chunks);
 }
 
-// Tile shapes (U vectors per lane per row, R rows per batch).  FMOE_FWD_TILE=<U><R> (e.g. "44")
-// overrides the choice for tuning.
+// Tile shapes (U vectors per lane per row, R rows per batch).  The "fwd_tile" option <U><R> (e.g.
+// 44) overrides the choice for tuning.
 template <typename TX, typename TO, int V>
 static int launch_fwd_v(const FwdArgs& a) {
   if constexpr (V == 1) {
     return launch_fwd_u<TX, TO, 1, 4, 4>(a);
   } else {
-    const int tile = env_int(a.mode == FMOE_MODE_DET ? "FMOE_FWD_TILE" : "FMOE_FWD_ATOMIC_TILE", 0);
+    const int tile = (int)fmoe_host::opt(a.mode == FMOE_MODE_DET ? fmoe_host::kOptFwdTile
+                                                                 : fmoe_host::kOptFwdAtomicTile);
     int U = tile / 10, R = tile % 10;
     if (!((U == 4 && R == 4) || (U == 2 && (R == 8 || R == 4)) || (U == 1 && R == 8))) {
-      U = pick_u(a.D, V, "FMOE_FWD_DET_U");
+      U = pick_u(a.D, V);
       R = U >= 4 ? 4 : 8;
     }
     if (U == 4) return launch_fwd_u<TX, TO, V, 4, 4>(a);
@@ -325,7 +321,7 @@ static int launch_fwd_t(const FwdArgs& a) {
   const int ob = (int)sizeof(TO) == 4 ? 4 : 2;
   const int64_t vb = (int64_t)V * ob;  // bytes of one output vector
   const bool vec_ok = (a.D % V == 0) && ((uintptr_t)a.out % vb == 0) &&
-                      ((a.out_stride * ob) % vb == 0) && env_int("FMOE_FORCE_SCALAR", 0) == 0;
+                      ((a.out_stride * ob) % vb == 0) && fmoe_host::opt(fmoe_host::kOptForceScalar) == 0;
   if (vec_ok) return launch_fwd_v<TX, TO, V>(a);
   return launch_fwd_v<TX, TO, 1>(a);
 }

@@ -1,0 +1,165 @@
+// Plan internals shared by the plan builders (plan.hip, plan_bucket.hip): the workspace layout,
+// the bucketed plan's geometry and the expert-table sources.
+#pragma once
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace fmoe {
+
+constexpr int kScanThreads = 1024;
+
+// ---- bucketed plan geometry -------------------------------------------------------------------
+// The T + 1 token bins (bin T: out-of-range rows) are grouped into buckets of 2^shift consecutive
+// bins; the rows are partitioned by bucket in slices of S rows (k_plan_part), then each bucket is
+// ordered by one wave (k_plan_bucket).
+constexpr int kPartThreads = 1024;
+constexpr int kPartWaves = kPartThreads / kWave;  // 16
+constexpr int kMaxBuckets = 1024;                 // bucket ids fit 10 bits
+constexpr int kMaxBucketBins = 4096;              // bins per bucket (one wave's LDS counters)
+constexpr int kMaxSlices = 512;                   // partition slices
+constexpr int64_t kBucketRows = 128;              // rows per bucket aimed at
+constexpr int64_t kMinSlice = 2048;               // rows per slice at least (multiple of 1024)
+
+struct PlanGeom {
+  int64_t S;   // rows per slice, a multiple of kPartThreads
+  int G1;      // slices (>= 1)
+  int shift;   // log2(bins per bucket)
+  int nbk;     // buckets
+  bool ok;     // within the bucketed plan's limits (else the three-launch plan)
+};
+
+__host__ __device__ inline PlanGeom plan_geom(int64_t N, int64_t T) {
+  PlanGeom g;
+  const int64_t nb = T + 1;
+  // bins per bucket: the power of two at or below the count that holds about kBucketRows rows
+  // (at most kMaxBucketBins), raised until the buckets number at most kMaxBuckets
+  const int64_t target = N > 0 ? nb * kBucketRows / N : nb;
+  int shift = 0;
+  while ((int64_t(2) << shift) <= target && (int64_t(2) << shift) <= kMaxBucketBins) ++shift;
+  while (((nb + (int64_t(1) << shift) - 1) >> shift) > kMaxBuckets) ++shift;
+  g.shift = shift;
+  g.nbk = (int)((nb + (int64_t(1) << shift) - 1) >> shift);
+  g.ok = (int64_t(1) << shift) <= kMaxBucketBins;
+  const int64_t per_slice = (N + kMaxSlices - 1) / kMaxSlices;
+  const int64_t S = (per_slice + kPartThreads - 1) / kPartThreads * kPartThreads;
+  g.S = S > kMinSlice ? S : kMinSlice;
+  g.G1 = (int)(N > 0 ? (N + g.S - 1) / g.S : 1);
+  return g;
+}
+
+// ---- plan workspace layout --------------------------------------------------------------------
+//   status   int32[3] (+ padding)
+//   cursor   int32[T + 1]      fill cursors of the three-launch plan
+//   row_ptr  int32[T + 2]
+//   tmp      the three-launch plan's unordered records (N x 16 B), or the bucketed plan's
+//            partition (N x int2) followed by its per-slice bucket counts and prefixes
+//            (2 x G1 x nbk int32)
+//   rec      N x 16-byte records
+struct PlanLayout {
+  int64_t status, cursor, row_ptr, rec_tmp, part, bcnt, bpre, rec, total;
+};
+
+__host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  const PlanGeom g = plan_geom(N, T);
+  const int64_t tab = (int64_t)g.G1 * g.nbk * 4;
+  PlanLayout L;
+  L.status = 0;
+  L.cursor = 256;
+  L.row_ptr = L.cursor + up((T + 1) * 4);
+  L.rec_tmp = L.row_ptr + up((T + 2) * 4);
+  L.part = L.rec_tmp;
+  L.bcnt = L.part + up(N * 8);
+  L.bpre = L.bcnt + up(tab);
+  const int64_t tmp_end = std::max(L.rec_tmp + up(N * 16), L.bpre + up(tab));
+  L.rec = tmp_end;
+  L.total = L.rec + up(N * 16);
+  return L;
+}
+
+// ---- where a plan builder gets the expert table from --------------------------------------------
+// TokMetaGlobal: the device arrays of fmoe_build_metadata.  TokMetaArgs: the table in the kernel
+// arguments (at most 256 experts), prefixed on the host -- each expert's address and first packed
+// row, and the largest row count -- so a workgroup only copies it into LDS; workgroup 0 also
+// writes the metadata outputs, so metadata and plan need no separate launch.
+struct TokMetaGlobal {
+  const int64_t* ptr_table;
+  const int64_t* offsets;
+};
+struct HostTable {
+  int64_t ptr[kMetaChunk];
+  int32_t off[kMetaChunk + 1];  // exclusive prefix of the row counts; off[count] = N < 2^31
+  int32_t count;
+  int32_t max_rows;
+};
+struct TokMetaArgs {
+  HostTable a;
+  int64_t* ptr_table;
+  int32_t* chunk_sizes;
+  int64_t* offsets;
+  int32_t* max_rows;
+};
+static_assert(sizeof(TokMetaArgs) <= 3200, "kernel-argument table too large");
+
+// The host side of TokMetaArgs: E <= kMetaChunk (address, rows) pairs, rows in [0, 2^31) and
+// summing below 2^31 (checked by the callers).
+inline void fill_host_table(TokMetaArgs* m, const int64_t* host_ptrs, const int64_t* host_rows,
+                            int64_t E, int64_t* ptr_table, int32_t* chunk_sizes, int64_t* offsets,
+                            int32_t* max_rows) {
+  int64_t run = 0, mx = 0;
+  for (int i = 0; i < kMetaChunk; ++i) {
+    const int64_t n = i < E ? host_rows[i] : 0;
+    m->a.ptr[i] = i < E ? host_ptrs[i] : 0;
+    m->a.off[i] = (int32_t)run;
+    run += n;
+    mx = std::max(mx, n);
+  }
+  m->a.off[kMetaChunk] = (int32_t)run;
+  m->a.count = (int32_t)E;
+  m->a.max_rows = (int32_t)mx;
+  m->ptr_table = ptr_table;
+  m->chunk_sizes = chunk_sizes;
+  m->offsets = offsets;
+  m->max_rows = max_rows;
+}
+
+// Largest e in [0, E) with off[e] <= g (int32 offsets, off[0] == 0 <= g < off[E]).
+__device__ __forceinline__ int expert_of_row32(const int* __restrict__ off, int E, int g) {
+  int lo = 0, hi = E;  // invariant: off[lo] <= g < off[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (off[mid] <= g) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// Lanes below this one in a 64-bit lane mask.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+}
+
+// Mask of the active lanes whose `bits`-bit key equals this lane's (bits wave-uniform).
+__device__ __forceinline__ uint64_t match_key(bool active, int key, int bits) {
+  uint64_t m = __ballot(active);
+  for (int q = 0; q < bits; ++q) {
+    const bool bit = (key >> q) & 1;
+    const uint64_t b = __ballot(bit);
+    m &= bit ? b : ~b;
+  }
+  return m;
+}
+
+}  // namespace fmoe
+
+// Launchers of the bucketed plan (plan_bucket.hip).  BARE: write row numbers (the bare CSR of
+// fmoe_invert_scatter_index) instead of records.
+namespace fmoe_plan {
+int launch_bucketed(const fmoe::TokMetaGlobal* gmeta, const fmoe::TokMetaArgs* ameta,
+                    const void* d_indices, int idx_dtype, const void* d_weights, int w_dtype,
+                    int64_t N, int64_t T, int64_t E, int64_t row_bytes, void* d_workspace,
+                    bool bare, int32_t* d_rows_bare, int32_t* d_row_ptr_bare, hipStream_t s,
+                    const char* who);
+}  // namespace fmoe_plan

@@ -6,53 +6,29 @@
 //
 //   row_ptr[T + 2]  : segment b = [row_ptr[b], row_ptr[b + 1]); b == T holds the rows whose index
 //                     is out of range (they are dropped by the forward, zero-filled by the backward)
-//   rec[N]          : 16-byte records {source row address, fp32 gate, g}; a segment of up to 64
-//                     rows is unordered (consumers that need the order rank it in registers),
-//                     a longer one is in ascending g
+//   rec[N]          : 16-byte records {source row address, fp32 gate, g}, ascending g in every
+//                     segment
 //
-// Built in one launch when T + 1 <= 256 * 4096, N <= 2^20 and E <= 4096 (k_plan_tok): P
-// workgroups each own a contiguous range of token bins, stream all of idx (from L2 after the
-// first), count the rows below their range and the rows of each of their own bins, scan their bins
-// and fill their rows' records; a segment longer than 64 rows is then ordered by g by the
-// workgroup that owns it.  No workgroup waits for another and nothing needs zero-filled memory.
+// Three builders, each linear in N + T except where noted:
+//   * one launch (k_plan_tok), up to kTokMaxRows rows: token-sliced workgroups that each stream
+//     all of idx and fill their own segments stably (below);
+//   * two launches (plan_bucket.hip), larger N: partition the rows by token bucket, then order
+//     each bucket with one wave;
+//   * three launches, beyond 2^22 tokens: count + scan (one 1024-thread workgroup histograms idx
+//     in LDS, or zero / global-atomic count / one-block scan for larger T), a fill of one thread
+//     per row with atomic cursors (arbitrary order within a segment), and an ordering pass over
+//     segments longer than 64 rows, quadratic in their length (the consumers order shorter
+//     segments in registers).
 //
-// Otherwise three steps (all on the caller's stream, no host synchronisation):
-//   1. count + scan   one 1024-thread workgroup histograms idx into LDS (T + 1 <= kLdsTokens) and
-//                     scans it; larger T fall back to zero / global-atomic count / one-block scan.
-//   2. fill           one thread per row: claims a slot in its segment with an atomic cursor and
-//                     writes its record (arbitrary order inside the segment).
-//   3. order          segments longer than 64 rows only (never for top-k routing; the kernel
-//                     exits at once otherwise): one wave per segment ranks its records by g and
-//                     writes them in order.
-// Segments of up to 64 rows are ordered by the consumers in registers, so every result is
-// bit-identical run to run even though the fill order is not.
-//
-// fmoe_invert_scatter_index runs the three-step count + scan, then writes bare row numbers
-// (ascending in every segment) instead of records.
+// fmoe_invert_scatter_index writes bare row numbers instead of records (two launches, or the
+// three-launch fallback).
 #include <algorithm>
 
-#include "common.h"
+#include "plan.h"
 
 namespace fmoe {
 
-constexpr int kScanThreads = 1024;
 constexpr int kLdsTokens = 33792;  // 132 KiB of LDS histogram (gfx950: 160 KiB per workgroup)
-
-struct PlanLayout {
-  int64_t status, cursor, row_ptr, rec_tmp, rec, total;
-};
-
-__host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
-  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
-  PlanLayout L;
-  L.status = 0;
-  L.cursor = 256;
-  L.row_ptr = L.cursor + up((T + 1) * 4);
-  L.rec_tmp = L.row_ptr + up((T + 2) * 4);
-  L.rec = L.rec_tmp + up(N * 16);
-  L.total = L.rec + up(N * 16);
-  return L;
-}
 
 // Exclusive scan of one int per thread over a 1024-thread block; *total gets the block sum.
 __device__ int block_exclusive_scan_1024(int v, int* total) {
@@ -270,93 +246,29 @@ __global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __rest
   }
 }
 
-// ---- one-launch plan: token-sliced count + scan + fill (+ ordering of long segments) --------
-// P workgroups; workgroup s owns the token bins [s * bins, (s + 1) * bins) of the T + 1 (bin T:
-// out-of-range rows), so every segment belongs to exactly one workgroup and the workgroups never
-// communicate.  Each streams all of idx (from L2 after the first) and
-//   * counts the rows whose bin lies below its range (a register sum: row_ptr of its first bin),
-//   * counts its own bins' rows with LDS atomics and stashes those rows' (g, bin) in LDS,
-// scans its bins into row_ptr and the fill cursors, and writes one record per stashed row.  A
-// wave whose stash region overflows (a heavily skewed index) makes the workgroup fill from a
-// second pass over idx instead.  Within a segment the slot order is arbitrary; a segment longer
-// than 64 rows is then ordered by g by the workgroup that owns it.
-constexpr int kTokBins = 4096;                         // bins per workgroup at most
+// ---- one-launch plan: token-sliced, stable --------------------------------------------------
+// P workgroups of 16 waves; workgroup p owns the token bins [p * bins, (p + 1) * bins) of the T + 1
+// (bin T: out-of-range rows), so every segment belongs to exactly one workgroup and the workgroups
+// never communicate.  Every workgroup streams all of idx (from L2 after the first): wave w takes
+// the w-th sixteenth of the rows, in ascending g, one row per lane per load, and
+//   * counts the rows whose bin lies below its workgroup's range (part of row_ptr of its first bin),
+//   * counts its rows of each of the range's bins in its own LDS row and stashes them (g, bin) in
+//     ascending g.
+// The workgroup then scans its bins bin-major and wave-minor, which gives row_ptr and each wave's
+// first place in every bin, and each wave writes the records of its stashed rows: a row goes to its
+// wave's cursor for the bin plus its rank among the lower lanes with the same bin.  Every segment
+// thus comes out in ascending g with no ordering pass, in time linear in N per workgroup.  A wave
+// whose stash overflows (a heavily skewed index) re-streams its own rows in the fill instead.
+// Every workgroup reading all of idx makes the total work N * P: beyond kTokMaxRows rows the
+// bucketed plan (plan_bucket.hip) takes over.
 constexpr int kTokWaves = kScanThreads / kWave;        // 16
-constexpr int kTokStash = 8192;                        // stashed rows per workgroup
-constexpr int kTokWaveStash = kTokStash / kTokWaves;   // 512 per wave
+constexpr int kTokBins = 512;                          // bins per workgroup at most
+constexpr int kTokWaveStash = 256;                     // stashed rows per wave
 constexpr int kTokRows = 256;                          // rows per workgroup aimed at
 constexpr int kTokGroups = 256;
-constexpr int kTokExperts = 4096;                      // int32 expert offsets staged in LDS
-constexpr int64_t kTokMaxRows = int64_t(1) << 20;      // every workgroup streams all of idx
-constexpr int32_t kLongBit = 1 << 30;                  // cursor flag: segment longer than 64 rows
-
-__device__ __forceinline__ int expert_of_row32(const int* __restrict__ off, int E, int g) {
-  int lo = 0, hi = E;  // invariant: off[lo] <= g < off[hi]
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (off[mid] <= g) lo = mid; else hi = mid;
-  }
-  return lo;
-}
-
-// Record of row g for the slot `v` (cursor value: slot | long flag); gate already loaded.
-__device__ __forceinline__ void tok_write_rec(int v, int g, float wg, const int* __restrict__ off32,
-                                              const uint64_t* __restrict__ ptr_lds, int ne,
-                                              int64_t row_bytes, Rec* __restrict__ rec_tmp,
-                                              Rec* __restrict__ rec) {
-  const int e = expert_of_row32(off32, ne, g);
-  Rec r;
-  r.src = ptr_lds[e] + (uint64_t)((int64_t)(g - off32[e]) * row_bytes);
-  r.w = wg;
-  r.g = g;
-  ((v & kLongBit) ? rec_tmp : rec)[v & (kLongBit - 1)] = r;
-}
-
-// Where the one-launch plan gets the expert table from.  TokMetaGlobal: the device arrays of
-// fmoe_build_metadata.  TokMetaArgs: the table in the kernel arguments (at most 256 experts),
-// prefixed on the host -- each expert's address and first packed row, and the largest row count --
-// so a workgroup only copies it into LDS; workgroup 0 also writes the metadata outputs, so
-// metadata and plan take one launch.
-struct TokMetaGlobal {
-  const int64_t* ptr_table;
-  const int64_t* offsets;
-};
-struct HostTable {
-  int64_t ptr[kMetaChunk];
-  int32_t off[kMetaChunk + 1];  // exclusive prefix of the row counts; off[count] = N < 2^31
-  int32_t count;
-  int32_t max_rows;
-};
-struct TokMetaArgs {
-  HostTable a;
-  int64_t* ptr_table;
-  int32_t* chunk_sizes;
-  int64_t* offsets;
-  int32_t* max_rows;
-};
-static_assert(sizeof(TokMetaArgs) <= 3200, "kernel-argument table too large");
-
-// The host side of TokMetaArgs: E <= kMetaChunk (address, rows) pairs, rows in [0, 2^31) and
-// summing below 2^31 (checked by the callers).
-inline void fill_host_table(TokMetaArgs* m, const int64_t* host_ptrs, const int64_t* host_rows,
-                            int64_t E, int64_t* ptr_table, int32_t* chunk_sizes, int64_t* offsets,
-                            int32_t* max_rows) {
-  int64_t run = 0, mx = 0;
-  for (int i = 0; i < kMetaChunk; ++i) {
-    const int64_t n = i < E ? host_rows[i] : 0;
-    m->a.ptr[i] = i < E ? host_ptrs[i] : 0;
-    m->a.off[i] = (int32_t)run;
-    run += n;
-    mx = std::max(mx, n);
-  }
-  m->a.off[kMetaChunk] = (int32_t)run;
-  m->a.count = (int32_t)E;
-  m->a.max_rows = (int32_t)mx;
-  m->ptr_table = ptr_table;
-  m->chunk_sizes = chunk_sizes;
-  m->offsets = offsets;
-  m->max_rows = max_rows;
-}
+constexpr int kTokExperts = 4096;                      // expert tables staged in LDS
+constexpr int64_t kTokMaxRows = int64_t(1) << 17;
+constexpr int kTokLoads = 16;                          // index loads per lane per batch
 
 __device__ __forceinline__ void tok_load_meta(const TokMetaGlobal& m, int ne, int* off32,
                                               uint64_t* ptr_lds) {
@@ -380,30 +292,44 @@ __device__ __forceinline__ void tok_load_meta(const TokMetaArgs& m, int ne, int*
   }
 }
 
-// Index vector of one 16-byte load: 2 int64 or 4 int32 scatter indices.
-template <typename TI> struct IdxVec {
-  static constexpr int kCount = 16 / (int)sizeof(TI);
-  static __device__ __forceinline__ int64_t get(const u32x4& v, int q) {
-    if constexpr (sizeof(TI) == 8)
-      return (int64_t)((uint64_t)v[2 * q] | ((uint64_t)v[2 * q + 1] << 32));
-    else
-      return (int64_t)(int32_t)v[q];
+// Exclusive scan of v and sum of s over a 1024-thread block, in one barrier round.
+__device__ __forceinline__ int tok_scan_and_sum(int v, int s, int* sum_s) {
+  __shared__ int wave_v[kTokWaves], wave_s[kTokWaves];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
   }
-};
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) s += __shfl_xor(s, d, kWave);
+  if (lane == kWave - 1) {
+    wave_v[wv] = incl;
+    wave_s[wv] = s;
+  }
+  __syncthreads();
+  int before = 0, tot_s = 0;
+#pragma unroll
+  for (int i = 0; i < kTokWaves; ++i) {
+    before += (i < wv) ? wave_v[i] : 0;
+    tot_s += wave_s[i];
+  }
+  *sum_s = tot_s;
+  return before + incl - v;
+}
 
 template <typename TI, typename TW, typename Meta>
 __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T, int bins,
     const Meta meta, int64_t E, int64_t row_bytes, int32_t* __restrict__ row_ptr,
-    Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, int32_t* __restrict__ status) {
-  using IV = IdxVec<TI>;
-  constexpr int kQ = IV::kCount;
-  __shared__ int cnt[kTokBins];         // rows per bin, then the fill cursors
-  __shared__ int2 stash[kTokStash];     // (g, local bin) of this range's rows; later the long list
+    Rec* __restrict__ rec, int32_t* __restrict__ status) {
+  __shared__ int cnt[kTokWaves * kTokBins];            // [wave][bin]: counts, then cursors
+  __shared__ int2 stash[kTokWaves * kTokWaveStash];    // per wave: (g, local bin), ascending g
   __shared__ int off32[kTokExperts + 1];
   __shared__ uint64_t ptr_lds[kTokExperts];
-  __shared__ int red[3][kTokWaves];
-  __shared__ int overflow, misaligned, n_long;
+  __shared__ int misaligned;
   const int nb = (int)T + 1;
   const int ne = (int)E;
   const int lo = (int)blockIdx.x * bins;  // the host makes every range non-empty
@@ -411,74 +337,62 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   const int nloc = hi - lo;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  for (int i = threadIdx.x; i < nloc; i += kScanThreads) cnt[i] = 0;
+  for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) cnt[i] = 0;
   tok_load_meta(meta, ne, off32, ptr_lds);
-  if (threadIdx.x == 0) {
-    overflow = 0;
-    misaligned = 0;
-    n_long = 0;
-  }
+  if (threadIdx.x == 0) misaligned = 0;
   __syncthreads();
 
-  // 1. one pass over idx, 16 bytes per lane per load, software-pipelined: the loads of the next
-  //    batch are in flight while this one is counted.  Only whole vectors are loaded (a vector
-  //    past the end gets the offset of the end, which the range check turns into zeros); the
-  //    N % kQ rows after the last whole vector are loaded one by one by wave 0.
-  const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));
-  int2* wstash = stash + wave * kTokWaveStash;
-  int below = 0;   // rows whose bin precedes this range
-  int wcount = 0;  // rows of this range seen by this wave (wave-uniform)
+  // 1. pass over this wave's rows [r0, r1), ascending g, kTokLoads loads per lane in flight
   const int n32 = (int)N;
-  const int nfull = n32 - n32 % kQ;
-  const uint32_t end_off = (uint32_t)n32 * (uint32_t)sizeof(TI);
-  auto count_row = [&](bool valid, int g, int64_t t) {
-    // (unsigned) t < T covers 0 <= t < T; nb marks rows that are not counted here
-    const int b = valid ? ((uint64_t)t < (uint64_t)T ? (int)t : (int)T) : nb;
-    below += b < lo ? 1 : 0;
-    const bool in = b >= lo && b < hi;
+  const int per = ((n32 + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;
+  const int r0 = min(n32, wave * per);
+  const int r1 = min(n32, r0 + per);
+  int* mycnt = cnt + wave * nloc;
+  int2* mystash = stash + wave * kTokWaveStash;
+  const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));
+  int below = 0;   // rows of this lane whose bin precedes the range
+  int wcount = 0;  // rows of the range seen by this wave (wave-uniform)
+  auto bin_at = [&](int g, TI raw) -> uint32_t {  // 0xffffffff: not a row of this wave
+    const int64_t t = (int64_t)raw;
+    return g < r1 ? ((uint64_t)t < (uint64_t)T ? (uint32_t)t : (uint32_t)T) : 0xffffffffu;
+  };
+  auto count_row = [&](int g, uint32_t b) {
+    below += b < (uint32_t)lo ? 1 : 0;
+    const uint32_t j = b - (uint32_t)lo;
+    const bool in = j < (uint32_t)nloc;
     const uint64_t m = __ballot(in);
-    if (in) {
-      atomicAdd(&cnt[b - lo], 1);
-      const int slot = wcount + (int)__builtin_amdgcn_mbcnt_hi(
-                                    (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-      if (slot < kTokWaveStash) wstash[slot] = make_int2(g, b - lo);
-    }
-    wcount += __popcll(m);
-  };
-  constexpr int kLoads = 8 / kQ;  // 8 rows per thread per batch
-  constexpr int kStep = kScanThreads * kQ;
-  constexpr int kBatchRows = kStep * kLoads;
-  auto load_batch = [&](int base, u32x4* v) {
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int g0 = base + i * kStep + (int)threadIdx.x * kQ;
-      v[i] = Raw<16>::ld<kCPolCached>(ri, g0 < nfull ? (uint32_t)g0 * (uint32_t)sizeof(TI) : end_off);
-    }
-  };
-  u32x4 cur[kLoads], nxt[kLoads];
-  load_batch(0, cur);
-  for (int base = 0; base < nfull; base += kBatchRows) {
-    load_batch(base + kBatchRows, nxt);  // past the end: zeros, no memory traffic
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-#pragma unroll
-      for (int q = 0; q < kQ; ++q) {
-        const int g = base + i * kStep + (int)threadIdx.x * kQ + q;
-        count_row(g < nfull, g, IV::get(cur[i], q));
+    if (m) {  // wave-uniform
+      if (in) {
+        atomicAdd(&mycnt[j], 1);
+        const int slot = wcount + lanes_below(m);
+        if (slot < kTokWaveStash) mystash[slot] = make_int2(g, (int)j);
       }
+      wcount += __popcll(m);
     }
+  };
+  auto load_batch = [&](int base, TI* v) {
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) cur[i] = nxt[i];
+    for (int i = 0; i < kTokLoads; ++i) {
+      const int g = base + i * kWave + lane;  // past N: zeros from the range check, no traffic
+      v[i] = __builtin_bit_cast(
+          TI, Raw<sizeof(TI)>::template ld<kCPolCached>(ri, (uint32_t)g * (uint32_t)sizeof(TI)));
+    }
+  };
+  constexpr int kBatchRows = kTokLoads * kWave;
+  if (r0 < r1) {  // wave-uniform
+    TI cur[kTokLoads], nxt[kTokLoads];
+    load_batch(r0, cur);
+    for (int base = r0; base < r1; base += kBatchRows) {
+      if (base + kBatchRows < r1) load_batch(base + kBatchRows, nxt);
+#pragma unroll
+      for (int i = 0; i < kTokLoads; ++i) {
+        const int g = base + i * kWave + lane;
+        count_row(g, bin_at(g, cur[i]));
+      }
+#pragma unroll
+      for (int i = 0; i < kTokLoads; ++i) cur[i] = nxt[i];
+    }
   }
-  if (nfull < n32 && wave == 0) {  // wave-uniform
-    const int g = nfull + lane;
-    const bool valid = g < n32;
-    int64_t t = 0;
-    if (valid) t = (int64_t)__builtin_bit_cast(
-        TI, Raw<sizeof(TI)>::template ld<kCPolCached>(ri, (uint32_t)g * (uint32_t)sizeof(TI)));
-    count_row(valid, g, t);
-  }
-  if (lane == 0 && wcount > kTokWaveStash) overflow = 1;
   if (blockIdx.x == 0) {
     // a source row is misaligned iff its expert's base is, or the expert has two or more rows
     // and the row length is not a multiple of 16 bytes
@@ -491,106 +405,65 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   }
   __syncthreads();
 
-  // 2. scan of this range's bins (at most 4 per thread), the rows below it and the longest
-  //    segment, in one barrier round
-  constexpr int kPer = kTokBins / kScanThreads;
-  const int per = (nloc + kScanThreads - 1) / kScanThreads;
-  const int b0 = min(nloc, (int)threadIdx.x * per);
-  const int b1 = min(nloc, b0 + per);
-  int c[kPer];
-  int local = 0, longest = 0;
-#pragma unroll
-  for (int p = 0; p < kPer; ++p) {
-    c[p] = b0 + p < b1 ? cnt[b0 + p] : 0;
-    local += c[p];
-    if (lo + b0 + p < nb - 1) longest = max(longest, c[p]);  // token bins only
-  }
-  int incl = local;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) {
-    below += __shfl_xor(below, d, kWave);
-    longest = max(longest, __shfl_xor(longest, d, kWave));
-  }
-  if (lane == kWave - 1) {
-    red[0][wave] = incl;
-    red[1][wave] = below;
-    red[2][wave] = longest;
-  }
-  __syncthreads();  // also: every count read above precedes the cursor writes below
-  int run = incl - local, range_rows = 0, rows_below = 0;
-#pragma unroll
-  for (int i = 0; i < kTokWaves; ++i) {
-    run += i < wave ? red[0][i] : 0;
-    range_rows += red[0][i];
-    rows_below += red[1][i];
-    longest = max(longest, red[2][i]);
-  }
-  int first[kPer];
-#pragma unroll
-  for (int p = 0; p < kPer; ++p) {
-    const int lb = b0 + p;
-    first[p] = rows_below + run;
-    if (lb < b1) {
-      const bool tok = lo + lb < nb - 1;  // a token bin (not the out-of-range bin T)
-      row_ptr[lo + lb] = first[p];
-      cnt[lb] = first[p] | ((tok && c[p] > kWave) ? kLongBit : 0);
-      if (!tok) status[kStatusInvalid] = c[p];
+  // 2. thread j owns bin j of the range: its rows over all waves, row_ptr, and each wave's first
+  //    place in it (the cursors)
+  const int bj = threadIdx.x;
+  int tot = 0;
+  if (bj < nloc)
+    for (int v = 0; v < kTokWaves; ++v) tot += cnt[v * nloc + bj];
+  int rows_below;
+  const int excl = tok_scan_and_sum(tot, below, &rows_below);
+  if (bj < nloc) {
+    int run = rows_below + excl;
+    row_ptr[lo + bj] = run;
+    if (lo + bj == nb - 1) status[kStatusInvalid] = tot;  // the out-of-range bin
+    for (int v = 0; v < kTokWaves; ++v) {
+      const int c = cnt[v * nloc + bj];
+      cnt[v * nloc + bj] = run;
+      run += c;
     }
-    run += c[p];
+    if (hi == nb && bj == nloc - 1) row_ptr[nb] = run;  // == N
   }
-  if (hi == nb && threadIdx.x == 0) row_ptr[nb] = rows_below + range_rows;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     status[kStatusMisaligned] = misaligned;
     status[kStatusLongest] = -1;  // not recorded: no workgroup sees every segment
   }
   __syncthreads();  // the cursors
 
-  // 3. fill: each wave its own stashed rows, two at a time; or all rows from a second pass
-  if (!overflow) {
-    const int n = wcount;  // <= kTokWaveStash here
-    for (int j = lane; j < n; j += 2 * kWave) {
-      const bool two = j + kWave < n;
-      const int2 a = wstash[j];
-      const int2 bb = two ? wstash[j + kWave] : a;
-      const float wa = ld1(w + a.x);
-      const float wb = ld1(w + bb.x);
-      const int va = atomicAdd(&cnt[a.y], 1);
-      const int vb = two ? atomicAdd(&cnt[bb.y], 1) : 0;
-      tok_write_rec(va, a.x, wa, off32, ptr_lds, ne, row_bytes, rec_tmp, rec);
-      if (two) tok_write_rec(vb, bb.x, wb, off32, ptr_lds, ne, row_bytes, rec_tmp, rec);
+  // 3. fill: each wave its rows in ascending g -- from the stash, or again from idx if the stash
+  //    overflowed
+  const int jbits = nloc > 1 ? 32 - __builtin_clz((unsigned)(nloc - 1)) : 0;
+  auto place = [&](bool act, int g, int j, float wg) {
+    const uint64_t m = match_key(act, j, jbits);
+    if (act) {
+      const int rank = lanes_below(m);
+      const int pos = mycnt[j] + rank;
+      if (rank == 0) mycnt[j] = pos + __popcll(m);
+      const int e = expert_of_row32(off32, ne, g);
+      Rec r;
+      r.src = ptr_lds[e] + (uint64_t)((int64_t)(g - off32[e]) * row_bytes);
+      r.w = wg;
+      r.g = g;
+      rec[pos] = r;
+    }
+  };
+  if (wcount <= kTokWaveStash) {  // wave-uniform
+    for (int c0 = 0; c0 < wcount; c0 += kWave) {
+      const bool act = c0 + lane < wcount;
+      const int2 e = act ? mystash[c0 + lane] : make_int2(0, 0);
+      const float wg = act ? ld1(w + e.x) : 0.f;
+      place(act, e.x, e.y, wg);
     }
   } else {
-    for (int64_t g = threadIdx.x; g < N; g += kScanThreads) {
-      const int64_t t = (int64_t)idx[g];
-      const int b = (t >= 0 && t < T) ? (int)t : (int)T;
-      if (b >= lo && b < hi)
-        tok_write_rec(atomicAdd(&cnt[b - lo], 1), (int)g, ld1(w + g), off32, ptr_lds, ne,
-                      row_bytes, rec_tmp, rec);
-    }
-  }
-  if (longest <= kWave) return;  // workgroup-uniform
-
-  // 4. order the segments longer than 64 rows (non-top-k routing only), one wave per segment
-  __syncthreads();  // the fill's records are visible to the workgroup; the stash is free
-  int2* list = stash;  // at most nloc <= kTokStash entries
-#pragma unroll
-  for (int p = 0; p < kPer; ++p)
-    if (b0 + p < b1 && lo + b0 + p < nb - 1 && c[p] > kWave)
-      list[atomicAdd(&n_long, 1)] = make_int2(first[p], c[p]);
-  __syncthreads();
-  const int nl = n_long;
-  for (int i = wave; i < nl; i += kTokWaves) {
-    const int beg = list[i].x, cn = list[i].y;
-    for (int j = lane; j < cn; j += kWave) {
-      const Rec r = rec_tmp[beg + j];
-      int rank = 0;
-      for (int m = 0; m < cn; ++m) rank += (rec_tmp[beg + m].g < r.g) ? 1 : 0;
-      rec[beg + rank] = r;
+    for (int base = r0; base < r1; base += kWave) {
+      const int g = base + lane;
+      const uint32_t b = bin_at(
+          g, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
+                                        ri, (uint32_t)g * (uint32_t)sizeof(TI))));
+      const uint32_t j = b - (uint32_t)lo;
+      const bool in = j < (uint32_t)nloc;
+      const float wg = in ? ld1(w + g) : 0.f;
+      place(in, g, (int)j, wg);
     }
   }
 }
@@ -750,11 +623,10 @@ int launch_count_scan(const void* d_indices, int idx_dtype, int64_t N, int64_t T
   return fmoe_host::check_launch(who);
 }
 
-// Grid of the one-launch plan, or false when its limits do not hold (or FMOE_PLAN_SPLIT=1).
+// Grid of the one-launch plan, or false when its limits do not hold (row count aside: the caller
+// weighs N).
 bool tok_grid(int64_t N, int64_t T, int64_t E, int64_t* groups_out, int64_t* bins_out) {
   using namespace fmoe;
-  const char* split_env = getenv("FMOE_PLAN_SPLIT");
-  if (split_env && *split_env && atoi(split_env) != 0) return false;
   const int64_t nb = T + 1;
   int64_t groups = std::max<int64_t>((N + kTokRows - 1) / kTokRows, (nb + kTokBins - 1) / kTokBins);
   groups = std::min<int64_t>(std::min<int64_t>(groups, kTokGroups), nb);
@@ -762,19 +634,20 @@ bool tok_grid(int64_t N, int64_t T, int64_t E, int64_t* groups_out, int64_t* bin
   groups = (nb + bins - 1) / bins;  // every workgroup gets a non-empty bin range
   *groups_out = groups;
   *bins_out = bins;
-  return E <= kTokExperts && N <= kTokMaxRows && bins <= kTokBins;
+  // index loads use 32-bit byte offsets (rows past N by up to one batch included)
+  return E <= kTokExperts && N <= (int64_t(1) << 28) && bins <= kTokBins;
 }
 
 template <typename Meta>
 int launch_plan_tok(const Meta& meta, const void* d_indices, int idx_dtype, const void* d_weights,
                     int w_dtype, int64_t N, int64_t T, int64_t E, int64_t row_bytes,
-                    int64_t groups, int64_t bins, int32_t* row_ptr, fmoe::Rec* rec_tmp,
-                    fmoe::Rec* rec, int32_t* status, hipStream_t s) {
+                    int64_t groups, int64_t bins, int32_t* row_ptr, fmoe::Rec* rec,
+                    int32_t* status, hipStream_t s) {
   using namespace fmoe;
 #define FMOE_TOK(TI, TW)                                                                           \
   hipLaunchKernelGGL((k_plan_tok<TI, TW, Meta>), dim3((unsigned)groups), dim3(kScanThreads), 0, s, \
                      static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
-                     (int)bins, meta, E, row_bytes, row_ptr, rec_tmp, rec, status)
+                     (int)bins, meta, E, row_bytes, row_ptr, rec, status)
 #define FMOE_TOK_W(TI)                                 \
   if (w_dtype == FMOE_F32) FMOE_TOK(TI, float);        \
   else if (w_dtype == FMOE_BF16) FMOE_TOK(TI, bf16_t); \
@@ -783,6 +656,20 @@ int launch_plan_tok(const Meta& meta, const void* d_indices, int idx_dtype, cons
 #undef FMOE_TOK_W
 #undef FMOE_TOK
   return fmoe_host::check_launch("fmoe_build_plan(one launch)");
+}
+
+// Which plan builds the records: the stable one-launch plan within its limits, else the bucketed
+// plan, else the three launches.  Option "plan": 0 automatic, 1 three launches, 2 bucketed,
+// 3 one launch (each where its limits hold; the next in that order otherwise).
+enum PlanPath { kPathTok, kPathBucketed, kPathSplit };
+PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bins) {
+  const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
+  const bool tok = tok_grid(N, T, E, groups, bins);
+  const bool bucketed = fmoe::plan_geom(N, T).ok;
+  if (algo == 1) return kPathSplit;
+  if (algo == 2) return bucketed ? kPathBucketed : kPathSplit;
+  if (tok && (algo == 3 || N <= fmoe::kTokMaxRows)) return kPathTok;
+  return bucketed ? kPathBucketed : kPathSplit;
 }
 
 }  // namespace
@@ -831,14 +718,18 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
 
-  // One token-sliced launch when its limits hold; otherwise count + scan, fill and order as
-  // three launches.  FMOE_PLAN_SPLIT=1 forces the latter (tests compare the two).
-  int64_t groups, bins;
-  if (tok_grid(N, T, E, &groups, &bins)) {
-    const TokMetaGlobal meta{d_ptr_table, d_offsets};
+  // The stable one-launch plan, the bucketed plan or the three launches (pick_plan; tests compare
+  // the paths through the "plan" option).
+  const TokMetaGlobal meta{d_ptr_table, d_offsets};
+  int64_t groups = 0, bins = 0;
+  const PlanPath path = pick_plan(N, T, E, &groups, &bins);
+  if (path == kPathTok)
     return launch_plan_tok(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
-                           groups, bins, row_ptr, rec_tmp, rec, status, s);
-  }
+                           groups, bins, row_ptr, rec, status, s);
+  if (path == kPathBucketed)
+    return fmoe_plan::launch_bucketed(&meta, nullptr, d_indices, idx_dtype, d_weights, w_dtype, N,
+                                      T, E, row_bytes, d_workspace, false, nullptr, nullptr, s,
+                                      "fmoe_build_plan");
 
   if (int rc = launch_count_scan(d_indices, idx_dtype, N, T, cursor, row_ptr, status, s,
                                  "fmoe_build_plan"))
@@ -885,7 +776,9 @@ extern "C" int fmoe_build_metadata_and_plan(
   }
   const bool small_table = E <= kMetaChunk;
   int64_t groups = 0, bins = 0;
-  if (!small_table || T < 1 || T >= (int64_t(1) << 30) || !tok_grid(N, T, E, &groups, &bins)) {
+  const bool sizes_ok = T >= 1 && T < (int64_t(1) << 30) && N < (int64_t(1) << 31);
+  const PlanPath path = sizes_ok ? pick_plan(N, T, E, &groups, &bins) : kPathSplit;
+  if (!small_table || path == kPathSplit) {
     // the two calls (each validates its own arguments)
     if (int rc = fmoe_build_metadata(host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes,
                                      d_offsets, d_max_rows, stream))
@@ -893,7 +786,8 @@ extern "C" int fmoe_build_metadata_and_plan(
     return fmoe_build_plan(d_indices, idx_dtype, d_weights, w_dtype, N, T, d_ptr_table, d_offsets,
                            E, row_bytes, d_workspace, stream);
   }
-  // one launch: the checks of fmoe_build_metadata and fmoe_build_plan
+  // one call (the metadata written by the plan's own kernels): the checks of fmoe_build_metadata
+  // and fmoe_build_plan
   for (int64_t e = 0; e < E; ++e) {
     FMOE_REQUIRE(host_rows[e] >= 0 && host_rows[e] < (int64_t(1) << 31),
                  "fmoe_build_metadata_and_plan: expert %lld has invalid row count %lld",
@@ -916,11 +810,16 @@ extern "C" int fmoe_build_metadata_and_plan(
   TokMetaArgs meta;
   fill_host_table(&meta, host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes, d_offsets,
                   d_max_rows);
+  if (path == kPathBucketed)
+    return fmoe_plan::launch_bucketed(nullptr, &meta, d_indices, idx_dtype, d_weights, w_dtype, N,
+                                      T, E, row_bytes, d_workspace, false, nullptr, nullptr,
+                                      static_cast<hipStream_t>(stream),
+                                      "fmoe_build_metadata_and_plan");
   const PlanLayout L = plan_layout(N, T);
   char* ws = static_cast<char*>(d_workspace);
   return launch_plan_tok(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
                          groups, bins, reinterpret_cast<int32_t*>(ws + L.row_ptr),
-                         reinterpret_cast<Rec*>(ws + L.rec_tmp), reinterpret_cast<Rec*>(ws + L.rec),
+                         reinterpret_cast<Rec*>(ws + L.rec),
                          reinterpret_cast<int32_t*>(ws + L.status), static_cast<hipStream_t>(stream));
 }
 
@@ -1054,6 +953,10 @@ extern "C" int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, i
   FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
                "fmoe_invert_scatter_index: workspace not 256B-aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fmoe_host::opt(fmoe_host::kOptPlan) != 1 && plan_geom(N, T).ok)  // else three launches
+    return fmoe_plan::launch_bucketed(nullptr, nullptr, d_indices, idx_dtype, nullptr, FMOE_F32, N,
+                                      T, 0, 0, d_workspace, true, d_rows, d_row_ptr, s,
+                                      "fmoe_invert_scatter_index");
   const PlanLayout L = plan_layout(N, T);
   char* ws = static_cast<char*>(d_workspace);
   int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);

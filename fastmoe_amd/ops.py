@@ -555,7 +555,7 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
 
     gx_ptr = gx.data_ptr() if gx is not None else None
     gw_ptr = gw.data_ptr() if gw is not None else None
-    fused = os.environ.get("FMOE_BWD_FUSED", "") not in ("", "0")
+    fused = _abi.option("bwd_fused") != 0
     if gx_ptr and gw_ptr and not fused:
         # The grad_X (write) and grad_w (read) passes, one call each -- the same two launches
         # fmoe_combine_bwd makes when given both outputs, issued separately so each is timed.

@@ -84,6 +84,24 @@ FMOE_API int fmoe_abi_version(void);
 FMOE_API const char* fmoe_last_error(void);
 
 /*
+ * Kernel-variant options (no counterpart in the reference, whose Triton kernel has none).  Every
+ * option defaults to the measured-best choice; the environment variable in brackets sets the
+ * starting value once, when the library loads.  Launches read the option table, never the
+ * environment.  Options select among variants that compute the same results (tests compare them):
+ *   "plan"            [FMOE_PLAN]      0 = automatic (one launch up to 2^17 rows, else two),
+ *                                      1 = count/fill/order (three launches; FMOE_PLAN_SPLIT=1),
+ *                                      2 = bucketed (two launches), 3 = one launch
+ *   "bwd_fused"       [FMOE_BWD_FUSED] 1 = both backward gradients in one pass
+ *   "gw_staged"       [FMOE_GW_STAGED] 0 = grad_w pass reads grad_out per wave, not through LDS
+ *   "force_scalar"    [FMOE_FORCE_SCALAR] 1 = element-wise instead of 16-byte accesses
+ *   "bwd_u", "fwd_tile", "fwd_atomic_tile", "fwd_det_u", "fwd_grid": tile shapes (0 = by D)
+ * fmoe_set_option returns FMOE_EINVAL for an unknown name; *previous (if not NULL) gets the old
+ * value.  Not synchronised with launches in flight on other threads.
+ */
+FMOE_API int fmoe_set_option(const char* name, int64_t value, int64_t* previous);
+FMOE_API int fmoe_get_option(const char* name, int64_t* value);
+
+/*
  * Pointer table and row-count metadata of E ragged expert buffers
  * (replaces prepare_grouped_metadata, src/fastmoe/kernels/ops.py:200-271).
  *
@@ -103,10 +121,11 @@ FMOE_API int fmoe_build_metadata(const int64_t* host_ptrs, const int64_t* host_r
 
 /*
  * Plan: token-major inverse of the scatter index.  For each token t, the packed rows g with
- * idx[g] == t, each as a 16-byte record {source row address, fp32 gate, g}; a segment of up to
- * 64 rows is stored in no particular order (the deterministic forward orders it by g in
- * registers), a longer one in ascending g.  Rows with an out-of-range index form one extra
- * segment (number T).
+ * idx[g] == t, each as a 16-byte record {source row address, fp32 gate, g}, in ascending g (the
+ * three-launch fallback for more than 2^22 tokens orders only segments longer than 64 rows; the
+ * consumers order shorter ones in registers).  Rows with an out-of-range index form one extra
+ * segment (number T).  Time is linear in N + T: one launch up to 2^17 rows, two beyond (option
+ * "plan" selects a path for tests).
  *
  * Workspace: fmoe_plan_workspace_bytes(N, T) bytes of device memory, 256-byte aligned, owned by the
  * caller; no zero-fill is needed.  Layout (byte offsets from the workspace base):
@@ -178,8 +197,9 @@ FMOE_API int fmoe_build_metadata_and_plan_from_slots(
  *                            holds the rows whose index lies outside [0, T)
  *   d_rows[N]        int32 : row numbers g, ascending within every segment
  * d_indices : [N] scatter index, FMOE_I64 or FMOE_I32.  Workspace: fmoe_plan_workspace_bytes(N, T)
- * bytes, 256-byte aligned, no zero-fill.  A segment longer than 64 rows is ordered in time
- * quadratic in its length.
+ * bytes, 256-byte aligned, no zero-fill.  Two launches, linear in N + T, up to 2^22 tokens; beyond
+ * that the three-launch fallback orders a segment longer than 64 rows in time quadratic in its
+ * length.
  */
 FMOE_API int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, int64_t num_rows,
                               int64_t num_tokens, int32_t* d_row_ptr, int32_t* d_rows,

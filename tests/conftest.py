@@ -28,3 +28,21 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def kernel_options():
+    """Set kernel-variant options of the library (fmoe_set_option) for one test; the previous
+    values come back at teardown.  Usage: ``kernel_options(plan=1, bwd_fused=1)``."""
+    from fastmoe_amd import _abi
+
+    saved = {}
+
+    def set_options(**values):
+        for k, v in values.items():
+            prev = _abi.set_option(k, v)
+            saved.setdefault(k, prev)
+
+    yield set_options
+    for k, v in saved.items():
+        _abi.set_option(k, v)

@@ -26,6 +26,12 @@ class FakeLib:
     def fmoe_last_error(self):
         return b"fake"
 
+    def fmoe_set_option(self, name, value, prev):
+        return self.real.fmoe_set_option(name, value, prev)
+
+    def fmoe_get_option(self, name, value):
+        return self.real.fmoe_get_option(name, value)
+
     def fmoe_build_metadata(self, host_ptrs, host_rows, E, ptr_table, chunk, offsets, max_rows,
                             stream):
         assert isinstance(E, int) and E >= 1
@@ -117,12 +123,12 @@ def test_autograd_forward_and_backward_calls(fake):
     assert [g.shape[0] for g in grads[1:]] == [3, 0, 5]
 
 
-def test_fused_backward_is_one_call(fake, monkeypatch):
-    monkeypatch.setenv("FMOE_BWD_FUSED", "1")
+def test_fused_backward_is_one_call(fake):
     xs = [x.requires_grad_(True) for x in _experts()]
     w = torch.rand(8, requires_grad=True)
-    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, 4, (8,)), w, (4, 16))
-    torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
+    with _abi.options(bwd_fused=1):
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, 4, (8,)), w, (4, 16))
+        torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
     assert [c[0] for c in fake.calls] == ["metadata_plan", "fwd", "bwd"]
     assert fake.calls[2][6:8] == (True, True)
 

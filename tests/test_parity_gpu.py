@@ -97,21 +97,23 @@ def test_fwd_fp32_atomic_vs_det_on_published_shape():
 # narrower column steps chosen for small D.
 _BWD_VARIANTS = {
     "split": {},
-    "fused": {"FMOE_BWD_FUSED": "1"},
-    "split_u1": {"FMOE_BWD_U": "1"},
-    "fused_u2": {"FMOE_BWD_FUSED": "1", "FMOE_BWD_U": "2"},
+    "fused": {"bwd_fused": 1},
+    "split_u1": {"bwd_u": 1},
+    "fused_u2": {"bwd_fused": 1, "bwd_u": 2},
 }
 
 
-def _set_bwd_variant(monkeypatch, variant):
-    for k, v in _BWD_VARIANTS[variant].items():
-        monkeypatch.setenv(k, v)
+def _set_bwd_variant(kernel_options, variant):
+    kernel_options(**_BWD_VARIANTS[variant])
+
+
+_PLAN_PATHS = {"tok": 3, "bucketed": 2, "split": 1}  # values of the "plan" option
 
 
 @pytest.mark.parametrize("variant", list(_BWD_VARIANTS))
 @pytest.mark.parametrize("name", ["plumbing", "gigachat", "skewed"])
-def test_bwd_grad_x_bitexact_grad_w_close(name, variant, monkeypatch):
-    _set_bwd_variant(monkeypatch, variant)
+def test_bwd_grad_x_bitexact_grad_w_close(name, variant, kernel_options):
+    _set_bwd_variant(kernel_options, variant)
     wl, T, idx, w, experts = _inputs(name)
     xd, idd, wd = _to_dev(experts, idx, w)
     xd = [x.requires_grad_(True) for x in xd]
@@ -133,7 +135,7 @@ def test_bwd_grad_x_bitexact_grad_w_close(name, variant, monkeypatch):
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 16384), (torch.float32, 4104),
                                      (torch.float16, 8200)])
-def test_bwd_grad_w_staged_equals_per_wave(dtype, D, monkeypatch):
+def test_bwd_grad_w_staged_equals_per_wave(dtype, D, kernel_options):
     """The grad_w pass shares grad_out through LDS for tokens of 1-8 rows and reads it per wave
     otherwise (longer segments, the out-of-range segment, or FMOE_GW_STAGED=0): both give the same
     bits, and both meet the oracle's 1e-6 bar.  Row lengths are not multiples of the LDS slice."""
@@ -152,7 +154,7 @@ def test_bwd_grad_w_staged_equals_per_wave(dtype, D, monkeypatch):
     xd, idd, wd = _to_dev(experts, idx, w)
     got = {}
     for staged in ("1", "0"):
-        monkeypatch.setenv("FMOE_GW_STAGED", staged)
+        kernel_options(gw_staged=int(staged))
         wg = wd.clone().requires_grad_(True)
         out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wg, (T, D))
         (got[staged],) = torch.autograd.grad(out, [wg], go.to(DEV))
@@ -163,10 +165,10 @@ def test_bwd_grad_w_staged_equals_per_wave(dtype, D, monkeypatch):
 
 
 @pytest.mark.parametrize("fused", ["0", "1"])
-def test_bwd_abi_both_outputs_in_one_call(fused, monkeypatch):
+def test_bwd_abi_both_outputs_in_one_call(fused, kernel_options):
     """fmoe_combine_bwd given both outputs (the call a C-ABI binding makes): grad_X and grad_w
     from its two back-to-back passes (or the fused pass) equal the oracle."""
-    monkeypatch.setenv("FMOE_BWD_FUSED", fused)
+    kernel_options(bwd_fused=int(fused))
     wl, T, idx, w, experts = _inputs("gigachat")
     xd, idd, wd = _to_dev(experts, idx, w)
     meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
@@ -344,8 +346,8 @@ def test_edge_large_segments_randint():
 
 
 @pytest.mark.parametrize("variant", ["split", "fused"])
-def test_edge_invalid_indices_dropped_and_flagged(variant, monkeypatch):
-    _set_bwd_variant(monkeypatch, variant)
+def test_edge_invalid_indices_dropped_and_flagged(variant, kernel_options):
+    _set_bwd_variant(kernel_options, variant)
     D, T = 32, 6
     gen = torch.Generator().manual_seed(5)
     experts = [torch.randn(4, D, generator=gen), torch.randn(3, D, generator=gen)]
@@ -480,18 +482,18 @@ def _plan_case(case: str):
     return T, idx, torch.rand(N, generator=gen), experts, 8
 
 
-@pytest.mark.parametrize("path", ["fused", "split"])
+@pytest.mark.parametrize("path", list(_PLAN_PATHS))
 @pytest.mark.parametrize("case", ["topk512", "long40", "long_pieces_short", "long_pieces_long",
                                   "wide_hist"])
-def test_plan_matches_oracle(case, path, monkeypatch):
+def test_plan_matches_oracle(case, path, kernel_options):
     """row_ptr, the records (source address, gate bits, g) and the status words equal the
-    oracle's inverse, for the one-launch fused plan and the split count/fill/order plan.  Segments
-    longer than 64 rows must come out in ascending g, including when several workgroups each fill
-    a piece of one segment."""
+    oracle's inverse, for the one-launch plan, the bucketed plan (two launches) and the split
+    count/fill/order plan.  The first two write every segment in ascending g (the records equal
+    the oracle's stable inverse as they are); the split plan orders segments longer than 64 rows,
+    including when several workgroups each fill a piece of one segment."""
     from oracle import cref
 
-    if path == "split":
-        monkeypatch.setenv("FMOE_PLAN_SPLIT", "1")
+    kernel_options(plan=_PLAN_PATHS[path])
     T, idx, w, experts, D = _plan_case(case)
     xd, idd, wd = _to_dev(experts, idx, w)
     meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
@@ -511,12 +513,14 @@ def test_plan_matches_oracle(case, path, monkeypatch):
             assert np.all(np.diff(g[want_rp[b]:want_rp[b + 1]]) > 0), b
     st = ops.plan_status(plan).cpu().numpy()
     misaligned = int((D * experts[0].element_size()) % 16 != 0)
-    # the longest segment is recorded by the split plan only (no workgroup of the one-launch plan
-    # sees every segment)
     assert st[0] == 0 and st[1] == misaligned
-    assert st[2] == (seg_len[:T].max() if path == "split" else -1)
+    # the longest segment: recorded by the split and bucketed plans; -1 from the one-launch plan
+    # (no workgroup sees every segment)
+    assert st[2] == (-1 if path == "tok" else seg_len[:T].max())
     if case != "topk512":
         assert seg_len[:T].max() > 64
+    if path != "split":  # stable: every segment already in ascending g
+        np.testing.assert_array_equal(g, want_g)
     # short segments may be unordered: order each segment by g before comparing
     order = np.concatenate([np.arange(want_rp[b], want_rp[b + 1])[np.argsort(g[want_rp[b]:want_rp[b + 1]])]
                             for b in range(T + 1)])
@@ -563,14 +567,13 @@ def test_bwd_f16_grad_x_rounds_twice_like_the_reference():
     np.testing.assert_array_equal(want_gx.view(np.float16), twice)  # the oracle rounds twice
 
 
-@pytest.mark.parametrize("plan", ["one_launch", "split"])
-def test_random_shapes_against_oracle(plan, monkeypatch):
+@pytest.mark.parametrize("plan", list(_PLAN_PATHS))
+def test_random_shapes_against_oracle(plan, kernel_options):
     """40 seeded random cases: tokens, experts (some empty), rows, D, every dtype combination,
     int32/int64 indices, and out-of-range indices mixed in; forward bits, grad_X bits and grad_w
-    (1e-6 of sum|terms|) against the oracle, through the autograd path, with the one-launch
-    and the three-launch plan."""
-    if plan == "split":
-        monkeypatch.setenv("FMOE_PLAN_SPLIT", "1")
+    (1e-6 of sum|terms|) against the oracle, through the autograd path, with each of the
+    three plans."""
+    kernel_options(plan=_PLAN_PATHS[plan])
     rng = np.random.default_rng(2026)
     dts = [torch.float32, torch.bfloat16, torch.float16]
     for case in range(40):
@@ -617,13 +620,13 @@ def test_random_shapes_against_oracle(plan, monkeypatch):
 
 
 @pytest.mark.parametrize("bwd", ["split", "fused"])
-def test_random_misaligned_buffers_against_oracle(bwd, monkeypatch):
+def test_random_misaligned_buffers_against_oracle(bwd, kernel_options):
     """16 seeded random cases whose buffers sit at arbitrary element offsets of shared pools:
     every expert (some empty) a contiguous view at a random offset, grad_out and an in-place out
     at odd offsets with padded row strides.  Forward (autograd and in place, det) bit-exact,
     grad_X bit-exact and grad_w within 1e-6 of sum|terms|, with the backward's two passes or its
     fused pass."""
-    monkeypatch.setenv("FMOE_BWD_FUSED", "1" if bwd == "fused" else "0")
+    kernel_options(bwd_fused=1 if bwd == "fused" else 0)
     rng = np.random.default_rng(4242)
     dts = [torch.float32, torch.bfloat16, torch.float16]
     for case in range(16):
@@ -721,13 +724,18 @@ def test_random_inplace_against_oracle():
             assert not bool(big[:, D:].any()), label  # the padding columns are never written
 
 
-@pytest.mark.parametrize("T,N", [(1, 1), (1, 5000), (2, 3), (2, 4500)])
-def test_plan_few_tokens(T, N):
-    """One or two tokens: one or two workgroups, a segment of thousands of rows (stash overflow
-    and the long-segment ordering), and out-of-range indices mixed in; the plan and the forward
-    against the oracle."""
+@pytest.mark.parametrize("path", ["tok", "bucketed"])
+@pytest.mark.parametrize("T,N", [(1, 1), (1, 5000), (2, 3), (2, 4500), (1, 100_000)])
+def test_plan_few_tokens(T, N, path, kernel_options):
+    """One or two tokens: a segment of thousands of rows (several partition slices feeding one
+    bucket) and out-of-range indices mixed in; the plan (in exact stable order, with the longest
+    segment recorded) and the forward against the oracle.  One token with 100,000 rows is the
+    regression case of the plan's linear time (an ordering pass quadratic in the segment length
+    takes minutes there); the one-launch plan's waves overflow their stashes there and
+    re-stream their rows."""
     from oracle import cref
 
+    kernel_options(plan=_PLAN_PATHS[path])
     gen = torch.Generator().manual_seed(43 + N)
     D = 12
     idx = torch.randint(0, T, (N,), generator=gen)
@@ -744,12 +752,10 @@ def test_plan_few_tokens(T, N):
     want_rp, want_g = cref.plan(idx.numpy(), T)
     np.testing.assert_array_equal(rp, want_rp)
     g = (rec[:, 1] >> 32).numpy().astype(np.int32)
-    for b in range(T + 1):
-        seg = g[want_rp[b]:want_rp[b + 1]]
-        if b < T and seg.size > 64:
-            assert np.all(np.diff(seg) > 0)  # long segments in ascending g
-        np.testing.assert_array_equal(np.sort(seg), want_g[want_rp[b]:want_rp[b + 1]])
-    assert int(ops.plan_status(plan)[0]) == int((want_rp[T + 1] - want_rp[T]))
+    np.testing.assert_array_equal(g, want_g)  # every segment in ascending g
+    st = ops.plan_status(plan).cpu().numpy()
+    assert int(st[0]) == int((want_rp[T + 1] - want_rp[T]))
+    assert int(st[2]) == (-1 if path == "tok" else int(np.diff(want_rp)[:T].max()))
     out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
     want, _, bad = oracle_fwd(experts, idx, w, T, torch.float32)
     assert bad == want_rp[T + 1] - want_rp[T]
@@ -772,8 +778,8 @@ def _sorted_plan(plan, N, T):
                                   "big_n"])
 def test_metadata_and_plan_in_one_call_equals_two_calls(case):
     """fmoe_build_metadata_and_plan writes exactly what fmoe_build_metadata + fmoe_build_plan
-    write: one launch for up to 256 experts (within the one-launch plan's limits), the two calls
-    otherwise (300 experts, N > 2^20)."""
+    write: the plan's own launches for up to 256 experts, the two calls otherwise (300 experts;
+    N > 2^20 rows is within the bucketed plan's limits)."""
     gen = torch.Generator().manual_seed(31)
     D, dtype, idt, wdt = 8, torch.float32, torch.int64, torch.float32
     if case == "big_n":
@@ -873,9 +879,10 @@ def test_metadata_matches_closed_forms():
 
 
 def test_many_experts_beyond_the_lds_tables():
-    """5000 experts (0-2 rows each): more than the one-launch plan's LDS expert tables (4096) and
-    the metadata's kernel-argument table (256), so metadata and plan take their multi-launch
-    paths; forward bits, grad_X bits and grad_w against the oracle."""
+    """5000 experts (0-2 rows each): more than the plan's LDS expert tables (4096) and the
+    metadata's kernel-argument table (256), so the plan looks experts up in global memory and
+    metadata and plan take separate calls; forward bits, grad_X bits and grad_w against the
+    oracle."""
     gen = torch.Generator().manual_seed(41)
     E, T, D = 5000, 700, 24
     sizes = torch.randint(0, 3, (E,), generator=gen).tolist()
@@ -898,12 +905,12 @@ def test_many_experts_beyond_the_lds_tables():
     assert np.all(np.abs(grads[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
-@pytest.mark.parametrize("path", ["split", "one_launch"])
-def test_large_token_count_plan_paths(path, monkeypatch):
+@pytest.mark.parametrize("path", list(_PLAN_PATHS))
+def test_large_token_count_plan_paths(path, kernel_options):
     """T = 40000: the split plan's histogram exceeds its LDS (33792 bins), so it counts and scans
-    in global memory; the one-launch plan spreads the 40001 bins over 40 workgroups."""
-    if path == "split":
-        monkeypatch.setenv("FMOE_PLAN_SPLIT", "1")
+    in global memory; the bucketed plan groups the 40001 bins into buckets of 64; the one-launch
+    plan spreads them over 255 workgroups."""
+    kernel_options(plan=_PLAN_PATHS[path])
     D, T, k = 16, 40000, 2
     wl = Workload("bigT", T, D, 16, k, torch.float32, 13, False)
     idx, w, counts = make_routing(wl)

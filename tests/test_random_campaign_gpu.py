@@ -44,7 +44,7 @@ def _expect_bits(got: torch.Tensor, want: np.ndarray, label: str) -> None:
                                   else want, err_msg=label)
 
 
-def test_campaign_autograd(monkeypatch):
+def test_campaign_autograd(kernel_options):
     rng = np.random.default_rng(1101)
     for case in range(120):
         T = _logu(rng, 20000)
@@ -74,11 +74,11 @@ def test_campaign_autograd(monkeypatch):
         xdt = DTS[int(rng.integers(3))]
         wdt = [torch.float32, torch.bfloat16][int(rng.integers(2))]
         idt = [torch.int64, torch.int32][int(rng.integers(2))]
-        split, fused = bool(rng.random() < 0.4), bool(rng.random() < 0.25)
-        monkeypatch.setenv("FMOE_PLAN_SPLIT", "1" if split else "0")
-        monkeypatch.setenv("FMOE_BWD_FUSED", "1" if fused else "0")
+        r, fused = rng.random(), bool(rng.random() < 0.25)
+        plan = 1 if r < 0.25 else (2 if r < 0.4 else 0)  # three launches / bucketed / automatic
+        kernel_options(plan=plan, bwd_fused=1 if fused else 0)
         label = (f"autograd case {case}: T={T} N={N} E={E} D={D} {routing} {xdt} {wdt} {idt} "
-                 f"split={split} fused={fused}")
+                 f"plan={plan} fused={fused}")
         gen = torch.Generator().manual_seed(1101 * 1000 + case)
         idx_t = torch.from_numpy(np.asarray(idx, dtype=np.int64)).to(idt)
         w = torch.rand(N, generator=gen).to(wdt)
@@ -99,7 +99,7 @@ def test_campaign_autograd(monkeypatch):
         assert np.all(err <= 1e-6 * scale + rtol * np.abs(want_gw) + 1e-30), label
 
 
-def test_campaign_permutation_and_inplace(monkeypatch):
+def test_campaign_permutation_and_inplace(kernel_options):
     rng = np.random.default_rng(2202)
     for case in range(160):
         gen = torch.Generator().manual_seed(2202 * 1000 + case)
@@ -145,15 +145,16 @@ def test_campaign_permutation_and_inplace(monkeypatch):
             pad = int(rng.choice([0, 0, 8, 40]))
             xdt, odt = DTS[int(rng.integers(3))], DTS[int(rng.integers(3))]
             mode = "atomic" if (odt == torch.float32 and rng.random() < 0.4) else "det"
-            split = bool(rng.random() < 0.4)
-            monkeypatch.setenv("FMOE_PLAN_SPLIT", "1" if split else "0")
+            r = rng.random()
+            plan = 1 if r < 0.25 else (2 if r < 0.4 else 0)  # three launches / bucketed / auto
+            kernel_options(plan=plan)
             sizes = _split(rng, N, E)
             idx = torch.from_numpy(rng.integers(0, T, N))
             if rng.random() < 0.25:
                 idx[:: int(rng.integers(3, 40))] = -1
             with_meta = bool(rng.random() < 0.5)
             label = (f"in-place case {case}: T={T} N={N} E={E} D={D} pad={pad} {xdt} out {odt} "
-                     f"{mode} split={split} metadata={with_meta}")
+                     f"{mode} plan={plan} metadata={with_meta}")
             w = torch.rand(N, generator=gen)
             experts = [torch.randn(n, D, generator=gen).to(xdt) for n in sizes]
             init = torch.randn(T, D, generator=gen).to(odt)
@@ -176,7 +177,7 @@ def test_campaign_permutation_and_inplace(monkeypatch):
                 assert not bool(big[:, D:].any()), label
 
 
-def test_campaign_inverse_slot_plan_and_graphs(monkeypatch):
+def test_campaign_inverse_slot_plan_and_graphs(kernel_options):
     rng = np.random.default_rng(3303)
     for case in range(150):
         gen = torch.Generator().manual_seed(3303 * 1000 + case)
