@@ -272,7 +272,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gigachat")
-    ap.add_argument("--mode", default="det", choices=["det", "atomic"])
+    ap.add_argument("--mode", default="det", choices=["det", "atomic", "atomic_packed"])
     ap.add_argument("--path", default="combine", choices=["combine", "dispatch", "moe"],
                     help="combine: the grouped combine (the headline); dispatch: the permutation "
                          "that feeds it (gate_and_sort's sort + gather) and its backward; moe: "

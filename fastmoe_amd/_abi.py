@@ -13,11 +13,11 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfastmoe_amd.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum fmoe_dtype / fmoe_mode / fmoe_status (include/fastmoe_amd.h)
 F32, BF16, F16, I64, I32 = 0, 1, 2, 3, 4
-MODE_DET, MODE_ATOMIC = 0, 1
+MODE_DET, MODE_ATOMIC, MODE_ATOMIC_PACKED = 0, 1, 2
 OK, EINVAL, EHIP, ERANGE = 0, -1, -2, -3
 
 _c_i64 = ctypes.c_int64
@@ -59,10 +59,11 @@ SIGNATURES: dict[str, tuple] = {
     "fmoe_invert_scatter_index": (
         _c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp],
     ),
+    "fmoe_combine_fwd_workspace_bytes": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
     "fmoe_combine_fwd": (
         _c_int,
         [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
-         _c_int, _c_vp, _c_int, _c_i64, _c_int, _c_vp],
+         _c_int, _c_vp, _c_int, _c_i64, _c_int, _c_vp, _c_i64, _c_vp],
     ),
     "fmoe_combine_fwd_noalloc": (
         _c_int,

@@ -1,7 +1,7 @@
 // Forward combine: out[idx[g], :] += w[g] * X_e[g - off[e], :]
 //
 // Replaces _launch_grouped_kernel + _grouped_weighted_scatter_add_kernel
-// (src/fastmoe/kernels/ops.py:277-310, :57-194).  Two modes:
+// (src/fastmoe/kernels/ops.py:277-310, :57-194).  Three modes:
 //
 // DET (token-major).  A wave owns one (token, column chunk).  It walks the token's plan segment in
 // ascending packed-row order (ordering a short segment in registers first), loads 16 bytes per
@@ -14,9 +14,16 @@
 //
 // ATOMIC (packed-row-major, the reference kernel's order).  A wave owns one (row g, column chunk):
 // binary-searches g's expert in the offsets (ops.py:151-154 does offsets + program id instead),
-// loads the row, scales it and adds it into out[idx[g]] with gfx950 hardware float atomics
-// (global_atomic_add_f32, global_atomic_pk_add_bf16 / _f16 on element pairs).  Needs a zero-filled
-// out and is not reproducible bit for bit.
+// loads the row, scales it and adds it into out[idx[g]] with global_atomic_add_f32.  A 16-bit
+// output is accumulated in an fp32 workspace (initialised from out, or zeroed) and converted once
+// at the end, so it is the fp32 sum rounded once, like the deterministic mode's; only the order of
+// the fp32 additions differs run to run.
+//
+// ATOMIC_PACKED.  As ATOMIC, but a 16-bit output takes gfx950's packed atomics
+// (global_atomic_pk_add_bf16 / _f16) on element pairs directly: no workspace and half the atomic
+// requests, but every add rounds to 16 bits (the reference kernel's behaviour with a bf16 output).
+#include <algorithm>
+
 #include "common.h"
 
 namespace fmoe {
@@ -216,6 +223,135 @@ __global__ __launch_bounds__(kGroup) void k_fwd_atomic(
     fwd_atomic_body<TX, TO, V, U, true>(src, wf, orow, D, chunk);
 }
 
+// ---- fp32 accumulator of a 16-bit output, and zero-fill of an overwritten output --------------
+// Row-major passes over [T, D]: a thread per 8 consecutive columns of a row, with 16-byte accesses
+// when the rows allow them (VEC: D % 8 == 0 and 16-byte aligned rows), element accesses otherwise.
+// The accumulator is a contiguous, 16-byte aligned fp32 [T, D] workspace.
+constexpr int kAccCols = 8;
+
+template <typename TO, bool VEC>
+__global__ __launch_bounds__(kGroup) void k_acc_init(float* __restrict__ acc,
+                                                     const TO* __restrict__ out, int64_t out_stride,
+                                                     uint32_t D, uint32_t T, int accumulate) {
+  const uint32_t groups = (D + kAccCols - 1) / kAccCols;
+  const int64_t total = (int64_t)T * groups;
+  for (int64_t i = (int64_t)blockIdx.x * kGroup + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kGroup) {
+    const uint32_t t = (uint32_t)(i / groups);
+    const uint32_t c = (uint32_t)(i - (int64_t)t * groups) * kAccCols;
+    const TO* o = out + (int64_t)t * out_stride + c;
+    float* a = acc + (int64_t)t * D + c;
+    float f[kAccCols];
+    if (!accumulate) {
+#pragma unroll
+      for (int k = 0; k < kAccCols; ++k) f[k] = 0.f;
+    } else if constexpr (VEC) {
+      Vec<TO, kAccCols>::cvt(*reinterpret_cast<const u32x4*>(o), f);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kAccCols; ++k) f[k] = c + k < D ? ld1(o + k) : 0.f;
+    }
+    if constexpr (VEC) {
+      reinterpret_cast<u32x4*>(a)[0] = u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]),
+                                             __float_as_uint(f[2]), __float_as_uint(f[3])};
+      reinterpret_cast<u32x4*>(a)[1] = u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]),
+                                             __float_as_uint(f[6]), __float_as_uint(f[7])};
+    } else {
+#pragma unroll
+      for (int k = 0; k < kAccCols; ++k)
+        if (c + k < D) a[k] = f[k];
+    }
+  }
+}
+
+template <typename TO, bool VEC>
+__global__ __launch_bounds__(kGroup) void k_acc_store(const float* __restrict__ acc,
+                                                      TO* __restrict__ out, int64_t out_stride,
+                                                      uint32_t D, uint32_t T) {
+  const uint32_t groups = (D + kAccCols - 1) / kAccCols;
+  const int64_t total = (int64_t)T * groups;
+  for (int64_t i = (int64_t)blockIdx.x * kGroup + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kGroup) {
+    const uint32_t t = (uint32_t)(i / groups);
+    const uint32_t c = (uint32_t)(i - (int64_t)t * groups) * kAccCols;
+    const float* a = acc + (int64_t)t * D + c;
+    TO* o = out + (int64_t)t * out_stride + c;
+    if constexpr (VEC) {
+      const u32x4 lo = reinterpret_cast<const u32x4*>(a)[0];
+      const u32x4 hi = reinterpret_cast<const u32x4*>(a)[1];
+      const float f[kAccCols] = {__uint_as_float(lo.x), __uint_as_float(lo.y),
+                                 __uint_as_float(lo.z), __uint_as_float(lo.w),
+                                 __uint_as_float(hi.x), __uint_as_float(hi.y),
+                                 __uint_as_float(hi.z), __uint_as_float(hi.w)};
+      *reinterpret_cast<u32x4*>(o) = Vec<TO, kAccCols>::pack(f);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kAccCols; ++k)
+        if (c + k < D) st1(o + k, a[k]);
+    }
+  }
+}
+
+// out[t, :] = 0 for every row (an atomic-mode call that overwrites out).
+template <typename TO>
+__global__ __launch_bounds__(kGroup) void k_rows_zero(TO* __restrict__ out, int64_t out_stride,
+                                                      uint32_t D, uint32_t T) {
+  const uint32_t groups = (D + kAccCols - 1) / kAccCols;
+  const int64_t total = (int64_t)T * groups;
+  for (int64_t i = (int64_t)blockIdx.x * kGroup + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kGroup) {
+    const uint32_t t = (uint32_t)(i / groups);
+    const uint32_t c = (uint32_t)(i - (int64_t)t * groups) * kAccCols;
+    TO* o = out + (int64_t)t * out_stride + c;
+#pragma unroll
+    for (int k = 0; k < kAccCols; ++k)
+      if (c + k < D) st1(o + k, 0.f);
+  }
+}
+
+static unsigned row_pass_blocks(int64_t T, int64_t D) {
+  const int64_t threads = T * ((D + kAccCols - 1) / kAccCols);
+  return (unsigned)std::min<int64_t>((threads + kGroup - 1) / kGroup, int64_t(1) << 16);
+}
+
+template <typename TO>
+static int launch_zero(void* out, int64_t stride, int64_t D, int64_t T, hipStream_t s) {
+  hipLaunchKernelGGL((k_rows_zero<TO>), dim3(row_pass_blocks(T, D)), dim3(kGroup), 0, s,
+                     static_cast<TO*>(out), stride, (uint32_t)D, (uint32_t)T);
+  return fmoe_host::check_launch("fmoe_combine_fwd(zero out)");
+}
+
+static int zero_out(void* out, int out_dtype, int64_t stride, int64_t D, int64_t T,
+                    hipStream_t s) {
+  if (out_dtype == FMOE_F32) return launch_zero<float>(out, stride, D, T, s);
+  if (out_dtype == FMOE_BF16) return launch_zero<bf16_t>(out, stride, D, T, s);
+  return launch_zero<f16_t>(out, stride, D, T, s);
+}
+
+template <typename TO>
+static int launch_acc_pass(bool init, float* acc, void* out, int64_t stride, int64_t D, int64_t T,
+                           int accumulate, hipStream_t s) {
+  const bool vec = D % kAccCols == 0 && (uintptr_t)out % 16 == 0 &&
+                   (stride * (int64_t)sizeof(TO)) % 16 == 0;
+  const dim3 grid(row_pass_blocks(T, D));
+  if (init) {
+    if (vec)
+      hipLaunchKernelGGL((k_acc_init<TO, true>), grid, dim3(kGroup), 0, s, acc,
+                         static_cast<const TO*>(out), stride, (uint32_t)D, (uint32_t)T, accumulate);
+    else
+      hipLaunchKernelGGL((k_acc_init<TO, false>), grid, dim3(kGroup), 0, s, acc,
+                         static_cast<const TO*>(out), stride, (uint32_t)D, (uint32_t)T, accumulate);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((k_acc_store<TO, true>), grid, dim3(kGroup), 0, s, acc,
+                         static_cast<TO*>(out), stride, (uint32_t)D, (uint32_t)T);
+    else
+      hipLaunchKernelGGL((k_acc_store<TO, false>), grid, dim3(kGroup), 0, s, acc,
+                         static_cast<TO*>(out), stride, (uint32_t)D, (uint32_t)T);
+  }
+  return fmoe_host::check_launch("fmoe_combine_fwd(fp32 accumulator)");
+}
+
 // ---- host dispatch ---------------------------------------------------------------------------
 // Vectors per lane per row: several 16-byte loads in flight per row, and preferably a chunk
 // width that divides D (no tail predication), while small D still spreads over many waves.
@@ -273,8 +409,8 @@ static int launch_fwd_k(const FwdArgs& a, int64_t chunks) {
   }
   if constexpr (V == 1 && sizeof(TO) == 2) {
     fmoe_host::set_error(
-        "fmoe_combine_fwd(atomic): a 16-bit output needs D %% %d == 0 and %d-byte aligned output "
-        "rows (packed atomics on element pairs); use the deterministic mode",
+        "fmoe_combine_fwd(atomic_packed): a 16-bit output needs D %% %d == 0 and %d-byte aligned "
+        "output rows (packed atomics on element pairs); use FMOE_MODE_ATOMIC or FMOE_MODE_DET",
         vec16<TX>(), vec16<TX>() * 2);
     return FMOE_EINVAL;
   } else {
@@ -339,16 +475,24 @@ static int launch_fwd_x(const FwdArgs& a, int out_dtype) {
 
 }  // namespace fmoe
 
+extern "C" int64_t fmoe_combine_fwd_workspace_bytes(int mode, int64_t num_tokens, int64_t hidden,
+                                                    int out_dtype) {
+  if (num_tokens < 1 || hidden < 1) return -1;
+  if (mode == FMOE_MODE_ATOMIC && (out_dtype == FMOE_BF16 || out_dtype == FMOE_F16))
+    return fmoe_host::round_up(num_tokens * hidden * 4, 256);
+  return 0;
+}
+
 extern "C" int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indices, int idx_dtype,
                                 const void* d_weights, int w_dtype, const int64_t* d_ptr_table,
                                 const int64_t* d_offsets, int64_t num_experts, int64_t num_rows,
                                 int64_t num_tokens, int64_t hidden, int x_dtype, void* d_out,
                                 int out_dtype, int64_t out_row_stride, int accumulate,
-                                void* stream) {
+                                void* d_workspace, int64_t workspace_bytes, void* stream) {
   using namespace fmoe;
   fmoe_host::clear_error();
-  FMOE_REQUIRE(mode == FMOE_MODE_DET || mode == FMOE_MODE_ATOMIC, "fmoe_combine_fwd: bad mode %d",
-               mode);
+  FMOE_REQUIRE(mode == FMOE_MODE_DET || mode == FMOE_MODE_ATOMIC || mode == FMOE_MODE_ATOMIC_PACKED,
+               "fmoe_combine_fwd: bad mode %d", mode);
   FMOE_REQUIRE(num_rows >= 0 && num_tokens >= 1 && hidden >= 1,
                "fmoe_combine_fwd: bad sizes N=%lld T=%lld D=%lld", (long long)num_rows,
                (long long)num_tokens, (long long)hidden);
@@ -383,27 +527,63 @@ extern "C" int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indi
     a.status = reinterpret_cast<const int32_t*>(ws + fmoe_plan_status_offset());
     a.row_ptr = reinterpret_cast<const int32_t*>(ws + fmoe_plan_row_ptr_offset(a.N, a.T));
     a.rec = reinterpret_cast<const Rec*>(ws + fmoe_plan_records_offset(a.N, a.T));
-  } else {
-    if (num_rows == 0) return FMOE_OK;
-    FMOE_REQUIRE(d_indices && d_weights && d_ptr_table && d_offsets,
-                 "fmoe_combine_fwd(atomic): null index/weight/metadata pointer");
-    FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype), "fmoe_combine_fwd: bad index dtype %d",
-                 idx_dtype);
-    FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_combine_fwd: bad weight dtype %d",
-                 w_dtype);
-    FMOE_REQUIRE(num_experts >= 1, "fmoe_combine_fwd: num_experts must be >= 1");
-    a.idx = d_indices;
-    a.idx_dtype = idx_dtype;
-    a.w = d_weights;
-    a.w_dtype = w_dtype;
-    a.ptr_table = d_ptr_table;
-    a.offsets = d_offsets;
+    switch (x_dtype) {
+      case FMOE_F32: return launch_fwd_x<float>(a, out_dtype);
+      case FMOE_BF16: return launch_fwd_x<bf16_t>(a, out_dtype);
+      case FMOE_F16: return launch_fwd_x<f16_t>(a, out_dtype);
+    }
+    fmoe_host::set_error("fmoe_combine_fwd: bad x dtype %d", x_dtype);
+    return FMOE_EINVAL;
   }
+  // atomic modes: the fp32 accumulator of a 16-bit output first (its size is checked before any
+  // launch)
+  const bool acc16 = mode == FMOE_MODE_ATOMIC && out_dtype != FMOE_F32;
+  const int64_t need = fmoe_combine_fwd_workspace_bytes(mode, num_tokens, hidden, out_dtype);
+  if (acc16)
+    FMOE_REQUIRE(d_workspace && workspace_bytes >= need && ((uintptr_t)d_workspace & 15) == 0,
+                 "fmoe_combine_fwd(atomic): a 16-bit output needs a 16-byte aligned fp32 "
+                 "workspace of %lld bytes (fmoe_combine_fwd_workspace_bytes), got %lld",
+                 (long long)need, (long long)workspace_bytes);
+  if (num_rows == 0)  // nothing to add: an overwrite still clears out
+    return accumulate ? FMOE_OK : zero_out(d_out, out_dtype, out_row_stride, hidden, num_tokens, a.s);
+  FMOE_REQUIRE(d_indices && d_weights && d_ptr_table && d_offsets,
+               "fmoe_combine_fwd(atomic): null index/weight/metadata pointer");
+  FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype), "fmoe_combine_fwd: bad index dtype %d",
+               idx_dtype);
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_combine_fwd: bad weight dtype %d",
+               w_dtype);
+  FMOE_REQUIRE(num_experts >= 1, "fmoe_combine_fwd: num_experts must be >= 1");
+  a.idx = d_indices;
+  a.idx_dtype = idx_dtype;
+  a.w = d_weights;
+  a.w_dtype = w_dtype;
+  a.ptr_table = d_ptr_table;
+  a.offsets = d_offsets;
+  int target_dtype = out_dtype;
+  float* acc = static_cast<float*>(d_workspace);
+  if (acc16) {
+    const int rc = out_dtype == FMOE_BF16
+                       ? launch_acc_pass<bf16_t>(true, acc, d_out, out_row_stride, hidden,
+                                                 num_tokens, accumulate, a.s)
+                       : launch_acc_pass<f16_t>(true, acc, d_out, out_row_stride, hidden,
+                                                num_tokens, accumulate, a.s);
+    if (rc) return rc;
+    a.out = acc;
+    a.out_stride = hidden;
+    target_dtype = FMOE_F32;
+  } else if (!accumulate) {
+    if (int rc = zero_out(d_out, out_dtype, out_row_stride, hidden, num_tokens, a.s)) return rc;
+  }
+  int rc = FMOE_EINVAL;
   switch (x_dtype) {
-    case FMOE_F32: return launch_fwd_x<float>(a, out_dtype);
-    case FMOE_BF16: return launch_fwd_x<bf16_t>(a, out_dtype);
-    case FMOE_F16: return launch_fwd_x<f16_t>(a, out_dtype);
+    case FMOE_F32: rc = launch_fwd_x<float>(a, target_dtype); break;
+    case FMOE_BF16: rc = launch_fwd_x<bf16_t>(a, target_dtype); break;
+    case FMOE_F16: rc = launch_fwd_x<f16_t>(a, target_dtype); break;
   }
-  fmoe_host::set_error("fmoe_combine_fwd: bad x dtype %d", x_dtype);
-  return FMOE_EINVAL;
+  if (rc || !acc16) return rc;
+  return out_dtype == FMOE_BF16
+             ? launch_acc_pass<bf16_t>(false, acc, d_out, out_row_stride, hidden, num_tokens, 1,
+                                       a.s)
+             : launch_acc_pass<f16_t>(false, acc, d_out, out_row_stride, hidden, num_tokens, 1,
+                                      a.s);
 }

@@ -121,5 +121,5 @@ extern "C" int fmoe_combine_fwd_noalloc(const int64_t* host_ptrs, const int64_t*
     return rc;
   return fmoe_combine_fwd(FMOE_MODE_DET, plan, nullptr, FMOE_I64, nullptr, FMOE_F32, ptr_table,
                           offsets, E, N, T, hidden, x_dtype, d_out, out_dtype, out_row_stride,
-                          accumulate, stream);
+                          accumulate, nullptr, 0, stream);
 }

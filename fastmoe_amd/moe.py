@@ -27,7 +27,7 @@ import torch.nn.functional as F
 
 from .consts import MoEImplementation
 from .dispatch import PermutedTokens, permute_tokens
-from .ops import _GroupedCombinePermuted, grouped_weighted_scatter_add
+from .ops import _apply, _GroupedCombinePermuted, grouped_weighted_scatter_add
 
 __all__ = ["MoEFeedForward", "compute_experts", "gate_and_sort", "unpermute"]
 
@@ -88,8 +88,8 @@ def unpermute(x_out: Union[torch.Tensor, Sequence[torch.Tensor]], reverse_map_in
     if impl == MoEImplementation.FAST:
         if permutation is not None:
             k = permutation.slot_pos.numel() // (B * T) if B * T else 0
-            out = _GroupedCombinePermuted.apply((permutation.slot_pos, k), reverse_map_indices,
-                                                sorted_weights, (B * T, D), *parts)
+            out = _apply(_GroupedCombinePermuted, (permutation.slot_pos, k), reverse_map_indices,
+                         sorted_weights, (B * T, D), *parts)
         else:
             out = grouped_weighted_scatter_add(parts, reverse_map_indices, sorted_weights,
                                                (B * T, D))

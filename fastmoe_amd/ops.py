@@ -23,8 +23,11 @@ Differences from the reference, each deliberate:
   * The backward also returns the gate gradient when ``weights.requires_grad`` (the reference
     returns None, ops.py:358-359).
   * ``mode`` selects the forward kernel: "det" (default; token-major, fixed-order, bit-identical
-    run to run) or "atomic" (hardware float atomics in packed-row order, like the reference's
-    Triton kernel).  The default comes from ``FASTMOE_COMBINE_MODE``.
+    run to run), "atomic" (hardware fp32 atomics in packed-row order, like the reference's Triton
+    kernel; a bf16/f16 output is accumulated in fp32 and rounded once) or "atomic_packed" (a
+    bf16/f16 output takes packed 16-bit atomics directly, rounding at every add, as the Triton
+    kernel does with a bf16 output).  ``FASTMOE_COMBINE_MODE`` sets the default when the module
+    is imported.
   * Scatter indices outside [0, T) are dropped by the forward and get zero gradient instead of
     faulting; ``validate=True`` (or ``FASTMOE_VALIDATE=1``) raises IndexError for them at the cost
     of one device->host synchronisation.
@@ -64,20 +67,24 @@ def _span(name: str):
 
 _FLOAT_CODES = {torch.float32: _abi.F32, torch.bfloat16: _abi.BF16, torch.float16: _abi.F16}
 _INDEX_CODES = {torch.int64: _abi.I64, torch.int32: _abi.I32}
-_MODES = {"det": _abi.MODE_DET, "atomic": _abi.MODE_ATOMIC}
+_MODES = {"det": _abi.MODE_DET, "atomic": _abi.MODE_ATOMIC,
+          "atomic_packed": _abi.MODE_ATOMIC_PACKED}
+
+# Defaults of ``mode`` and ``validate``, read from the environment once, at import.
+_DEFAULT_MODE = os.environ.get("FASTMOE_COMBINE_MODE", "det")
+_DEFAULT_VALIDATE = os.environ.get("FASTMOE_VALIDATE", "0") not in ("", "0")
 
 
 def _mode_code(mode: Optional[str]) -> int:
-    name = (mode or os.environ.get("FASTMOE_COMBINE_MODE", "det")).lower()
+    name = (mode or _DEFAULT_MODE).lower()
     if name not in _MODES:
-        raise ValueError(f"fastmoe_amd: unknown combine mode {name!r} (expected 'det' or 'atomic')")
+        raise ValueError(f"fastmoe_amd: unknown combine mode {name!r} "
+                         f"(expected one of {sorted(_MODES)})")
     return _MODES[name]
 
 
 def _validate_default(validate: Optional[bool]) -> bool:
-    if validate is not None:
-        return bool(validate)
-    return os.environ.get("FASTMOE_VALIDATE", "0") not in ("", "0")
+    return _DEFAULT_VALIDATE if validate is None else bool(validate)
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -122,7 +129,6 @@ class GroupedMetadata(tuple):
         self.hidden = extra["hidden"]
         self.dtype = extra["dtype"]
         self.device = extra["device"]
-        self.device_index = self.tensors[0].get_device()
         self.num_rows = sum(self.sizes)
         return self
 
@@ -139,17 +145,24 @@ class GroupedMetadata(tuple):
         match)."""
         if len(expert_tensors) != len(self.ptrs):
             return False
-        dev_index = self.device_index
-        return all(
-            t.shape[0] == n and (t.data_ptr() if n else 0) == p and t.dtype == self.dtype
-            and t.dim() == 2 and t.shape[1] == self.hidden and t.get_device() == dev_index
-            and t.is_contiguous()
-            for t, p, n in zip(expert_tensors, self.ptrs, self.sizes)
-        )
+        try:
+            checked = _check_experts(expert_tensors)
+        except (ValueError, TypeError, RuntimeError):
+            return False
+        return (checked[0] == self.dtype and checked[1] == self.device
+                and checked[2] == self.hidden and tuple(checked[3]) == self.sizes
+                and tuple(checked[4]) == self.ptrs)
 
 
 def _check_experts(expert_tensors: Sequence[torch.Tensor]):
-    """Validate the expert buffers in one pass; returns (dtype, device, hidden, sizes, ptrs)."""
+    """Validate the expert buffers; returns (dtype, device, hidden, sizes, ptrs).
+
+    Every buffer must be a 2-D [rows, D] tensor of one float dtype on one GPU, row-contiguous
+    (``is_contiguous()`` on a 2-D tensor is exactly the layout the kernels address: strides (D, 1)
+    for several rows, a unit column stride for one row, anything for no rows).  With hundreds of
+    experts this runs on every call, so each property is read once per tensor in a comprehension;
+    only a failing list is walked again, to name the first offending buffer.
+    """
     if len(expert_tensors) == 0:
         raise ValueError("fastmoe_amd: expert_tensors is empty")
     ref = expert_tensors[0]
@@ -159,25 +172,41 @@ def _check_experts(expert_tensors: Sequence[torch.Tensor]):
     if ref.dim() != 2:
         raise ValueError(f"fastmoe_amd: expert tensors must be 2-D [rows, D], got {tuple(ref.shape)}")
     dtype, device, hidden = ref.dtype, ref.device, ref.shape[1]
-    dev_index = ref.get_device()
-    sizes, ptrs = [], []
+    shapes = [t.shape for t in expert_tensors]
+    if ({t.dtype for t in expert_tensors} != {dtype}
+            or {t.device for t in expert_tensors} != {device}
+            or not all([len(sh) == 2 and sh[1] == hidden for sh in shapes])
+            or not all([t.is_contiguous() for t in expert_tensors])):
+        _explain_bad_expert(expert_tensors, dtype, device, hidden)
+    return dtype, device, hidden, [sh[0] for sh in shapes], [t.data_ptr() for t in expert_tensors]
+
+
+def _explain_bad_expert(expert_tensors, dtype, device, hidden) -> None:
     for i, t in enumerate(expert_tensors):
-        shape = t.shape
-        # is_contiguous() on a 2-D tensor is exactly the layout the kernels address: strides
-        # (D, 1) for several rows, a unit column stride for one row, anything for no rows.
-        if (t.dtype != dtype or t.get_device() != dev_index or len(shape) != 2
-                or shape[1] != hidden or not t.is_contiguous()):
-            if t.dtype != dtype or t.get_device() != dev_index:
-                raise ValueError(f"fastmoe_amd: expert_tensors[{i}] differs in device/dtype from [0]")
-            if len(shape) != 2 or shape[1] != hidden:
-                raise ValueError(f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(shape)}, "
-                                 f"expected [*, {hidden}]")
+        if t.dtype != dtype or t.device != device:
+            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] differs in device/dtype from [0]")
+        if t.dim() != 2 or t.shape[1] != hidden:
+            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(t.shape)}, "
+                             f"expected [*, {hidden}]")
+        if not t.is_contiguous():
             raise ValueError(
                 f"fastmoe_amd: expert_tensors[{i}] must be row-contiguous (strides {t.stride()})")
-        n = shape[0]
-        sizes.append(n)
-        ptrs.append(t.data_ptr() if n else 0)
-    return dtype, device, hidden, sizes, ptrs
+    raise AssertionError("unreachable")
+
+
+def _host_table(values) -> ctypes.Array:
+    """int64 host array for the C ABI."""
+    return (ctypes.c_int64 * len(values))(*values)
+
+
+def _meta_arrays(E: int, dev, plan_bytes: int = 0):
+    """Device arrays of the metadata (ptr_table int64[E], chunk_sizes int32[E], offsets
+    int64[E + 1], max_rows int32[1]) and, if asked for, the plan workspace."""
+    return (torch.empty(E, dtype=torch.int64, device=dev),
+            torch.empty(E, dtype=torch.int32, device=dev),
+            torch.empty(E + 1, dtype=torch.int64, device=dev),
+            torch.empty(1, dtype=torch.int32, device=dev),
+            torch.empty(plan_bytes, dtype=torch.uint8, device=dev) if plan_bytes else None)
 
 
 def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None) -> GroupedMetadata:
@@ -193,27 +222,28 @@ def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None
     return _metadata(expert_tensors, checked)
 
 
-def _metadata(expert_tensors, checked) -> GroupedMetadata:
+def _new_metadata(expert_tensors, checked, arrays) -> GroupedMetadata:
     dtype, dev, hidden, sizes, ptrs = checked
-    lib = _abi.lib()
-    E = len(expert_tensors)
-    ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
-    chunk_sizes = torch.empty(E, dtype=torch.int32, device=dev)
-    offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
-    max_rows_dev = torch.empty(1, dtype=torch.int32, device=dev)
-    host_ptrs = (ctypes.c_int64 * E)(*ptrs)
-    host_rows = (ctypes.c_int64 * E)(*sizes)
-    with torch.cuda.device(dev), _span("metadata"):
-        rc = lib.fmoe_build_metadata(
-            host_ptrs, host_rows, E, ptr_table.data_ptr(), chunk_sizes.data_ptr(),
-            offsets.data_ptr(), max_rows_dev.data_ptr(), _stream_handle(dev),
-        )
-    _abi.check(rc, "fmoe_build_metadata")
+    ptr_table, chunk_sizes, offsets, max_rows_dev, _ = arrays
     return GroupedMetadata(
-        ptr_table, chunk_sizes, offsets, max(sizes), E,
+        ptr_table, chunk_sizes, offsets, max(sizes), len(sizes),
         max_rows_device=max_rows_dev, tensors=expert_tensors, sizes=sizes, ptrs=ptrs,
         hidden=hidden, dtype=dtype, device=dev,
     )
+
+
+def _metadata(expert_tensors, checked) -> GroupedMetadata:
+    dtype, dev, hidden, sizes, ptrs = checked
+    lib = _abi.lib()
+    E = len(sizes)
+    arrays = _meta_arrays(E, dev)
+    with torch.cuda.device(dev), _span("metadata"):
+        rc = lib.fmoe_build_metadata(
+            _host_table(ptrs), _host_table(sizes), E, arrays[0].data_ptr(), arrays[1].data_ptr(),
+            arrays[2].data_ptr(), arrays[3].data_ptr(), _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_build_metadata")
+    return _new_metadata(expert_tensors, checked, arrays)
 
 
 def _routing_args(indices: torch.Tensor, weights: torch.Tensor, num_rows: int, dev):
@@ -233,6 +263,30 @@ def _routing_args(indices: torch.Tensor, weights: torch.Tensor, num_rows: int, d
     return indices.reshape(-1).contiguous(), weights.reshape(-1).contiguous()
 
 
+def _check_plan_status(plan: torch.Tensor, num_tokens: int) -> None:
+    bad = int(plan_status(plan)[0])
+    if bad:
+        raise IndexError(f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})")
+
+
+def _build_plan_raw(ptr_table, offsets_full, E: int, N: int, row_bytes: int, idx, w,
+                    num_tokens: int, dev) -> torch.Tensor:
+    """fmoe_build_plan into a new workspace; idx and w already flat and checked."""
+    lib = _abi.lib()
+    nbytes = lib.fmoe_plan_workspace_bytes(N, num_tokens)
+    if nbytes <= 0:
+        raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev), _span("plan"):
+        rc = lib.fmoe_build_plan(
+            idx.data_ptr(), _INDEX_CODES[idx.dtype], w.data_ptr(), _FLOAT_CODES[w.dtype], N,
+            num_tokens, ptr_table.data_ptr(), offsets_full.data_ptr(), E, row_bytes,
+            ws.data_ptr(), _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_build_plan")
+    return ws
+
+
 def build_plan(meta: GroupedMetadata, indices: torch.Tensor, weights: torch.Tensor,
                num_tokens: int, validate: Optional[bool] = None) -> torch.Tensor:
     """Token-major inverse of ``indices`` (``fmoe_build_plan``) as an opaque uint8 device tensor.
@@ -240,27 +294,13 @@ def build_plan(meta: GroupedMetadata, indices: torch.Tensor, weights: torch.Tens
     The deterministic forward and the backward read it.  With ``validate`` it synchronises once
     and raises IndexError if any index lies outside [0, num_tokens).
     """
-    lib = _abi.lib()
     N = meta.num_rows
     idx, w = _routing_args(indices, weights, N, meta.device)
-    nbytes = lib.fmoe_plan_workspace_bytes(N, num_tokens)
-    if nbytes <= 0:
-        raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=meta.device)
-    with torch.cuda.device(meta.device), _span("plan"):
-        rc = lib.fmoe_build_plan(
-            idx.data_ptr(), _INDEX_CODES[idx.dtype], w.data_ptr(), _FLOAT_CODES[w.dtype], N,
-            num_tokens, meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(), len(meta.sizes),
-            meta.hidden * meta.tensors[0].element_size(), ws.data_ptr(),
-            _stream_handle(meta.device),
-        )
-    _abi.check(rc, "fmoe_build_plan")
+    ws = _build_plan_raw(meta.ptr_table, meta.offsets_full, len(meta.sizes), N,
+                         meta.hidden * meta.tensors[0].element_size(), idx, w, num_tokens,
+                         meta.device)
     if _validate_default(validate):
-        bad = int(plan_status(ws)[0])
-        if bad:
-            raise IndexError(
-                f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})"
-            )
+        _check_plan_status(ws, num_tokens)
     return ws
 
 
@@ -268,43 +308,61 @@ def prepare_metadata_and_plan(expert_tensors: Sequence[torch.Tensor], indices: t
                               weights: torch.Tensor, num_tokens: int,
                               validate: Optional[bool] = None):
     """``prepare_grouped_metadata`` followed by ``build_plan`` in one C-ABI call
-    (``fmoe_build_metadata_and_plan``: one kernel launch for up to 256 experts); returns
-    ``(metadata, plan)``, each exactly what the two calls return."""
-    return _metadata_and_plan(expert_tensors, _check_experts(expert_tensors), indices, weights,
-                              num_tokens, validate)
+    (``fmoe_build_metadata_and_plan``: the plan's own launches write the metadata for up to 256
+    experts); returns ``(metadata, plan)``, each exactly what the two calls return."""
+    checked = _check_experts(expert_tensors)
+    idx, w = _routing_args(indices, weights, sum(checked[3]), checked[1])
+    return _metadata_and_plan(expert_tensors, checked, idx, w, num_tokens, validate)
 
 
-def _metadata_and_plan(expert_tensors, checked, indices, weights, num_tokens, validate):
+def _metadata_and_plan(expert_tensors, checked, idx, w, num_tokens, validate):
+    """idx and w already flat and checked (_routing_args)."""
     dtype, dev, hidden, sizes, ptrs = checked
     lib = _abi.lib()
-    E, N = len(expert_tensors), sum(sizes)
-    idx, w = _routing_args(indices, weights, N, dev)
+    E, N = len(sizes), sum(sizes)
     nbytes = lib.fmoe_plan_workspace_bytes(N, num_tokens)
     if nbytes <= 0:
         raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
-    ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
-    chunk_sizes = torch.empty(E, dtype=torch.int32, device=dev)
-    offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
-    max_rows_dev = torch.empty(1, dtype=torch.int32, device=dev)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    arrays = _meta_arrays(E, dev, nbytes)
+    ws = arrays[4]
     with torch.cuda.device(dev), _span("metadata_plan"):
         rc = lib.fmoe_build_metadata_and_plan(
-            (ctypes.c_int64 * E)(*ptrs), (ctypes.c_int64 * E)(*sizes), E, ptr_table.data_ptr(),
-            chunk_sizes.data_ptr(), offsets.data_ptr(), max_rows_dev.data_ptr(), idx.data_ptr(),
-            _INDEX_CODES[idx.dtype], w.data_ptr(), _FLOAT_CODES[w.dtype], num_tokens,
+            _host_table(ptrs), _host_table(sizes), E, arrays[0].data_ptr(), arrays[1].data_ptr(),
+            arrays[2].data_ptr(), arrays[3].data_ptr(), idx.data_ptr(), _INDEX_CODES[idx.dtype],
+            w.data_ptr(), _FLOAT_CODES[w.dtype], num_tokens,
             hidden * expert_tensors[0].element_size(), ws.data_ptr(), _stream_handle(dev),
         )
     _abi.check(rc, "fmoe_build_metadata_and_plan")
-    meta = GroupedMetadata(
-        ptr_table, chunk_sizes, offsets, max(sizes), E,
-        max_rows_device=max_rows_dev, tensors=expert_tensors, sizes=sizes, ptrs=ptrs,
-        hidden=hidden, dtype=dtype, device=dev,
-    )
+    meta = _new_metadata(expert_tensors, checked, arrays)
     if _validate_default(validate):
-        bad = int(plan_status(ws)[0])
-        if bad:
-            raise IndexError(f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})")
+        _check_plan_status(ws, num_tokens)
     return meta, ws
+
+
+def _check_slots(slot_pos, weights, N: int, num_tokens: int, top_k: int, dev):
+    if N != num_tokens * top_k or not (1 <= top_k <= 64):
+        raise ValueError(f"fastmoe_amd: a slot plan needs rows == T*k and k <= 64 "
+                         f"(rows {N}, T {num_tokens}, k {top_k})")
+    if slot_pos.dtype != torch.int32 or slot_pos.numel() != N or slot_pos.device != dev:
+        raise ValueError("fastmoe_amd: slot_pos must be int32 [T*k] on the experts' device")
+    w = weights.reshape(-1).contiguous()
+    if w.dtype not in _FLOAT_CODES or w.numel() != N:
+        raise ValueError("fastmoe_amd: weights must be a float [T*k] tensor")
+    return slot_pos.contiguous(), w
+
+
+def _build_plan_from_slots_raw(ptr_table, offsets_full, E: int, N: int, row_bytes: int,
+                               slot_pos, w, num_tokens: int, top_k: int, dev) -> torch.Tensor:
+    lib = _abi.lib()
+    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev), _span("plan"):
+        rc = lib.fmoe_build_plan_from_slots(
+            slot_pos.data_ptr(), num_tokens, top_k, w.data_ptr(), _FLOAT_CODES[w.dtype],
+            ptr_table.data_ptr(), offsets_full.data_ptr(), E, N, row_bytes, ws.data_ptr(),
+            _stream_handle(dev),
+        )
+    _abi.check(rc, "fmoe_build_plan_from_slots")
+    return ws
 
 
 def build_plan_from_slots(meta: GroupedMetadata, slot_pos: torch.Tensor, weights: torch.Tensor,
@@ -315,27 +373,11 @@ def build_plan_from_slots(meta: GroupedMetadata, slot_pos: torch.Tensor, weights
     ``slot_pos[t * top_k : (t + 1) * top_k]``.  Requires every slot to be a row of the combine
     (``meta.num_rows == num_tokens * top_k``) and ``top_k <= 64``.  Same layout as build_plan.
     """
-    lib = _abi.lib()
     N = meta.num_rows
-    if N != num_tokens * top_k or not (1 <= top_k <= 64):
-        raise ValueError(f"fastmoe_amd: a slot plan needs rows == T*k and k <= 64 "
-                         f"(rows {N}, T {num_tokens}, k {top_k})")
-    if slot_pos.dtype != torch.int32 or slot_pos.numel() != N or slot_pos.device != meta.device:
-        raise ValueError("fastmoe_amd: slot_pos must be int32 [T*k] on the experts' device")
-    w = weights.reshape(-1).contiguous()
-    if w.dtype not in _FLOAT_CODES or w.numel() != N:
-        raise ValueError("fastmoe_amd: weights must be a float [T*k] tensor")
-    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8,
-                     device=meta.device)
-    with torch.cuda.device(meta.device), _span("plan"):
-        rc = lib.fmoe_build_plan_from_slots(
-            slot_pos.contiguous().data_ptr(), num_tokens, top_k, w.data_ptr(),
-            _FLOAT_CODES[w.dtype], meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(),
-            len(meta.sizes), N, meta.hidden * meta.tensors[0].element_size(), ws.data_ptr(),
-            _stream_handle(meta.device),
-        )
-    _abi.check(rc, "fmoe_build_plan_from_slots")
-    return ws
+    sp, w = _check_slots(slot_pos, weights, N, num_tokens, top_k, meta.device)
+    return _build_plan_from_slots_raw(meta.ptr_table, meta.offsets_full, len(meta.sizes), N,
+                                      meta.hidden * meta.tensors[0].element_size(), sp, w,
+                                      num_tokens, top_k, meta.device)
 
 
 def prepare_metadata_and_plan_from_slots(expert_tensors: Sequence[torch.Tensor],
@@ -351,35 +393,19 @@ def prepare_metadata_and_plan_from_slots(expert_tensors: Sequence[torch.Tensor],
 def _metadata_and_plan_from_slots(expert_tensors, checked, slot_pos, weights, num_tokens, top_k):
     dtype, dev, hidden, sizes, ptrs = checked
     lib = _abi.lib()
-    E, N = len(expert_tensors), sum(sizes)
-    if N != num_tokens * top_k or not (1 <= top_k <= 64):
-        raise ValueError(f"fastmoe_amd: a slot plan needs rows == T*k and k <= 64 "
-                         f"(rows {N}, T {num_tokens}, k {top_k})")
-    if slot_pos.dtype != torch.int32 or slot_pos.numel() != N or slot_pos.device != dev:
-        raise ValueError("fastmoe_amd: slot_pos must be int32 [T*k] on the experts' device")
-    w = weights.reshape(-1).contiguous()
-    if w.dtype not in _FLOAT_CODES or w.numel() != N:
-        raise ValueError("fastmoe_amd: weights must be a float [T*k] tensor")
-    ptr_table = torch.empty(E, dtype=torch.int64, device=dev)
-    chunk_sizes = torch.empty(E, dtype=torch.int32, device=dev)
-    offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
-    max_rows_dev = torch.empty(1, dtype=torch.int32, device=dev)
-    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
+    E, N = len(sizes), sum(sizes)
+    sp, w = _check_slots(slot_pos, weights, N, num_tokens, top_k, dev)
+    arrays = _meta_arrays(E, dev, lib.fmoe_plan_workspace_bytes(N, num_tokens))
+    ws = arrays[4]
     with torch.cuda.device(dev), _span("metadata_plan"):
         rc = lib.fmoe_build_metadata_and_plan_from_slots(
-            (ctypes.c_int64 * E)(*ptrs), (ctypes.c_int64 * E)(*sizes), E, ptr_table.data_ptr(),
-            chunk_sizes.data_ptr(), offsets.data_ptr(), max_rows_dev.data_ptr(),
-            slot_pos.contiguous().data_ptr(), num_tokens, top_k, w.data_ptr(),
-            _FLOAT_CODES[w.dtype], hidden * expert_tensors[0].element_size(), ws.data_ptr(),
-            _stream_handle(dev),
+            _host_table(ptrs), _host_table(sizes), E, arrays[0].data_ptr(), arrays[1].data_ptr(),
+            arrays[2].data_ptr(), arrays[3].data_ptr(), sp.data_ptr(), num_tokens, top_k,
+            w.data_ptr(), _FLOAT_CODES[w.dtype], hidden * expert_tensors[0].element_size(),
+            ws.data_ptr(), _stream_handle(dev),
         )
     _abi.check(rc, "fmoe_build_metadata_and_plan_from_slots")
-    meta = GroupedMetadata(
-        ptr_table, chunk_sizes, offsets, max(sizes), E,
-        max_rows_device=max_rows_dev, tensors=expert_tensors, sizes=sizes, ptrs=ptrs,
-        hidden=hidden, dtype=dtype, device=dev,
-    )
-    return meta, ws
+    return _new_metadata(expert_tensors, checked, arrays), ws
 
 
 def invert_scatter_index(indices: torch.Tensor, num_tokens: int):
@@ -438,7 +464,14 @@ def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
                 accumulate: bool) -> None:
     lib = _abi.lib()
     T, D = out.shape
-    with torch.cuda.device(meta.device), _span("fwd_det" if mode == _abi.MODE_DET else "fwd_atomic"):
+    out_code = _FLOAT_CODES[out.dtype]
+    ws, ws_bytes = None, 0
+    if mode == _abi.MODE_ATOMIC and out_code != _abi.F32:
+        # the fp32 accumulator of a 16-bit output (fmoe_combine_fwd_workspace_bytes)
+        ws_bytes = lib.fmoe_combine_fwd_workspace_bytes(mode, T, D, out_code)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=meta.device)
+    name = "fwd_det" if mode == _abi.MODE_DET else "fwd_atomic"
+    with torch.cuda.device(meta.device), _span(name):
         rc = lib.fmoe_combine_fwd(
             mode,
             plan.data_ptr() if plan is not None else None,
@@ -447,9 +480,9 @@ def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
             w.data_ptr() if w is not None else None,
             _FLOAT_CODES[w.dtype] if w is not None else _abi.F32,
             meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(), len(meta.sizes),
-            meta.num_rows, T, D, _FLOAT_CODES[meta.dtype], out.data_ptr(),
-            _FLOAT_CODES[out.dtype], out.stride(0) if T > 1 else D, 1 if accumulate else 0,
-            _stream_handle(meta.device),
+            meta.num_rows, T, D, _FLOAT_CODES[meta.dtype], out.data_ptr(), out_code,
+            out.stride(0) if T > 1 else D, 1 if accumulate else 0,
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream_handle(meta.device),
         )
     _abi.check(rc, "fmoe_combine_fwd")
 
@@ -460,17 +493,16 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
     code = _mode_code(mode)
     T = out.shape[0]
     plan = None
-    if metadata is None or not isinstance(metadata, GroupedMetadata) or not metadata.matches(
-        expert_tensors
-    ):
+    if isinstance(metadata, GroupedMetadata) and metadata.matches(expert_tensors):
+        idx, w = _routing_args(indices, weights, metadata.num_rows, metadata.device)
+    else:
         checked = _check_experts(expert_tensors)
+        idx, w = _routing_args(indices, weights, sum(checked[3]), checked[1])
         if code == _abi.MODE_DET and sum(checked[3]) > 0:
-            metadata, plan = _metadata_and_plan(expert_tensors, checked, indices, weights, T,
-                                                validate)
+            metadata, plan = _metadata_and_plan(expert_tensors, checked, idx, w, T, validate)
         else:
             metadata = _metadata(expert_tensors, checked)
     _check_out(out, None, metadata.hidden, metadata.device)
-    idx, w = _routing_args(indices, weights, metadata.num_rows, metadata.device)
     if metadata.max_rows == 0:  # ops.py:286: nothing to add
         return out
     if code == _abi.MODE_DET:
@@ -485,78 +517,106 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
 
 
 def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices, weights,
-                     out_shape, expert_tensors, slots=None):
+                     out_shape, expert_tensors, w_grad: bool, slots=None):
+    """Autograd forward.  ``w_grad``: the gate gradient will be asked for (the expert tensors are
+    then saved for the backward, which reads them for it; otherwise only the index and gates are,
+    as in the reference, ops.py:326)."""
     checked = _check_experts(expert_tensors)
-    hidden, sizes = checked[2], checked[3]
+    dtype, dev, hidden, sizes, ptrs = checked
     shape = tuple(int(s) for s in out_shape)
     if len(shape) != 2 or shape[1] != hidden:
         raise ValueError(f"fastmoe_amd: out_shape {shape} must be [T, {hidden}]")
-    T, D = shape
+    T = shape[0]
     code = _mode_code(mode)
     rows = sum(sizes)
-    # metadata and plan in one call (one launch for up to 256 experts)
+    idx, w = _routing_args(indices, weights, rows, dev)
+    use_slots = slots is not None and rows == T * slots[1] and slots[1] <= 64
+    plan = None
     if rows == 0:
-        meta, plan = _metadata(expert_tensors, checked), None
-    elif slots is not None and rows == T * slots[1] and slots[1] <= 64:
-        _, w0 = _routing_args(indices, weights, rows, checked[1])
-        meta, plan = _metadata_and_plan_from_slots(expert_tensors, checked, slots[0], w0, T,
-                                                   slots[1])
-    else:
-        meta, plan = _metadata_and_plan(expert_tensors, checked, indices, weights, T, validate)
-    idx, w = _routing_args(indices, weights, meta.num_rows, meta.device)
-    if plan is None:
-        out = torch.zeros(shape, dtype=meta.dtype, device=meta.device)
+        meta = _metadata(expert_tensors, checked)
+        out = torch.zeros(shape, dtype=dtype, device=dev)
     elif code == _abi.MODE_DET:
-        # Every output row is written exactly once (tokens without rows get zeros): no zero-fill.
-        out = torch.empty(shape, dtype=meta.dtype, device=meta.device)
-        _launch_fwd(meta, _abi.MODE_DET, plan, None, None, out, accumulate=False)
+        # metadata and plan in one call; every output row is written exactly once (tokens
+        # without rows get zeros), so out needs no zero-fill
+        if use_slots:
+            meta, plan = _metadata_and_plan_from_slots(expert_tensors, checked, slots[0], w, T,
+                                                       slots[1])
+        else:
+            meta, plan = _metadata_and_plan(expert_tensors, checked, idx, w, T, validate)
+        out = torch.empty(shape, dtype=dtype, device=dev)
+        _launch_fwd(meta, code, plan, None, None, out, accumulate=False)
     else:
-        out = torch.zeros(shape, dtype=meta.dtype, device=meta.device)
-        _launch_fwd(meta, _abi.MODE_ATOMIC, None, idx, w, out, accumulate=True)
-    ctx.save_for_backward(idx, w, *expert_tensors)
+        # the atomic forward reads no plan: the backward builds it if a gradient is asked for
+        meta = _metadata(expert_tensors, checked)
+        if _validate_default(validate):
+            _check_plan_status(_build_plan_raw(meta.ptr_table, meta.offsets_full, len(sizes), rows,
+                                               hidden * expert_tensors[0].element_size(), idx, w,
+                                               T, dev), T)
+        out = torch.empty(shape, dtype=dtype, device=dev)  # overwritten: the library clears it
+        _launch_fwd(meta, code, None, idx, w, out, accumulate=False)
+    if w_grad:
+        ctx.save_for_backward(idx, w, *expert_tensors)
+    else:
+        ctx.save_for_backward(idx, w)
     ctx.plan = plan
-    ctx.sizes = meta.sizes
+    # what a deferred plan needs (device arrays only: no reference to the expert tensors)
+    ctx.meta_arrays = (meta.ptr_table, meta.offsets_full) if plan is None else None
+    ctx.slots = (slots[0], slots[1]) if (use_slots and plan is None) else None
+    ctx.sizes = sizes
+    ctx.hidden = hidden
+    ctx.row_bytes = hidden * expert_tensors[0].element_size()
     ctx.num_tokens = T
-    ctx.x_dtype = meta.dtype
+    ctx.x_dtype = dtype
+    ctx.w_shape = weights.shape
     return out
 
 
 def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
     saved = ctx.saved_tensors
     idx, w = saved[0], saved[1]
-    experts = saved[2:]
-    need_x = any(needs_x)
     sizes = ctx.sizes
-    if ctx.plan is None or not (needs_w or need_x):
-        gw = torch.zeros_like(w) if needs_w else None
-        gx = [torch.zeros_like(t) if n else None for t, n in zip(experts, needs_x)]
+    need_x = any(needs_x)
+    N, T, D = sum(sizes), ctx.num_tokens, ctx.hidden
+    dev = idx.device
+    if not (needs_w or need_x):
+        return None, [None] * len(sizes)
+    if N == 0:
+        gw = torch.zeros(ctx.w_shape, dtype=w.dtype, device=dev) if needs_w else None
+        gx = [torch.zeros((n, D), dtype=ctx.x_dtype, device=dev) if need else None
+              for n, need in zip(sizes, needs_x)]
         return gw, gx
-    N = sum(sizes)
-    T = ctx.num_tokens
-    D = experts[0].shape[1]
+    plan = ctx.plan
+    if plan is None:  # atomic forward: the plan now
+        ptr_table, offsets_full = ctx.meta_arrays
+        if ctx.slots is not None:
+            plan = _build_plan_from_slots_raw(ptr_table, offsets_full, len(sizes), N,
+                                              ctx.row_bytes, ctx.slots[0], w, T, ctx.slots[1],
+                                              dev)
+        else:
+            plan = _build_plan_raw(ptr_table, offsets_full, len(sizes), N, ctx.row_bytes, idx, w,
+                                   T, dev)
     go = grad_output
     if go.dtype != ctx.x_dtype:
         go = go.to(ctx.x_dtype)
     if D > 1 and go.stride(1) != 1:
         go = go.contiguous()
-    dev = go.device
     gx = torch.empty((N, D), dtype=ctx.x_dtype, device=dev) if need_x else None
     gw = torch.empty(N, dtype=w.dtype, device=dev) if needs_w else None
     lib = _abi.lib()
+    stream = _stream_handle(dev)
 
     def launch(name, gx_ptr, gw_ptr):
         with torch.cuda.device(dev), _span(name):
             rc = lib.fmoe_combine_bwd(
-                ctx.plan.data_ptr(), N, T, D, _FLOAT_CODES[ctx.x_dtype], go.data_ptr(),
+                plan.data_ptr(), N, T, D, _FLOAT_CODES[ctx.x_dtype], go.data_ptr(),
                 _FLOAT_CODES[go.dtype], go.stride(0) if T > 1 else D, gx_ptr, gw_ptr,
-                _FLOAT_CODES[w.dtype], _stream_handle(dev),
+                _FLOAT_CODES[w.dtype], stream,
             )
         _abi.check(rc, "fmoe_combine_bwd")
 
     gx_ptr = gx.data_ptr() if gx is not None else None
     gw_ptr = gw.data_ptr() if gw is not None else None
-    fused = _abi.option("bwd_fused") != 0
-    if gx_ptr and gw_ptr and not fused:
+    if gx_ptr and gw_ptr and not _abi.option("bwd_fused"):
         # The grad_X (write) and grad_w (read) passes, one call each -- the same two launches
         # fmoe_combine_bwd makes when given both outputs, issued separately so each is timed.
         launch("bwd_gx", gx_ptr, None)
@@ -568,7 +628,12 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
         grads_x = [p if n else None for p, n in zip(parts, needs_x)]
     else:
         grads_x = [None] * len(sizes)
-    return gw, grads_x
+    return (gw.view(ctx.w_shape) if gw is not None else None), grads_x
+
+
+def _apply(fn, *args):
+    """``fn.apply(*args)`` (one place for every autograd entry of the combine)."""
+    return fn.apply(*args)
 
 
 class GroupedWeightedScatterAdd(torch.autograd.Function):
@@ -577,13 +642,15 @@ class GroupedWeightedScatterAdd(torch.autograd.Function):
     forward : out = zeros(out_shape, dtype=experts[0].dtype) + combine   (ops.py:317-331)
     backward: grad_X_e = split(grad_out[indices] * weights[:, None])     (ops.py:333-353)
               plus grad_weights[g] = <grad_out[indices[g]], X[g]>  when weights require grad.
-    Both directions share one plan (token-major inverse of the indices) built in the forward.
+    Both directions share one plan (token-major inverse of the indices), built in the forward
+    (deterministic mode) or in the backward (atomic modes, whose forward does not read it).
     The forward kernel is chosen by ``FASTMOE_COMBINE_MODE`` ("det" by default).
     """
 
     @staticmethod
     def forward(ctx, indices, weights, out_shape, *expert_tensors):
-        return _combine_forward(ctx, None, None, indices, weights, out_shape, expert_tensors)
+        return _combine_forward(ctx, None, None, indices, weights, out_shape, expert_tensors,
+                                ctx.needs_input_grad[1])
 
     @staticmethod
     def backward(ctx, grad_output):
@@ -598,7 +665,8 @@ class _GroupedCombineWithOptions(torch.autograd.Function):
     @staticmethod
     def forward(ctx, options, indices, weights, out_shape, *expert_tensors):
         mode, validate = options
-        return _combine_forward(ctx, mode, validate, indices, weights, out_shape, expert_tensors)
+        return _combine_forward(ctx, mode, validate, indices, weights, out_shape, expert_tensors,
+                                ctx.needs_input_grad[2])
 
     @staticmethod
     def backward(ctx, grad_output):
@@ -614,7 +682,7 @@ class _GroupedCombinePermuted(torch.autograd.Function):
     @staticmethod
     def forward(ctx, slots, indices, weights, out_shape, *expert_tensors):
         return _combine_forward(ctx, None, None, indices, weights, out_shape, expert_tensors,
-                                slots=slots)
+                                ctx.needs_input_grad[2], slots=slots)
 
     @staticmethod
     def backward(ctx, grad_output):
@@ -636,9 +704,9 @@ def grouped_weighted_scatter_add(expert_tensors, indices, weights, out_shape, ou
         return _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=metadata,
                                       mode=mode, validate=validate)
     if mode is None and validate is None:
-        return GroupedWeightedScatterAdd.apply(indices, weights, out_shape, *expert_tensors)
-    return _GroupedCombineWithOptions.apply((mode, validate), indices, weights, out_shape,
-                                            *expert_tensors)
+        return _apply(GroupedWeightedScatterAdd, indices, weights, out_shape, *expert_tensors)
+    return _apply(_GroupedCombineWithOptions, (mode, validate), indices, weights, out_shape,
+                  *expert_tensors)
 
 
 def weighted_scatter_add(src, indices, weights, out_shape, out=None, *, mode=None, validate=None):

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 1
+#define FMOE_ABI_VERSION 2
 
 /* Element types. */
 enum fmoe_dtype {
@@ -65,9 +65,15 @@ enum fmoe_mode {
   /* Token-major: every output row is reduced in ascending packed-row order in fp32 registers and
      written once.  Bit-identical run to run; bit-identical to the CPU index_add_ path in fp32. */
   FMOE_MODE_DET = 0,
-  /* Packed-row-major like the reference kernel: hardware float atomics into `out`
-     (global_atomic_add_f32 / global_atomic_pk_add_bf16 / global_atomic_pk_add_f16). */
-  FMOE_MODE_ATOMIC = 1
+  /* Packed-row-major like the reference kernel: hardware fp32 atomics (global_atomic_add_f32).
+     A bf16/f16 `out` is accumulated in a caller-owned fp32 workspace and rounded once at the end,
+     so it is within 1 ulp of the fp32 sum rounded once; the order of the fp32 additions (and so
+     the last bits) varies run to run. */
+  FMOE_MODE_ATOMIC = 1,
+  /* As FMOE_MODE_ATOMIC, but a bf16/f16 `out` takes gfx950's packed 16-bit atomics
+     (global_atomic_pk_add_bf16 / _f16) directly: no workspace, half the atomic requests, and a
+     rounding to 16 bits at every add (the reference Triton kernel's behaviour with a bf16 out). */
+  FMOE_MODE_ATOMIC_PACKED = 2
 };
 
 enum fmoe_status {
@@ -209,20 +215,28 @@ FMOE_API int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, int
  * Forward combine (replaces _launch_grouped_kernel + _grouped_weighted_scatter_add_kernel,
  * src/fastmoe/kernels/ops.py:277-310 and :57-194).
  *
- * mode == FMOE_MODE_DET    : reads the plan (d_plan from fmoe_build_plan on the same inputs);
- *                            d_indices/d_weights/d_ptr_table/d_offsets may be NULL.
- * mode == FMOE_MODE_ATOMIC : reads d_indices/d_weights/d_ptr_table/d_offsets; d_plan may be NULL.
+ * mode == FMOE_MODE_DET     : reads the plan (d_plan from fmoe_build_plan on the same inputs);
+ *                             d_indices/d_weights/d_ptr_table/d_offsets may be NULL.
+ * mode == FMOE_MODE_ATOMIC[_PACKED] : reads d_indices/d_weights/d_ptr_table/d_offsets; d_plan may
+ *                             be NULL.
  * out        : [T, D] with row stride out_row_stride (elements) and unit column stride.
  * accumulate : 1 = add into the existing contents of out (the reference's in-place contract,
- *              ops.py:389-390); 0 = overwrite (rows of tokens without routed rows become 0).
- *              FMOE_MODE_ATOMIC always accumulates: the caller zero-fills out beforehand.
+ *              ops.py:389-390); 0 = overwrite (rows of tokens without routed rows become 0; the
+ *              atomic modes clear out first with a fill kernel).
  * x_dtype    : dtype of every expert buffer; out_dtype: dtype of out.
+ * d_workspace, workspace_bytes : device memory the caller owns, at least
+ *              fmoe_combine_fwd_workspace_bytes(mode, T, D, out_dtype) bytes, 16-byte aligned
+ *              (the fp32 accumulator of FMOE_MODE_ATOMIC with a 16-bit out, T * D * 4 bytes);
+ *              NULL / 0 when that is 0.
  */
+FMOE_API int64_t fmoe_combine_fwd_workspace_bytes(int mode, int64_t num_tokens, int64_t hidden,
+                                         int out_dtype);
 FMOE_API int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indices, int idx_dtype,
                      const void* d_weights, int w_dtype, const int64_t* d_ptr_table,
                      const int64_t* d_offsets, int64_t num_experts, int64_t num_rows,
                      int64_t num_tokens, int64_t hidden, int x_dtype, void* d_out, int out_dtype,
-                     int64_t out_row_stride, int accumulate, void* stream);
+                     int64_t out_row_stride, int accumulate, void* d_workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /*
  * Allocation-free deterministic forward.  No counterpart in the reference: it is for callers that

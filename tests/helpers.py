@@ -64,6 +64,40 @@ def reorder_tol(n_terms: int, scale):
     return 2.0 * max(n_terms - 1, 1) * 2.0 ** -24 * (1.0 + 2.0 ** -20) * scale + 1e-30
 
 
+# bf16 / f16: unit roundoff, significand bits (with the implicit one), smallest spacing
+_U16 = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+_P16 = {torch.bfloat16: 8, torch.float16: 11}
+_MIN_ULP16 = {torch.bfloat16: 2.0 ** -133, torch.float16: 2.0 ** -24}
+
+
+def ulp16(x, dtype):
+    """Spacing of the bf16 / f16 grid at |x| (at a power of two: the spacing above it)."""
+    a = np.abs(np.asarray(x, dtype=np.float64))
+    _, e = np.frexp(a)  # a = m * 2^e, 0.5 <= m < 1
+    ulp = np.ldexp(1.0, e - _P16[dtype])
+    return np.where(a == 0, _MIN_ULP16[dtype], np.maximum(ulp, _MIN_ULP16[dtype]))
+
+
+def within_one_ulp16(got, want, dtype, n_terms: int, scale):
+    """The "<= 1 ulp after fp32 accumulation" bar for a 16-bit output: ``got`` is some fp32 sum
+    of the terms rounded once to ``dtype``, ``want`` the oracle's (the sequential fp32 sum rounded
+    once).  The two fp32 sums differ by at most reorder_tol(n_terms, scale); each rounding moves a
+    value by at most half a spacing, so the results differ by at most one spacing (taken at the
+    larger magnitude) plus that gap.  Elementwise boolean."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    tol = ulp16(np.maximum(np.abs(got), np.abs(want)), dtype) + reorder_tol(n_terms, scale)
+    return np.abs(got - want) <= tol
+
+
+def packed_tol(n_terms: int, scale, dtype):
+    """Error bound of packed 16-bit atomics against the oracle's 16-bit result: each of the n
+    terms is rounded to 16 bits and each of the n adds rounds the running sum (at most u times
+    sum|terms| each, u the unit roundoff), and the oracle's own result is one rounding of its fp32
+    sum: (n + 2) u sum|terms|, first order; the factor (1 + 2^-6) covers the higher-order terms."""
+    return (n_terms + 2) * _U16[dtype] * (1.0 + 2.0 ** -6) * scale + _MIN_ULP16[dtype]
+
+
 def abs_sum(experts, idx, w, T):
     """sum_g |w[g] * X[g, d]| per output element (scale of reordering error of a fp32 sum)."""
     D = experts[0].shape[1]

@@ -81,20 +81,29 @@ def test_combine_entry_points_reject_bad_arguments():
     dev = 0x10000
     # bad mode
     rc = lib.fmoe_combine_fwd(7, dev, None, _abi.I64, None, _abi.F32, None, None, 1, 4, 4, 8,
-                              _abi.F32, dev, _abi.F32, 8, 0, None)
+                              _abi.F32, dev, _abi.F32, 8, 0, None, 0, None)
     assert rc == _abi.EINVAL and b"mode" in lib.fmoe_last_error()
     # det without plan
     rc = lib.fmoe_combine_fwd(_abi.MODE_DET, None, None, _abi.I64, None, _abi.F32, None, None, 1,
-                              4, 4, 8, _abi.F32, dev, _abi.F32, 8, 0, None)
+                              4, 4, 8, _abi.F32, dev, _abi.F32, 8, 0, None, 0, None)
     assert rc == _abi.EINVAL
     # out stride smaller than D
     rc = lib.fmoe_combine_fwd(_abi.MODE_DET, dev * 256, None, _abi.I64, None, _abi.F32, None, None,
-                              1, 4, 4, 8, _abi.F32, dev, _abi.F32, 4, 0, None)
+                              1, 4, 4, 8, _abi.F32, dev, _abi.F32, 4, 0, None, 0, None)
     assert rc == _abi.EINVAL
     # too many rows for the 32-bit counters
     rc = lib.fmoe_combine_fwd(_abi.MODE_DET, dev * 256, None, _abi.I64, None, _abi.F32, None, None,
-                              1, 1 << 31, 4, 8, _abi.F32, dev, _abi.F32, 8, 0, None)
+                              1, 1 << 31, 4, 8, _abi.F32, dev, _abi.F32, 8, 0, None, 0, None)
     assert rc == _abi.ERANGE
+    # atomic mode with a 16-bit output: the fp32 accumulator workspace is required
+    need = lib.fmoe_combine_fwd_workspace_bytes(_abi.MODE_ATOMIC, 4, 8, _abi.BF16)
+    assert need == 256 and lib.fmoe_combine_fwd_workspace_bytes(_abi.MODE_DET, 4, 8, _abi.BF16) == 0
+    assert lib.fmoe_combine_fwd_workspace_bytes(_abi.MODE_ATOMIC, 4, 8, _abi.F32) == 0
+    assert lib.fmoe_combine_fwd_workspace_bytes(_abi.MODE_ATOMIC_PACKED, 4, 8, _abi.BF16) == 0
+    for ws, nbytes in [(None, 0), (dev * 256, need - 4), (dev * 256 + 8, need)]:
+        rc = lib.fmoe_combine_fwd(_abi.MODE_ATOMIC, None, dev, _abi.I64, dev, _abi.F32, dev, dev, 1,
+                                  4, 4, 8, _abi.BF16, dev, _abi.BF16, 8, 0, ws, nbytes, None)
+        assert rc == _abi.EINVAL and b"workspace" in lib.fmoe_last_error()
     # backward: grad_out dtype must equal the expert dtype
     rc = lib.fmoe_combine_bwd(dev * 256, 4, 4, 8, _abi.BF16, dev, _abi.F32, 8, dev, None,
                               _abi.F32, None)

@@ -44,7 +44,8 @@ def test_cpu_tensors_raise_instead_of_falling_back():
 def test_mode_parsing(monkeypatch):
     assert ops._mode_code(None) == ops._abi.MODE_DET
     assert ops._mode_code("atomic") == ops._abi.MODE_ATOMIC
-    monkeypatch.setenv("FASTMOE_COMBINE_MODE", "atomic")
+    assert ops._mode_code("atomic_packed") == ops._abi.MODE_ATOMIC_PACKED
+    monkeypatch.setattr(ops, "_DEFAULT_MODE", "atomic")  # FASTMOE_COMBINE_MODE, read at import
     assert ops._mode_code(None) == ops._abi.MODE_ATOMIC
     with pytest.raises(ValueError):
         ops._mode_code("fast")

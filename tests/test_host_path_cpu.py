@@ -75,12 +75,17 @@ class FakeLib:
         self.calls.append(("metadata_plan_slots", E, list(host_rows), T, k, row_bytes, wdt))
         return 0
 
+    def fmoe_combine_fwd_workspace_bytes(self, mode, T, D, odt):
+        return self.real.fmoe_combine_fwd_workspace_bytes(mode, T, D, odt)
+
     def fmoe_combine_fwd(self, mode, plan, idx, idt, w, wdt, ptr_table, offsets, E, N, T, D, xdt,
-                         out, odt, ostride, acc, stream):
+                         out, odt, ostride, acc, ws, ws_bytes, stream):
         if mode == _abi.MODE_DET:
             assert isinstance(plan, int)
         else:
             assert isinstance(idx, int) and isinstance(w, int)
+        need = self.real.fmoe_combine_fwd_workspace_bytes(mode, T, D, odt)
+        assert ws_bytes >= need and (need == 0 or isinstance(ws, int))
         self.calls.append(("fwd", mode, N, T, D, xdt, odt, ostride, acc))
         return 0
 
@@ -147,7 +152,7 @@ def test_backward_skips_unneeded_outputs(fake):
     assert fake.calls[-1][6:8] == (True, False)
 
 
-def test_atomic_mode_zero_fills_and_skips_plan_in_place(fake):
+def test_atomic_mode_overwrites_and_defers_the_plan(fake):
     xs = _experts(torch.float32)
     out = torch.full((4, 16), 3.0)
     meta = fastmoe_amd.prepare_grouped_metadata(xs, "cuda")
@@ -162,10 +167,33 @@ def test_atomic_mode_zero_fills_and_skips_plan_in_place(fake):
     assert [c[0] for c in fake.calls] == ["fwd"]
     assert fake.calls[0][1] == _abi.MODE_ATOMIC and fake.calls[0][-1] == 1
     fake.calls.clear()
+    # autograd path without gradients: no plan at all; the forward overwrites out (accumulate=0,
+    # the library clears it), so the API allocates it without a zero-fill
     out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
                                                    torch.rand(8), (4, 16), mode="atomic")
-    assert torch.all(out == 0)
-    assert [c[0] for c in fake.calls] == ["metadata_plan", "fwd"]
+    assert [c[0] for c in fake.calls] == ["metadata", "fwd"]
+    assert fake.calls[1][1] == _abi.MODE_ATOMIC and fake.calls[1][-1] == 0
+    # with gradients: the backward builds the plan it reads
+    fake.calls.clear()
+    xg = [x.requires_grad_(True) for x in _experts(torch.float32)]
+    wg = torch.rand(8, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xg, torch.zeros(8, dtype=torch.long), wg,
+                                                   (4, 16), mode="atomic")
+    assert [c[0] for c in fake.calls] == ["metadata", "fwd"]
+    torch.autograd.grad(out, [wg, *xg], torch.ones(4, 16))
+    assert [c[0] for c in fake.calls] == ["metadata", "fwd", "plan", "bwd", "bwd"]
+
+
+def test_gate_gradient_keeps_the_weights_shape_and_experts_saved_only_for_it(fake):
+    xs = [x.requires_grad_(True) for x in _experts(torch.float32)]
+    w = torch.rand(4, 2, requires_grad=True)  # [T, k]-shaped gates
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long), w, (2, 16))
+    assert len(out.grad_fn.saved_tensors) == 2 + len(xs)
+    (gw,) = torch.autograd.grad(out, [w], torch.ones(2, 16))
+    assert gw.shape == w.shape
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
+                                                   w.detach(), (2, 16))
+    assert len(out.grad_fn.saved_tensors) == 2  # index and gates only, as the reference saves
 
 
 def test_stale_metadata_is_rebuilt(fake):

@@ -292,3 +292,64 @@ def test_reorder_tolerance_covers_two_summation_orders(n):
     assert np.all(gap <= reorder_tol(n, scale))
     if n == 3:
         assert np.any(gap > (n - 1) * 2.0 ** -24 * scale)
+
+
+def _round16(a: np.ndarray, dtype) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dtype).float().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [2, 3, 8])
+def test_one_ulp_bar_covers_reordered_fp32_sums_and_rejects_two(dtype, n):
+    """The bar of the atomic mode with a 16-bit output (fp32 accumulation, one rounding): two fp32
+    sums of the same terms in different orders, each rounded once, pass within_one_ulp16; the same
+    result moved by two spacings fails it."""
+    from tests.helpers import ulp16, within_one_ulp16
+
+    rng = np.random.default_rng(10 * n + (dtype == torch.float16))
+    M = 100_000
+    x = rng.standard_normal((M, n)).astype(np.float32)
+    xp = np.take_along_axis(x, rng.permuted(np.tile(np.arange(n), (M, 1)), axis=1), 1)
+    s1 = np.zeros(M, np.float32)
+    s2 = np.zeros(M, np.float32)
+    for i in range(n):
+        s1 = s1 + x[:, i]
+        s2 = s2 + xp[:, i]
+    scale = np.abs(x.astype(np.float64)).sum(1)
+    r1, r2 = _round16(s1, dtype), _round16(s2, dtype)
+    assert np.all(within_one_ulp16(r2, r1, dtype, n, scale))
+    if n > 2:  # (two terms add commutatively: one result)
+        assert np.any(r1 != r2)  # the orders do round differently somewhere
+    moved = r2 + 2 * ulp16(r2, dtype)
+    assert np.mean(within_one_ulp16(moved, r1, dtype, n, scale)) < 0.01
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [2, 8])
+def test_packed_bound_covers_rounding_at_every_add_and_catches_a_dropped_term(dtype, n):
+    """packed_tol against a model of packed 16-bit atomics (every term rounded to 16 bits, every
+    add rounded to 16 bits, round to nearest even, in any order): the model stays within the bound
+    of the oracle's result (the sequential fp32 sum rounded once); dropping one term exceeds it
+    on most outputs."""
+    from tests.helpers import packed_tol
+
+    rng = np.random.default_rng(20 * n + (dtype == torch.float16))
+    M = 50_000
+    x = rng.standard_normal((M, n)).astype(np.float32)
+    xp = np.take_along_axis(x, rng.permuted(np.tile(np.arange(n), (M, 1)), axis=1), 1)
+    oracle = np.zeros(M, np.float32)
+    for i in range(n):
+        oracle = oracle + x[:, i]
+    oracle16 = _round16(oracle, dtype)
+    scale = np.abs(x.astype(np.float64)).sum(1)
+
+    def packed(cols):
+        acc = np.zeros(M, np.float32)
+        for i in cols:
+            acc = _round16(acc + _round16(xp[:, i], dtype), dtype)
+        return acc
+
+    err = np.abs(packed(range(n)).astype(np.float64) - oracle16)
+    assert np.all(err <= packed_tol(n, scale, dtype))
+    dropped = np.abs(packed(range(1, n)).astype(np.float64) - oracle16)
+    assert np.mean(dropped > packed_tol(n, scale, dtype)) > 0.5

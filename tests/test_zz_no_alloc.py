@@ -77,7 +77,7 @@ def _with_workspace(c, out, accumulate):
     _abi.check(rc, "fmoe_build_metadata_and_plan")
     rc = lib.fmoe_combine_fwd(_abi.MODE_DET, ws.data_ptr(), None, _abi.I64, None, _abi.F32,
                               ptr_table.data_ptr(), offs.data_ptr(), E, N, T, D, CODE[xdt],
-                              out.data_ptr(), CODE[out.dtype], out.stride(0), accumulate,
+                              out.data_ptr(), CODE[out.dtype], out.stride(0), accumulate, None, 0,
                               _stream())
     _abi.check(rc, "fmoe_combine_fwd")
     return ws  # kept alive until the caller synchronises
