@@ -256,6 +256,186 @@ def _verify_moe(wl, x, ids, gates, out):
             "against": "fp32 torch index_add_ of the stably permuted products (tiny_model.py:396-403)"}
 
 
+class _StepCtx:
+    """Stand-in for the autograd context of GroupedWeightedScatterAdd: with it the forward and
+    backward functions of the autograd path (fastmoe_amd.ops._combine_forward / _combine_backward)
+    issue exactly the launches an autograd step makes -- metadata + plan, forward, grad_X and
+    grad_w passes -- without the autograd engine, all from the calling thread."""
+
+    def save_for_backward(self, *tensors):
+        self.saved_tensors = tensors
+
+
+def _timed(fn, n):
+    """(device ms per call between two events on the current stream, host wall ms per call)."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(n):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / n, (time.perf_counter() - t0) * 1e3 / n
+
+
+def _event_kernels(step, steps):
+    """Per-kernel durations: HIP events around every C-ABI launch, on the launch stream.  A sleep
+    kernel first gives the GPU a backlog so that the host has enqueued each event-kernel-event
+    triple before the GPU reaches it (the events then bracket the kernel, not host gaps)."""
+    import torch
+
+    from fastmoe_amd import ops
+
+    timer = EventTimer()
+    ops._TIMER = timer
+    timer.enabled = True
+    try:
+        torch.cuda._sleep(int(steps * 3e-3 * 2.4e9))
+        backlog = True
+    except Exception:
+        backlog = False
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    timer.enabled = False
+    ops._TIMER = None
+    return timer.summary(), backlog
+
+
+def _graph_ms(capture_step, steps, warmup):
+    """Replay time of one step captured as a HIP graph: (ms per replay, wall ms, error or None)."""
+    import torch
+
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                capture_step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            capture_step()
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+    except Exception as exc:  # capture unsupported: the caller reports eager numbers only
+        return None, None, f"{type(exc).__name__}: {exc}"
+    ms, wall_ms = _timed(graph.replay, steps)
+    del graph
+    return ms, wall_ms, None
+
+
+def _combine_inputs(wl, dev, backward, inplace=False):
+    import torch
+
+    from fastmoe_amd.workloads import make_experts, make_routing
+
+    idx, w, counts = make_routing(wl)
+    idx, w = idx.to(dev), w.to(dev)
+    xs = make_experts(counts, wl.D, wl.dtype, dev, wl.seed)
+    if backward:
+        xs = [x.requires_grad_(True) for x in xs]
+        w.requires_grad_(True)
+    gen_dev = torch.Generator(device=dev)
+    grad_out = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
+                           generator=gen_dev.manual_seed(1)).to(wl.dtype)
+    return idx, w, xs, grad_out
+
+
+def _combine_steps(wl, xs, idx, w, grad_out, mode, backward, inplace, dev):
+    """(public autograd / in-place step, graph-capturable step with the same launches)."""
+    import torch
+
+    import fastmoe_amd
+    from fastmoe_amd import ops
+
+    inputs = [w, *xs]
+    if inplace:
+        out_static = torch.zeros((wl.T, wl.D), device=dev)
+        meta = fastmoe_amd.prepare_grouped_metadata(xs, dev)
+
+        def step():
+            out_static.zero_()
+            return fastmoe_amd.grouped_weighted_scatter_add(
+                xs, idx, w, (wl.T, wl.D), out=out_static, metadata=meta, mode=mode)
+        return step, step
+
+    def step():
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (wl.T, wl.D), mode=mode)
+        if backward:
+            torch.autograd.grad(out, inputs, grad_out)
+        return out
+
+    def direct_step():
+        with torch.no_grad():
+            ctx = _StepCtx()
+            out = ops._combine_forward(ctx, mode, None, idx, w, (wl.T, wl.D), xs, backward)
+            if backward:
+                ops._combine_backward(ctx, grad_out, True, [True] * len(xs))
+        return out
+    return step, direct_step
+
+
+def _summarize_kernels(kernels, kbytes):
+    """Attach algorithmic bytes, GB/s and fraction of peak to the event-timed kernels; return the
+    dominant (longest) one's name."""
+    for name, k in kernels.items():
+        if name in kbytes:
+            k["algorithmic_bytes"] = kbytes[name]
+            k["GBs"] = kbytes[name] / (k["avg_us"] * 1e-6) / 1e9
+            k["frac"] = k["GBs"] / HBM_PEAK_GBS
+    return max((n for n in kernels if n in kbytes), key=lambda n: kernels[n]["avg_us"])
+
+
+def _config_line(name, mode, steps, warmup, dev):
+    """One BASELINE configuration measured in this run: graph-replayed step, % of peak, the
+    metadata + plan span and the dominant kernel (HIP events)."""
+    import torch
+
+    from fastmoe_amd.workloads import WORKLOADS, algorithmic_bytes, kernel_bytes
+
+    wl = WORKLOADS[name]
+    backward = wl.backward
+    idx, w, xs, grad_out = _combine_inputs(wl, dev, backward)
+    xb = torch.empty(0, dtype=wl.dtype).element_size()
+    fwd_b, bwd_b = algorithmic_bytes(wl.T, wl.D, wl.N, xb, xb)
+    step_bytes = fwd_b + (bwd_b if backward else 0)
+    step, direct_step = _combine_steps(wl, xs, idx, w, grad_out, mode, backward, False, dev)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    kernels, _ = _event_kernels(step, steps)
+    dom = _summarize_kernels(kernels, kernel_bytes(wl.T, wl.D, wl.N, xb, xb))
+    ms, _, err = _graph_ms(direct_step, steps, warmup)
+    if ms is None:
+        ms, _ = _timed(step, steps)
+    plan_us = sum(v["avg_us"] for k, v in kernels.items() if k in ("metadata_plan", "plan", "metadata"))
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    res = {
+        "workload": name, "mode": mode, "backward": backward,
+        "ms_per_step": round(ms, 4), "GBs": round(gbs, 1),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "timing": "hip-graph replay" if err is None else f"eager ({err})",
+        "metadata_plan_us": round(plan_us, 2),
+        "dominant_kernel": dom, "dominant_avg_us": round(kernels[dom]["avg_us"], 2),
+        "dominant_frac": round(kernels[dom]["frac"], 4),
+    }
+    del idx, w, xs, grad_out, step, direct_step
+    torch.cuda.empty_cache()
+    return res
+
+
+# The other BASELINE configurations, measured in every default run beside the headline.
+CONFIG_LINES = [("mid", "det"), ("mid", "atomic"), ("skewed", "det"), ("skewed", "atomic"),
+                ("detatomic", "det"), ("detatomic", "atomic"), ("plumbing", "det")]
+
+
 def _cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -297,6 +477,9 @@ def main() -> int:
                          "the permutation's slot map")
     ap.add_argument("--no-standard", action="store_true",
                     help="skip the torch STANDARD combine timed on the same GPU")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other BASELINE configurations (the 'configs' object)")
+    ap.add_argument("--config-steps", type=int, default=10)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -309,9 +492,8 @@ def main() -> int:
     import torch
 
     import fastmoe_amd
-    from fastmoe_amd import ops
     from fastmoe_amd.workloads import (WORKLOADS, algorithmic_bytes, dispatch_bytes,
-                                       kernel_bytes, make_experts, make_routing, make_topk)
+                                       kernel_bytes, make_topk)
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -322,34 +504,13 @@ def main() -> int:
     backward = wl.backward and not args.fwd_only and not args.inplace
     gen_dev = torch.Generator(device=dev)
     xb = torch.empty(0, dtype=wl.dtype).element_size()
+    direct_step = None
     if args.path == "combine":
         metric = METRIC
-        idx, w, counts = make_routing(wl)
-        idx, w = idx.to(dev), w.to(dev)
-        xs = make_experts(counts, wl.D, wl.dtype, dev, wl.seed)
-        if backward:
-            xs = [x.requires_grad_(True) for x in xs]
-            w.requires_grad_(True)
-        grad_out = torch.randn(wl.T, wl.D, device=dev, dtype=torch.float32,
-                               generator=gen_dev.manual_seed(1)).to(wl.dtype)
+        idx, w, xs, grad_out = _combine_inputs(wl, dev, backward)
         fwd_b, bwd_b = algorithmic_bytes(wl.T, wl.D, wl.N, xb, 4 if args.inplace else xb)
-        inputs = [w, *xs]
-
-        if args.inplace:
-            out_static = torch.zeros((wl.T, wl.D), device=dev)
-            meta = fastmoe_amd.prepare_grouped_metadata(xs, dev)
-
-            def step():
-                out_static.zero_()
-                return fastmoe_amd.grouped_weighted_scatter_add(
-                    xs, idx, w, (wl.T, wl.D), out=out_static, metadata=meta, mode=args.mode)
-        else:
-            def step():
-                out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (wl.T, wl.D),
-                                                                mode=args.mode)
-                if backward:
-                    torch.autograd.grad(out, inputs, grad_out)
-                return out
+        step, direct_step = _combine_steps(wl, xs, idx, w, grad_out, args.mode, backward,
+                                           args.inplace, dev)
 
         std = lambda: _standard_combine_step(wl, xs, idx, w, grad_out, backward)  # noqa: E731
         verify = lambda: _verify_combine(wl, xs, idx, w, args.mode)  # noqa: E731
@@ -421,71 +582,25 @@ def main() -> int:
     torch.cuda.synchronize()
     fast_peak = torch.cuda.max_memory_allocated(dev) - base_mem
 
-    timer = EventTimer()
-    ops._TIMER = timer
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    def timed(fn, n):
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record()
-        for _ in range(n):
-            fn()
-        stop.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(stop) / n, (time.perf_counter() - t0) * 1e3 / n
-
-    # Eager steps through the public autograd API (host-inclusive: Python + autograd over E
-    # expert tensors is part of this number).
-    eager_ms, eager_wall_ms = timed(step, args.steps)
-
-    # Per-kernel durations: HIP events around every C-ABI launch, on the launch stream.  A sleep
-    # kernel first gives the GPU a backlog so that the host has enqueued each event-kernel-event
-    # triple before the GPU reaches it (the events then bracket the kernel, not host gaps).
-    timer.records.clear()
-    timer.enabled = True
-    try:
-        torch.cuda._sleep(int(args.steps * 3e-3 * 2.4e9))
-        backlog = True
-    except Exception:
-        backlog = False
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    timer.enabled = False
-    kernels = timer.summary()
-    timer.records.clear()
+    # Eager steps through the public API (host-inclusive: Python + autograd over E expert tensors
+    # is part of this number).
+    eager_ms, eager_wall_ms = _timed(step, args.steps)
+    kernels, backlog = _event_kernels(step, args.steps)
 
     graph_error = None
-    graph = None
+    ms = None
     if not args.eager:
-        # The same step captured once as a HIP graph (metadata upload, plan, forward, backward)
-        # and replayed: the timed region is pure device work, the convention of the reference's
-        # own kernel benchmark (run_on_cloud.py:66-92).
-        try:
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for _ in range(2):
-                    step()
-            torch.cuda.current_stream().wait_stream(side)
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                step()
-            for _ in range(args.warmup):
-                graph.replay()
-            torch.cuda.synchronize()
-        except Exception as exc:  # capture unsupported: report eager numbers only
-            graph_error = f"{type(exc).__name__}: {exc}"
-            graph = None
-
-    if graph is not None:
-        ms, wall_ms = timed(graph.replay, args.steps)
+        # The step captured once as a HIP graph and replayed: the timed region is pure device
+        # work, the convention of the reference's own kernel benchmark (run_on_cloud.py:66-92).
+        # The combine's step is captured from the launches the autograd path makes, issued by its
+        # own forward and backward functions on this thread (_StepCtx), without the autograd
+        # engine.
+        ms, wall_ms, graph_error = _graph_ms(direct_step or step, args.steps, args.warmup)
+    if ms is not None:
         timing = "hip-graph replay of one captured step"
     else:
         ms, wall_ms = eager_ms, eager_wall_ms
@@ -494,19 +609,20 @@ def main() -> int:
 
     # Dominant kernel: the single-kernel span with the longest average launch.
     kbytes = kernel_bytes(wl.T, wl.D, wl.N, xb, 4 if args.inplace else xb)
-    for name, k in kernels.items():
-        if name in kbytes:
-            k["algorithmic_bytes"] = kbytes[name]
-            k["GBs"] = kbytes[name] / (k["avg_us"] * 1e-6) / 1e9
-            k["frac"] = k["GBs"] / HBM_PEAK_GBS
-    dom_name = max((n for n in kernels if n in kbytes), key=lambda n: kernels[n]["avg_us"])
+    dom_name = _summarize_kernels(kernels, kbytes)
     dom_bytes = kbytes[dom_name]
     dom_us = kernels[dom_name]["avg_us"]
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    traffic = None
+    traffic, traffic_info = None, None
     tfile = ROOT / "profiles" / f"traffic_{wl.name}_{dom_name}.json"
     if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        from fastmoe_amd.build import source_hash
+
+        tj = json.loads(tfile.read_text())
+        traffic = tj.get("hbm_bytes_per_launch")
+        traffic_info = {"file": str(tfile.relative_to(ROOT)), "commit": tj.get("commit"),
+                        "sources_sha256": tj.get("sources_sha256"),
+                        "matches_current_sources": tj.get("sources_sha256") == source_hash()}
 
     value = step_bytes / (ms * 1e-3) / 1e9
     res = {
@@ -550,6 +666,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_measured_on": traffic_info,
             "algorithmic_bytes": dom_bytes,
             "avg_launch_us": round(dom_us, 3),
         },
@@ -562,6 +679,11 @@ def main() -> int:
         res["peak_mem_gb"] = round(fast_peak / 2 ** 30, 3)
     if not args.no_cpu_baseline and args.path == "combine":
         res["cpu_baseline"] = _cpu_baseline(wl, args.cpu_sample_tokens or wl.T, args.cpu_reps)
+    if (args.path == "combine" and not args.no_configs and not args.inplace
+            and args.workload == "gigachat"):
+        # the other BASELINE configurations, timed in this run (no CPU baseline)
+        torch.cuda.empty_cache()
+        res["configs"] = [_config_line(n, m, args.config_steps, 3, dev) for n, m in CONFIG_LINES]
     print(json.dumps(res), flush=True)
     return 0
 

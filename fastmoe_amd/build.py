@@ -44,6 +44,21 @@ HIPCC_FLAGS = [
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall"]
 
 
+def source_hash() -> str:
+    """sha256 (hex, 16 digits) of every source the library is built from: the HIP and host
+    translation units, their headers and the C ABI header.  Measurements kept in profiles/ record
+    it, so a reader (bench.py) can tell whether they describe the current kernels."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.cpp"))
+    files.append(PKG.parent / "include" / "fastmoe_amd.h")
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def _hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     cand = Path(rocm) / "bin" / "hipcc"
