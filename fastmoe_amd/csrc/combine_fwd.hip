@@ -75,14 +75,15 @@ __device__ __forceinline__ void fwd_det_body(const int32_t* __restrict__ row_ptr
     // segments are already in ascending g.
     if (end - beg <= kWave) lr.sort_by_row(cnt, lane);
     for (int i = 0; i < cnt; i += R) {
-      // Batch of R rows; a partial batch repeats its last row for the loads (never accumulated),
-      // so every load is issued unconditionally.
+      // Batch of R rows.  The spare slots of a partial batch load through an empty range
+      // (num_records 0): the hardware range check returns zeros without a memory request, so
+      // every load is issued unconditionally and none is wasted.
       raw_t a[R][U];
       float wr[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int ir = min(i + r, cnt - 1);
-        const rsrc_t rx = make_rsrc(lr.src(ir), xrow_bytes);
+        const rsrc_t rx = make_rsrc(lr.src(ir), i + r < cnt ? xrow_bytes : 0u);
         wr[r] = lr.w(ir);
 #pragma unroll
         for (int u = 0; u < U; ++u) a[r][u] = load_x<TX, V, AL>(rx, xoff[u]);
@@ -440,10 +441,12 @@ static int launch_fwd_v(const FwdArgs& a) {
     const int tile = (int)fmoe_host::opt(a.mode == FMOE_MODE_DET ? fmoe_host::kOptFwdTile
                                                                  : fmoe_host::kOptFwdAtomicTile);
     int U = tile / 10, R = tile % 10;
-    if (!((U == 4 && R == 4) || (U == 2 && (R == 8 || R == 4)) || (U == 1 && R == 8))) {
+    if (!((U == 4 && (R == 4 || R == 2)) || (U == 2 && (R == 8 || R == 4)) ||
+          (U == 1 && R == 8))) {
       U = pick_u(a.D, V);
       R = U >= 4 ? 4 : 8;
     }
+    if (U == 4 && R == 2) return launch_fwd_u<TX, TO, V, 4, 2>(a);
     if (U == 4) return launch_fwd_u<TX, TO, V, 4, 4>(a);
     if (U == 2 && R == 4) return launch_fwd_u<TX, TO, V, 2, 4>(a);
     if (U == 2) return launch_fwd_u<TX, TO, V, 2, 8>(a);

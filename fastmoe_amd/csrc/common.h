@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "../../include/fastmoe_amd.h"
+#include "options.h"
 
 #pragma clang fp contract(off)
 
@@ -380,22 +381,6 @@ namespace fmoe_host {
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();
 
-// Kernel-variant options (fmoe_set_option).  Each starts from its environment variable, read once
-// when the library loads, else from the measured-best default; launches read the table, not the
-// environment.
-enum Opt {
-  kOptPlan = 0,      // "plan": 0 bucketed (default), 1 three-launch count/fill/order
-  kOptBwdFused,      // "bwd_fused": 1 = both gradients in one backward pass
-  kOptGwStaged,      // "gw_staged": 0 = grad_w pass reads grad_out per wave instead of via LDS
-  kOptForceScalar,   // "force_scalar": 1 = element-wise (unvectorised) kernels
-  kOptBwdU,          // "bwd_u": backward vectors per lane per column step (0 = by D)
-  kOptFwdTile,       // "fwd_tile": forward tile <U><R> (0 = by D)
-  kOptFwdAtomicTile, // "fwd_atomic_tile"
-  kOptFwdDetU,       // "fwd_det_u": forward vectors per lane per row (0 = by D)
-  kOptFwdGrid,       // "fwd_grid": forward workgroups (0 = one wave per unit)
-  kOptCount
-};
-int64_t opt(int o);
 
 inline int dtype_bytes(int dt) {
   switch (dt) {

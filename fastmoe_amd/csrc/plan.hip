@@ -268,29 +268,58 @@ constexpr int kTokRows = 256;                          // rows per workgroup aim
 constexpr int kTokGroups = 256;
 constexpr int kTokExperts = 4096;                      // expert tables staged in LDS
 constexpr int64_t kTokMaxRows = int64_t(1) << 17;
-constexpr int kTokLoads = 16;                          // index loads per lane per batch
+constexpr int kTokLoads = 8;                           // 16-byte index loads per lane per batch
 
-__device__ __forceinline__ void tok_load_meta(const TokMetaGlobal& m, int ne, int* off32,
-                                              uint64_t* ptr_lds) {
-  for (int i = threadIdx.x; i <= ne; i += kScanThreads) {
-    off32[i] = (int)m.offsets[i];
-    if (i < ne) ptr_lds[i] = (uint64_t)m.ptr_table[i];
-  }
-}
-__device__ __forceinline__ void tok_load_meta(const TokMetaArgs& m, int ne, int* off32,
-                                              uint64_t* ptr_lds) {
-  const int e = threadIdx.x;  // ne <= 256 < kScanThreads: one expert per thread
-  if (e <= ne) off32[e] = m.a.off[e];
-  if (e < ne) ptr_lds[e] = (uint64_t)m.a.ptr[e];
-  if (blockIdx.x == 0) {  // workgroup-uniform: the metadata outputs (fmoe_build_metadata's)
-    if (e < ne) {
-      m.ptr_table[e] = m.a.ptr[e];
-      m.chunk_sizes[e] = m.a.off[e + 1] - m.a.off[e];
+// The expert table of a plan workgroup, loaded into registers when the workgroup starts and
+// written to LDS after the pass over idx, so that its load latency overlaps the pass instead of
+// preceding it.
+template <typename Meta> struct TokMetaRegs;
+template <> struct TokMetaRegs<TokMetaGlobal> {
+  static constexpr int Q = kTokExperts / kScanThreads;  // experts per thread (the last thread
+  int off[Q + 1];                                       // also holds off[kTokExperts])
+  uint64_t ptr[Q];
+  __device__ __forceinline__ void load(const TokMetaGlobal& m, int ne) {
+#pragma unroll
+    for (int q = 0; q <= Q; ++q) {
+      const int e = (int)threadIdx.x + q * kScanThreads;
+      off[q] = e <= ne ? (int)m.offsets[e] : 0;
+      if (q < Q) ptr[q] = e < ne ? (uint64_t)m.ptr_table[e] : 0;
     }
-    if (e <= ne) m.offsets[e] = m.a.off[e];
-    if (e == 0) *m.max_rows = m.a.max_rows;
   }
-}
+  __device__ __forceinline__ void store(const TokMetaGlobal&, int ne, int* off32,
+                                        uint64_t* ptr_lds) const {
+#pragma unroll
+    for (int q = 0; q <= Q; ++q) {
+      const int e = (int)threadIdx.x + q * kScanThreads;
+      if (e <= ne) off32[e] = off[q];
+      if (q < Q && e < ne) ptr_lds[e] = ptr[q];
+    }
+  }
+};
+template <> struct TokMetaRegs<TokMetaArgs> {
+  int off, next;  // off[e], off[e + 1]
+  uint64_t ptr;
+  __device__ __forceinline__ void load(const TokMetaArgs& m, int ne) {
+    const int e = threadIdx.x;  // ne <= 256 < kScanThreads: one expert per thread
+    off = e <= ne ? m.a.off[e] : 0;
+    next = e < ne ? m.a.off[e + 1] : 0;
+    ptr = e < ne ? (uint64_t)m.a.ptr[e] : 0;
+  }
+  __device__ __forceinline__ void store(const TokMetaArgs& m, int ne, int* off32,
+                                        uint64_t* ptr_lds) const {
+    const int e = threadIdx.x;
+    if (e <= ne) off32[e] = off;
+    if (e < ne) ptr_lds[e] = ptr;
+    if (blockIdx.x == 0) {  // workgroup-uniform: the metadata outputs (fmoe_build_metadata's)
+      if (e < ne) {
+        m.ptr_table[e] = (int64_t)ptr;
+        m.chunk_sizes[e] = next - off;
+      }
+      if (e <= ne) m.offsets[e] = off;
+      if (e == 0) *m.max_rows = m.a.max_rows;
+    }
+  }
+};
 
 // Exclusive scan of v and sum of s over a 1024-thread block, in one barrier round.
 __device__ __forceinline__ int tok_scan_and_sum(int v, int s, int* sum_s) {
@@ -337,24 +366,32 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   const int nloc = hi - lo;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
+  TokMetaRegs<Meta> mreg;
+  mreg.load(meta, ne);  // used after the pass over idx
   for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) cnt[i] = 0;
-  tok_load_meta(meta, ne, off32, ptr_lds);
   if (threadIdx.x == 0) misaligned = 0;
   __syncthreads();
 
-  // 1. pass over this wave's rows [r0, r1), ascending g, kTokLoads loads per lane in flight
+  // 1. pass over this wave's rows [r0, r1) in ascending g.  Every workgroup reads all of idx, so
+  //    the pass is bound by the rate at which a CU issues vector loads, not by bytes: the index
+  //    is read with 16-byte loads, RPL consecutive rows per lane (a lane's rows, then the next
+  //    lane's, so the wave still sees its rows in ascending g).  The rows past the last whole
+  //    vector (fewer than RPL) are read one per lane after the pass.
+  constexpr int RPL = 16 / (int)sizeof(TI);
   const int n32 = (int)N;
-  const int per = ((n32 + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;
+  const int n_al = n32 - n32 % RPL;  // rows in whole 16-byte vectors
+  const int per = ((n32 + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;  // 64 | per
   const int r0 = min(n32, wave * per);
   const int r1 = min(n32, r0 + per);
   int* mycnt = cnt + wave * nloc;
   int2* mystash = stash + wave * kTokWaveStash;
-  const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));
+  const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));  // element loads
+  const rsrc_t rv = make_rsrc(idx, (uint32_t)((int64_t)n_al * (int64_t)sizeof(TI)));  // vectors
   int below = 0;   // rows of this lane whose bin precedes the range
   int wcount = 0;  // rows of the range seen by this wave (wave-uniform)
-  auto bin_at = [&](int g, TI raw) -> uint32_t {  // 0xffffffff: not a row of this wave
+  auto bin_at = [&](int g, int lim, TI raw) -> uint32_t {  // 0xffffffff: not a row of this wave
     const int64_t t = (int64_t)raw;
-    return g < r1 ? ((uint64_t)t < (uint64_t)T ? (uint32_t)t : (uint32_t)T) : 0xffffffffu;
+    return g < lim ? ((uint64_t)t < (uint64_t)T ? (uint32_t)t : (uint32_t)T) : 0xffffffffu;
   };
   auto count_row = [&](int g, uint32_t b) {
     below += b < (uint32_t)lo ? 1 : 0;
@@ -370,29 +407,93 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       wcount += __popcll(m);
     }
   };
-  auto load_batch = [&](int base, TI* v) {
+  // rows g0 .. g0 + RPL - 1 of this lane: a row's stash slot counts the range's rows held by the
+  // lower lanes (all RPL of theirs) and by this lane's lower rows
+  auto count_vec = [&](int g0, const uint32_t* b) {
+    uint32_t j[RPL];
+    bool in[RPL];
+    uint64_t m[RPL];
+    uint64_t any = 0;
 #pragma unroll
-    for (int i = 0; i < kTokLoads; ++i) {
-      const int g = base + i * kWave + lane;  // past N: zeros from the range check, no traffic
-      v[i] = __builtin_bit_cast(
-          TI, Raw<sizeof(TI)>::template ld<kCPolCached>(ri, (uint32_t)g * (uint32_t)sizeof(TI)));
+    for (int r = 0; r < RPL; ++r) {
+      below += b[r] < (uint32_t)lo ? 1 : 0;
+      j[r] = b[r] - (uint32_t)lo;
+      in[r] = j[r] < (uint32_t)nloc;
+      m[r] = __ballot(in[r]);
+      any |= m[r];
+    }
+    if (any) {  // wave-uniform
+      int slot = wcount;
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) slot += lanes_below(m[r]);
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) {
+        if (in[r]) {
+          atomicAdd(&mycnt[j[r]], 1);
+          if (slot < kTokWaveStash) mystash[slot] = make_int2(g0 + r, (int)j[r]);
+          ++slot;
+        }
+        wcount += __popcll(m[r]);
+      }
     }
   };
-  constexpr int kBatchRows = kTokLoads * kWave;
-  if (r0 < r1) {  // wave-uniform
-    TI cur[kTokLoads], nxt[kTokLoads];
+  auto load_batch = [&](int base, u32x4* v) {  // past n_al: zeros from the range check, no traffic
+#pragma unroll
+    for (int i = 0; i < kTokLoads; ++i) {
+      const int g0 = base + (i * kWave + lane) * RPL;
+      v[i] = Raw<16>::template ld<kCPolCached>(rv, (uint32_t)g0 * (uint32_t)sizeof(TI));
+    }
+  };
+  auto row_of = [](const u32x4& v, int r) -> TI {
+    if constexpr (sizeof(TI) == 8)
+      return (TI)((uint64_t)v[2 * r] | ((uint64_t)v[2 * r + 1] << 32));
+    else
+      return (TI)v[r];
+  };
+  constexpr int kBatchRows = kTokLoads * kWave * RPL;
+  const int lim = min(r1, n_al);
+  if (r0 < lim) {  // wave-uniform
+    u32x4 cur[kTokLoads], nxt[kTokLoads];
     load_batch(r0, cur);
-    for (int base = r0; base < r1; base += kBatchRows) {
-      if (base + kBatchRows < r1) load_batch(base + kBatchRows, nxt);
+    for (int base = r0; base < lim; base += kBatchRows) {
+      // Unconditional: a prefetch under a branch makes the compiler wait for the first of these
+      // loads before it uses `cur` (one wait count must fit both paths), which serialises the
+      // batches on the memory latency.  Past the range the loads return zeros without traffic.
+      load_batch(base + kBatchRows, nxt);
 #pragma unroll
       for (int i = 0; i < kTokLoads; ++i) {
-        const int g = base + i * kWave + lane;
-        count_row(g, bin_at(g, cur[i]));
+        const int g0 = base + (i * kWave + lane) * RPL;
+        uint32_t b[RPL];
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) b[r] = bin_at(g0 + r, lim, row_of(cur[i], r));
+        count_vec(g0, b);
       }
 #pragma unroll
       for (int i = 0; i < kTokLoads; ++i) cur[i] = nxt[i];
     }
   }
+  if (r1 > n_al && r0 < r1) {  // wave-uniform: the rows past the last whole vector
+    const int g = max(r0, n_al) + lane;
+    count_row(g, bin_at(g, r1,
+                        __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
+                                                   ri, (uint32_t)g * (uint32_t)sizeof(TI)))));
+  }
+  mreg.store(meta, ne, off32, ptr_lds);
+  // The gates of the stashed rows, loaded before the scan so that their latency overlaps it.
+  constexpr int kStashChunks = kTokWaveStash / kWave;
+  int2 se[kStashChunks];
+  float sw[kStashChunks];
+  if (wcount <= kTokWaveStash) {  // wave-uniform
+#pragma unroll
+    for (int q = 0; q < kStashChunks; ++q) {
+      const int at = q * kWave + lane;
+      const bool act = at < wcount;
+      se[q] = act ? mystash[at] : make_int2(0, 0);
+      sw[q] = act ? ld1(w + se[q].x) : 0.f;
+    }
+  }
+  __syncthreads();  // the expert table and every wave's counts
+
   if (blockIdx.x == 0) {
     // a source row is misaligned iff its expert's base is, or the expert has two or more rows
     // and the row length is not a multiple of 16 bytes
@@ -401,9 +502,8 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       const int n = off32[e + 1] - off32[e];
       if (n > 0 && ((ptr_lds[e] & 15) || (n > 1 && (row_bytes & 15)))) mis = 1;
     }
-    if (mis) misaligned = 1;
+    if (mis) misaligned = 1;  // read after the next barrier
   }
-  __syncthreads();
 
   // 2. thread j owns bin j of the range: its rows over all waves, row_ptr, and each wave's first
   //    place in it (the cursors)
@@ -424,11 +524,11 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     }
     if (hi == nb && bj == nloc - 1) row_ptr[nb] = run;  // == N
   }
+  __syncthreads();  // the cursors (and the misaligned flag)
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     status[kStatusMisaligned] = misaligned;
     status[kStatusLongest] = -1;  // not recorded: no workgroup sees every segment
   }
-  __syncthreads();  // the cursors
 
   // 3. fill: each wave its rows in ascending g -- from the stash, or again from idx if the stash
   //    overflowed
@@ -448,18 +548,15 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     }
   };
   if (wcount <= kTokWaveStash) {  // wave-uniform
-    for (int c0 = 0; c0 < wcount; c0 += kWave) {
-      const bool act = c0 + lane < wcount;
-      const int2 e = act ? mystash[c0 + lane] : make_int2(0, 0);
-      const float wg = act ? ld1(w + e.x) : 0.f;
-      place(act, e.x, e.y, wg);
-    }
+#pragma unroll
+    for (int q = 0; q < kStashChunks; ++q)
+      if (q * kWave < wcount) place(q * kWave + lane < wcount, se[q].x, se[q].y, sw[q]);
   } else {
     for (int base = r0; base < r1; base += kWave) {
       const int g = base + lane;
       const uint32_t b = bin_at(
-          g, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
-                                        ri, (uint32_t)g * (uint32_t)sizeof(TI))));
+          g, r1, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
+                                            ri, (uint32_t)g * (uint32_t)sizeof(TI))));
       const uint32_t j = b - (uint32_t)lo;
       const bool in = j < (uint32_t)nloc;
       const float wg = in ? ld1(w + g) : 0.f;
@@ -630,6 +727,8 @@ bool tok_grid(int64_t N, int64_t T, int64_t E, int64_t* groups_out, int64_t* bin
   const int64_t nb = T + 1;
   int64_t groups = std::max<int64_t>((N + kTokRows - 1) / kTokRows, (nb + kTokBins - 1) / kTokBins);
   groups = std::min<int64_t>(std::min<int64_t>(groups, kTokGroups), nb);
+  if (const int64_t forced = fmoe_host::opt(fmoe_host::kOptPlanGroups); forced > 0)
+    groups = std::min<int64_t>(std::min<int64_t>(forced, kTokGroups), nb);
   const int64_t bins = (nb + groups - 1) / groups;
   groups = (nb + bins - 1) / bins;  // every workgroup gets a non-empty bin range
   *groups_out = groups;
