@@ -331,6 +331,45 @@ def _graph_ms(capture_step, steps, warmup):
     return ms, wall_ms, None
 
 
+def _autograd_floor_ms(wl, xs, idx, w, grad_out, steps):
+    """Host time per step of torch's autograd machinery alone for this call shape: a Function
+    that takes the same arguments (indices, weights, out_shape, *expert_tensors), does no work and
+    returns gradients of the same shapes, then torch.autograd.grad over [w, *xs] as the eager step
+    does.  Everything the eager step costs above this is the library's own host work."""
+    import torch
+
+    N = sum(x.shape[0] for x in xs)
+    sizes = [x.shape[0] for x in xs]
+    gx_all = torch.empty(N, wl.D, dtype=wl.dtype, device=w.device)
+    gw = torch.empty_like(w)
+
+    class _NoOp(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, indices, weights, out_shape, *expert_tensors):
+            ctx.save_for_backward(indices, weights, *expert_tensors)
+            return torch.empty(out_shape, dtype=expert_tensors[0].dtype,
+                               device=expert_tensors[0].device)
+
+        @staticmethod
+        def backward(ctx, g):
+            return (None, gw, None, *torch.split(gx_all, sizes))
+
+    inputs = [w, *xs]
+
+    def step():
+        out = _NoOp.apply(idx, w, (wl.T, wl.D), *xs)
+        torch.autograd.grad(out, inputs, grad_out)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
 def _combine_inputs(wl, dev, backward, inplace=False):
     import torch
 
@@ -589,6 +628,8 @@ def main() -> int:
     # Eager steps through the public API (host-inclusive: Python + autograd over E expert tensors
     # is part of this number).
     eager_ms, eager_wall_ms = _timed(step, args.steps)
+    floor_ms = (_autograd_floor_ms(wl, xs, idx, w, grad_out, args.steps)
+                if args.path == "combine" and backward else None)
     kernels, backlog = _event_kernels(step, args.steps)
 
     graph_error = None
@@ -653,6 +694,7 @@ def main() -> int:
         "eager_ms_per_step": round(eager_ms, 4),
         "eager_value": round(step_bytes / (eager_ms * 1e-3) / 1e9, 2),
         "eager_wall_ms_per_step": round(eager_wall_ms, 4),
+        "eager_autograd_floor_ms": round(floor_ms, 4) if floor_ms is not None else None,
         "graph_error": graph_error,
         "kernel_timing": "HIP events around each launch in eager steps queued behind a sleep kernel"
                          if backlog else "HIP events around each launch in eager steps",

@@ -550,6 +550,44 @@ def test_plan_matches_oracle(case, path, kernel_options):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+@pytest.mark.parametrize("groups", [1, 7, 64, 256])
+def test_plan_one_launch_any_group_count(groups, idx_dtype, kernel_options):
+    """The one-launch plan is the oracle's stable inverse whatever the number of workgroups that
+    split the token bins (option plan_groups): one workgroup for all bins, a count that leaves a
+    ragged last range, and more workgroups than the automatic choice.  N = 5003 is neither even
+    nor a multiple of 4, so the rows past the last whole 16-byte index vector take the tail
+    path, for int64 (2 rows per vector) and int32 (4 rows per vector) indices; 3% of the indices
+    are out of range."""
+    from oracle import cref
+
+    kernel_options(plan=_PLAN_PATHS["tok"], plan_groups=groups)
+    gen = torch.Generator().manual_seed(61 + groups)
+    T, N, D = 300, 5003, 8
+    idx = torch.randint(0, T, (N,), generator=gen)
+    bad = torch.rand(N, generator=gen) < 0.03
+    idx = torch.where(bad, torch.full_like(idx, T + 5), idx).to(idx_dtype)
+    w = torch.rand(N, generator=gen)
+    cuts = torch.sort(torch.randint(0, N + 1, (15,), generator=gen)).values.tolist()
+    sizes = [b - a for a, b in zip([0] + cuts, cuts + [N])]
+    experts = [torch.randn(n, D, generator=gen) for n in sizes]
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
+    plan = fastmoe_amd.build_plan(meta, idd, wd, T)
+    lib = fastmoe_amd._abi.lib()
+    rp_off = lib.fmoe_plan_row_ptr_offset(N, T)
+    rec_off = lib.fmoe_plan_records_offset(N, T)
+    row_ptr = plan[rp_off: rp_off + 4 * (T + 2)].view(torch.int32).cpu().numpy()
+    rec = plan[rec_off: rec_off + 16 * N].view(torch.int64).view(N, 2).cpu()
+    want_rp, want_g = cref.plan(idx.to(torch.int64).numpy(), T)
+    np.testing.assert_array_equal(row_ptr, want_rp)
+    np.testing.assert_array_equal((rec[:, 1] >> 32).numpy().astype(np.int32), want_g)
+    wbits = (rec[:, 1] & 0xFFFFFFFF).numpy().astype(np.uint32)
+    np.testing.assert_array_equal(wbits, w.numpy()[want_g].view(np.uint32))
+    st = ops.plan_status(plan).cpu().numpy()
+    assert st[0] == int(bad.sum()) and st[1] == 0
+
+
 def test_bwd_f16_grad_x_rounds_twice_like_the_reference():
     """f16 experts, fp32 gates: grad_X is the fp32 product rounded to fp32 and then to f16
     (index_select * w, then autograd's cast; ops.py:344-353).  The inputs include elements where
