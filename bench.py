@@ -456,6 +456,18 @@ def _config_line(name, mode, steps, warmup, dev):
         ms, _ = _timed(step, steps)
     plan_us = sum(v["avg_us"] for k, v in kernels.items() if k in ("metadata_plan", "plan", "metadata"))
     gbs = step_bytes / (ms * 1e-3) / 1e9
+    repeat = None
+    if name == "detatomic":
+        # BASELINE's det-vs-atomic configuration: 10 runs on the same inputs; det must repeat bit
+        # for bit, atomic is reported with its largest run-to-run difference
+        with torch.no_grad():
+            ref = step().clone()
+            same, worst = True, 0.0
+            for _ in range(9):
+                o = step()
+                same = same and torch.equal(o.view(torch.int16), ref.view(torch.int16))
+                worst = max(worst, (o.float() - ref.float()).abs().max().item())
+        repeat = {"runs": 10, "bit_identical": same, "max_abs_diff": worst}
     res = {
         "workload": name, "mode": mode, "backward": backward,
         "ms_per_step": round(ms, 4), "GBs": round(gbs, 1),
@@ -465,6 +477,8 @@ def _config_line(name, mode, steps, warmup, dev):
         "dominant_kernel": dom, "dominant_avg_us": round(kernels[dom]["avg_us"], 2),
         "dominant_frac": round(kernels[dom]["frac"], 4),
     }
+    if repeat is not None:
+        res["repeatability"] = repeat
     del idx, w, xs, grad_out, step, direct_step
     torch.cuda.empty_cache()
     return res

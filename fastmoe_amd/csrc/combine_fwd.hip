@@ -293,8 +293,9 @@ __global__ __launch_bounds__(kGroup) void k_acc_store(const float* __restrict__ 
   }
 }
 
-// out[t, :] = 0 for every row (an atomic-mode call that overwrites out).
-template <typename TO>
+// out[t, :] = 0 for every row (an atomic-mode call that overwrites out); 16-byte stores when
+// the rows allow them (VEC, as in the accumulator passes).
+template <typename TO, bool VEC>
 __global__ __launch_bounds__(kGroup) void k_rows_zero(TO* __restrict__ out, int64_t out_stride,
                                                       uint32_t D, uint32_t T) {
   const uint32_t groups = (D + kAccCols - 1) / kAccCols;
@@ -304,9 +305,15 @@ __global__ __launch_bounds__(kGroup) void k_rows_zero(TO* __restrict__ out, int6
     const uint32_t t = (uint32_t)(i / groups);
     const uint32_t c = (uint32_t)(i - (int64_t)t * groups) * kAccCols;
     TO* o = out + (int64_t)t * out_stride + c;
+    if constexpr (VEC) {
+      constexpr int kWords = kAccCols * (int)sizeof(TO) / 16;  // 16-byte words per 8 columns
 #pragma unroll
-    for (int k = 0; k < kAccCols; ++k)
-      if (c + k < D) st1(o + k, 0.f);
+      for (int k = 0; k < kWords; ++k) reinterpret_cast<u32x4*>(o)[k] = u32x4{0u, 0u, 0u, 0u};
+    } else {
+#pragma unroll
+      for (int k = 0; k < kAccCols; ++k)
+        if (c + k < D) st1(o + k, 0.f);
+    }
   }
 }
 
@@ -317,8 +324,14 @@ static unsigned row_pass_blocks(int64_t T, int64_t D) {
 
 template <typename TO>
 static int launch_zero(void* out, int64_t stride, int64_t D, int64_t T, hipStream_t s) {
-  hipLaunchKernelGGL((k_rows_zero<TO>), dim3(row_pass_blocks(T, D)), dim3(kGroup), 0, s,
-                     static_cast<TO*>(out), stride, (uint32_t)D, (uint32_t)T);
+  const bool vec = D % kAccCols == 0 && (uintptr_t)out % 16 == 0 &&
+                   (stride * (int64_t)sizeof(TO)) % 16 == 0;
+  if (vec)
+    hipLaunchKernelGGL((k_rows_zero<TO, true>), dim3(row_pass_blocks(T, D)), dim3(kGroup), 0, s,
+                       static_cast<TO*>(out), stride, (uint32_t)D, (uint32_t)T);
+  else
+    hipLaunchKernelGGL((k_rows_zero<TO, false>), dim3(row_pass_blocks(T, D)), dim3(kGroup), 0, s,
+                       static_cast<TO*>(out), stride, (uint32_t)D, (uint32_t)T);
   return fmoe_host::check_launch("fmoe_combine_fwd(zero out)");
 }
 
