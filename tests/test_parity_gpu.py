@@ -1079,6 +1079,73 @@ def test_graph_capture_autograd_step_replays(mode):
         _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum().item()
 
 
+class _DirectCtx:
+    """The autograd context's part that GroupedWeightedScatterAdd's forward/backward functions
+    use (save_for_backward / saved_tensors), for calling them without the autograd engine."""
+
+    def save_for_backward(self, *tensors):
+        self.saved_tensors = tensors
+
+
+@pytest.mark.parametrize("mode", ["det", "atomic"])
+def test_graph_capture_direct_step_replays(mode):
+    """bench.py's timed step: the launches of one autograd step (metadata + plan, forward, grad_X
+    and grad_w passes), issued by the autograd path's own forward and backward functions on this
+    thread, captured once as a graph.  Every replay (with eager work in between) equals the oracle
+    -- forward and grad_X bit for bit in det mode, the one-ulp bar in atomic mode, grad_w within
+    1e-6 of sum|terms| -- and, in det mode, the eager step bit for bit."""
+    wl, T, idx, w, experts = _inputs("gigachat", T=128)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    go_cpu = torch.randn(T, wl.D, generator=torch.Generator().manual_seed(5)).to(wl.dtype)
+    go = go_cpu.to(DEV)
+    want, _, _ = oracle_fwd(experts, idx, w, T, wl.dtype)
+    want16 = torch.from_numpy(want.view(np.int16)).view(wl.dtype).float().numpy()
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, go_cpu)
+    scale_fwd = abs_sum(experts, idx, w, T)
+    scale_gw = abs_dot(experts, idx, go_cpu, T)
+    k = int(np.bincount(idx.numpy(), minlength=T).max())
+
+    def step():
+        with torch.no_grad():
+            ctx = _DirectCtx()
+            out = ops._combine_forward(ctx, mode, None, idd, wd, (T, wl.D), xd, True)
+            gw, gx = ops._combine_backward(ctx, go, True, [True] * len(xd))
+        return (out, gw, *gx)
+
+    def check(res):
+        out, gw, gx = res[0], res[1], res[2:]
+        if mode == "det":
+            np.testing.assert_array_equal(bits(out), want)
+        else:
+            assert np.all(within_one_ulp16(out.float().cpu().numpy(), want16, wl.dtype, k,
+                                           scale_fwd))
+        np.testing.assert_array_equal(np.concatenate([to_np(t) for t in gx]), want_gx)
+        assert np.all(np.abs(gw.double().cpu().numpy() - want_gw) <= 1e-6 * scale_gw + 1e-30)
+
+    first = step()
+    torch.cuda.synchronize()
+    check(first)
+    eager = [bits(t) for t in first]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static = step()
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        check(static)
+        if mode == "det":
+            for got, want_bits in zip(static, eager):
+                np.testing.assert_array_equal(bits(got), want_bits)
+        _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum().item()
+
+
 @pytest.mark.parametrize("name", ["gigachat"])
 def test_full_size_fwd_bwd_parity(name):
     """The BASELINE headline config at its full size: forward bit-exact, grad_X bit-exact,
