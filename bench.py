@@ -33,6 +33,24 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+# Memory-side float-atomic ceiling of one MI355X, measured with a synthetic kernel that issues the
+# atomic forward's adds alone (64 consecutive elements per wave instruction): about 20.7 G 64-byte
+# line requests per second, fp32 and packed bf16 alike.
+ATOMIC_CEILING_LINES_PER_S = 20.7e9
+
+
+def _atomic_rate(wl, mode, us):
+    """Request rate of an atomic-mode forward call (its fmoe_combine_fwd span of ``us``), against
+    the measured atomic ceiling.  Each element add is one lane of a 64-lane instruction: fp32 adds
+    (mode atomic, or any fp32 target) make N*D*4/64 line requests, packed 16-bit pairs N*D*2/64."""
+    import torch
+
+    out_bytes = 4 if (mode == "atomic" or wl.dtype == torch.float32) else 2
+    lines = wl.N * wl.D * out_bytes / 64
+    rate = lines / (us * 1e-6)
+    return {"atomic_requests_per_launch": int(lines), "atomic_requests_per_s": round(rate / 1e9, 2),
+            "atomic_ceiling_frac": round(rate / ATOMIC_CEILING_LINES_PER_S, 3),
+            "note": "G 64-byte line requests/s; ceiling 20.7 G/s measured with a synthetic kernel"}
 METRIC = "combine fwd+bwd GB/s & % HBM peak at D=16384,E=256,top-8 bf16; latency ms"
 
 
@@ -479,6 +497,8 @@ def _config_line(name, mode, steps, warmup, dev):
     }
     if repeat is not None:
         res["repeatability"] = repeat
+    if mode != "det" and "fwd_atomic" in kernels:
+        res["atomic"] = _atomic_rate(wl, mode, kernels["fwd_atomic"]["avg_us"])
     del idx, w, xs, grad_out, step, direct_step
     torch.cuda.empty_cache()
     return res
@@ -728,6 +748,8 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if args.path == "combine" and args.mode != "det" and "fwd_atomic" in kernels:
+        res["atomic"] = _atomic_rate(wl, args.mode, kernels["fwd_atomic"]["avg_us"])
     if not args.no_standard:
         res["verify"] = verify()
         std_step, what = std()
