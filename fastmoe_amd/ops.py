@@ -34,6 +34,7 @@ Differences from the reference, each deliberate:
 """
 from __future__ import annotations
 
+import array
 import contextlib
 import ctypes
 import os
@@ -195,8 +196,11 @@ def _explain_bad_expert(expert_tensors, dtype, device, hidden) -> None:
 
 
 def _host_table(values) -> ctypes.Array:
-    """int64 host array for the C ABI."""
-    return (ctypes.c_int64 * len(values))(*values)
+    """int64 host array for the C ABI: a ctypes view of an ``array.array``, which converts a list
+    of ints about three times faster than the ctypes array constructor (the view keeps the
+    buffer alive)."""
+    buf = array.array("q", values)
+    return (ctypes.c_int64 * len(buf)).from_buffer(buf)
 
 
 def _meta_arrays(E: int, dev, plan_bytes: int = 0):
