@@ -158,9 +158,9 @@ FMOE_API int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d
  * fmoe_build_metadata followed by fmoe_build_plan on the same experts, in one call (no counterpart
  * in the reference, which builds metadata per call in prepare_grouped_metadata, ops.py:200-271,
  * and needs no inverse).  Outputs and workspace exactly as those two calls; num_rows is the sum
- * of host_rows.  With at most 256 experts and the one-launch plan's limits (N <= 2^20, T < 2^20)
- * a single kernel launch writes both, the (address, rows) table riding in its arguments;
- * otherwise it makes the two calls.
+ * of host_rows.  With at most 256 experts the plan's own kernels also write the metadata, the
+ * (address, rows) table riding in their arguments: one launch up to 2^17 rows, two beyond (up to
+ * 2^22 tokens); otherwise it makes the two calls.
  */
 FMOE_API int fmoe_build_metadata_and_plan(const int64_t* host_ptrs, const int64_t* host_rows,
                                  int64_t num_experts, int64_t* d_ptr_table,
@@ -222,8 +222,9 @@ FMOE_API int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, int
  *                             be NULL.
  * out        : [T, D] with row stride out_row_stride (elements) and unit column stride.
  * accumulate : 1 = add into the existing contents of out (the reference's in-place contract,
- *              ops.py:389-390); 0 = overwrite (rows of tokens without routed rows become 0; the
- *              atomic modes clear out first with a fill kernel).
+ *              ops.py:389-390); 0 = overwrite (rows of tokens without routed rows become 0:
+ *              FMOE_MODE_ATOMIC with a 16-bit out starts its fp32 accumulator from zeros, the
+ *              other atomic cases clear out first with a fill kernel).
  * x_dtype    : dtype of every expert buffer; out_dtype: dtype of out.
  * d_workspace, workspace_bytes : device memory the caller owns, at least
  *              fmoe_combine_fwd_workspace_bytes(mode, T, D, out_dtype) bytes, 16-byte aligned
