@@ -20,8 +20,8 @@ BUILD_DIR = PKG / "_build"
 LIB_NAME = "libfastmoe_amd.so"
 LIB_PATH = PKG / LIB_NAME
 
-HIP_SOURCES = ["metadata.hip", "plan.hip", "plan_bucket.hip", "combine_fwd.hip", "combine_bwd.hip",
-               "permute.hip", "noalloc.hip"]
+HIP_SOURCES = ["metadata.hip", "plan.hip", "plan_bucket.hip", "plan_radix.hip", "combine_fwd.hip",
+               "combine_bwd.hip", "permute.hip", "noalloc.hip"]
 HOST_SOURCES = ["abi.cpp"]
 
 ARCH = "gfx950"

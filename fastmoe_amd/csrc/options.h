@@ -10,7 +10,7 @@ namespace fmoe_host {
 // when the library loads, else from the measured-best default; launches read the table, not the
 // environment.
 enum Opt {
-  kOptPlan = 0,      // "plan": 0 automatic, 1 three launches, 2 bucketed, 3 one launch
+  kOptPlan = 0,      // "plan": 0 automatic, 1 radix, 2 bucketed, 3 one launch
   kOptBwdFused,      // "bwd_fused": 1 = both gradients in one backward pass
   kOptGwStaged,      // "gw_staged": 0 = grad_w pass reads grad_out per wave instead of via LDS
   kOptForceScalar,   // "force_scalar": 1 = element-wise (unvectorised) kernels

@@ -1,5 +1,6 @@
-// Plan internals shared by the plan builders (plan.hip, plan_bucket.hip): the workspace layout,
-// the bucketed plan's geometry and the expert-table sources.
+// Plan internals shared by the plan builders (plan.hip, plan_bucket.hip, plan_radix.hip): the
+// workspace layout, the bucketed and radix plans' geometry, block reductions and the expert-table
+// sources.
 #pragma once
 
 #include <algorithm>
@@ -27,7 +28,7 @@ struct PlanGeom {
   int G1;      // slices (>= 1)
   int shift;   // log2(bins per bucket)
   int nbk;     // buckets
-  bool ok;     // within the bucketed plan's limits (else the three-launch plan)
+  bool ok;     // within the bucketed plan's limits (else the radix plan)
 };
 
 __host__ __device__ inline PlanGeom plan_geom(int64_t N, int64_t T) {
@@ -49,16 +50,47 @@ __host__ __device__ inline PlanGeom plan_geom(int64_t N, int64_t T) {
   return g;
 }
 
+// ---- radix plan geometry ----------------------------------------------------------------------
+// Beyond the bucketed plan's limits: a stable least-significant-digit radix sort of the rows by
+// token bin (plan_radix.hip), 8-bit digits, in tiles of whole 1024-row chunks -- about
+// kRadixTargetTiles tiles (several workgroups per CU), at most kRadixMaxTiles (so each pass's
+// per-tile digit table stays small).
+constexpr int kRadixThreads = 1024;
+constexpr int kRadixDigits = 256;
+constexpr int kRadixMaxPasses = 4;       // bins T + 1 <= 2^30 need at most 30 bits
+constexpr int64_t kRadixMaxTiles = 4096;
+constexpr int64_t kRadixTargetTiles = 2048;
+
+struct RadixGeom {
+  int passes;    // ceil(bits of T / 8): the largest bin is T (out-of-range rows)
+  int ntiles;    // >= 1
+  int64_t tile;  // rows per tile, a multiple of kRadixThreads
+};
+
+__host__ __device__ inline RadixGeom radix_geom(int64_t N, int64_t T) {
+  RadixGeom r;
+  int bits = 1;
+  while (bits < 62 && (T >> bits) != 0) ++bits;
+  r.passes = (bits + 7) / 8;
+  const int64_t per = kRadixThreads * kRadixTargetTiles;
+  const int64_t chunks = std::max<int64_t>(1, (N + per - 1) / per);
+  r.tile = chunks * kRadixThreads;
+  r.ntiles = (int)std::max<int64_t>(1, (N + r.tile - 1) / r.tile);
+  return r;
+}
+
 // ---- plan workspace layout --------------------------------------------------------------------
 //   status   int32[3] (+ padding)
-//   cursor   int32[T + 1]      fill cursors of the three-launch plan
+//   cursor   int32[T + 1]      the radix plan's per-block maxima of its row_ptr scan
 //   row_ptr  int32[T + 2]
-//   tmp      the three-launch plan's unordered records (N x 16 B), or the bucketed plan's
+//   tmp      the radix plan's two (bin, g) pair buffers (2 x N x int2), or the bucketed plan's
 //            partition (N x int2) followed by its per-slice bucket counts and prefixes
 //            (2 x G1 x nbk int32)
 //   rec      N x 16-byte records
+//   radix    the radix plan's digit totals (kRadixMaxPasses x 256 int32) and per-tile digit
+//            table (256 x ntiles int32)
 struct PlanLayout {
-  int64_t status, cursor, row_ptr, rec_tmp, part, bcnt, bpre, rec, total;
+  int64_t status, cursor, row_ptr, rec_tmp, part, bcnt, bpre, rec, radix_tot, radix_hist, total;
 };
 
 __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
@@ -75,8 +107,50 @@ __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
   L.bpre = L.bcnt + up(tab);
   const int64_t tmp_end = std::max(L.rec_tmp + up(N * 16), L.bpre + up(tab));
   L.rec = tmp_end;
-  L.total = L.rec + up(N * 16);
+  L.radix_tot = L.rec + up(N * 16);
+  L.radix_hist = L.radix_tot + up(kRadixMaxPasses * kRadixDigits * 4);
+  L.total = L.radix_hist + up((int64_t)kRadixDigits * radix_geom(N, T).ntiles * 4);
   return L;
+}
+
+// ---- 1024-thread block reductions -------------------------------------------------------------
+// Exclusive scan of one int per thread over a 1024-thread block; *total gets the block sum.
+__device__ __forceinline__ int block_exclusive_scan_1024(int v, int* total) {
+  __shared__ int wave_tot[kScanThreads / kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  if (lane == kWave - 1) wave_tot[wv] = incl;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kScanThreads / kWave; ++i) {
+    const int x = wave_tot[i];
+    before += (i < wv) ? x : 0;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + incl - v;
+}
+
+// Max of one int per thread over a 1024-thread block (all threads get it).
+__device__ __forceinline__ int block_max_1024(int v) {
+  __shared__ int wave_max[kScanThreads / kWave];
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) v = max(v, __shfl_xor(v, d, kWave));
+  if ((threadIdx.x & (kWave - 1)) == 0) wave_max[threadIdx.x / kWave] = v;
+  __syncthreads();
+  int m = 0;
+#pragma unroll
+  for (int i = 0; i < kScanThreads / kWave; ++i) m = max(m, wave_max[i]);
+  __syncthreads();
+  return m;
 }
 
 // ---- where a plan builder gets the expert table from --------------------------------------------
@@ -162,4 +236,12 @@ int launch_bucketed(const fmoe::TokMetaGlobal* gmeta, const fmoe::TokMetaArgs* a
                     int64_t N, int64_t T, int64_t E, int64_t row_bytes, void* d_workspace,
                     bool bare, int32_t* d_rows_bare, int32_t* d_row_ptr_bare, hipStream_t s,
                     const char* who);
+
+// Launcher of the radix plan (plan_radix.hip): row_ptr (d_row_ptr), the status words and the
+// records (gmeta) or, bare, the row numbers (d_rows_bare), in 3 + 3 x passes launches (two more
+// when T + 2 exceeds 16384 bins).
+int launch_radix(const fmoe::TokMetaGlobal* gmeta, const void* d_indices, int idx_dtype,
+                 const void* d_weights, int w_dtype, int64_t N, int64_t T, int64_t E,
+                 int64_t row_bytes, void* d_workspace, int32_t* d_row_ptr, bool bare,
+                 int32_t* d_rows_bare, hipStream_t s, const char* who);
 }  // namespace fmoe_plan

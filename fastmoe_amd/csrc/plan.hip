@@ -9,242 +9,24 @@
 //   rec[N]          : 16-byte records {source row address, fp32 gate, g}, ascending g in every
 //                     segment
 //
-// Three builders, each linear in N + T except where noted:
+// Three builders, each linear in N + T and each writing every segment in ascending g:
 //   * one launch (k_plan_tok), up to kTokMaxRows rows: token-sliced workgroups that each stream
 //     all of idx and fill their own segments stably (below);
 //   * two launches (plan_bucket.hip), larger N: partition the rows by token bucket, then order
 //     each bucket with one wave;
-//   * three launches, beyond 2^22 tokens: count + scan (one 1024-thread workgroup histograms idx
-//     in LDS, or zero / global-atomic count / one-block scan for larger T), a fill of one thread
-//     per row with atomic cursors (arbitrary order within a segment), and an ordering pass over
-//     segments longer than 64 rows, quadratic in their length (the consumers order shorter
-//     segments in registers).
+//   * the radix plan (plan_radix.hip), beyond 2^22 tokens: count + scan (one 1024-thread
+//     workgroup histograms idx in LDS, or zero / global-atomic count / one-block scan for larger
+//     T) for row_ptr and the status words, then a stable LSD radix sort of the rows by token bin.
 //
-// fmoe_invert_scatter_index writes bare row numbers instead of records (two launches, or the
-// three-launch fallback).
+// fmoe_invert_scatter_index writes bare row numbers instead of records (the bucketed or the radix
+// plan).
 #include <algorithm>
 
 #include "plan.h"
 
 namespace fmoe {
 
-constexpr int kLdsTokens = 33792;  // 132 KiB of LDS histogram (gfx950: 160 KiB per workgroup)
-
-// Exclusive scan of one int per thread over a 1024-thread block; *total gets the block sum.
-__device__ int block_exclusive_scan_1024(int v, int* total) {
-  __shared__ int wave_tot[kScanThreads / kWave];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wv = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-  if (lane == kWave - 1) wave_tot[wv] = incl;
-  __syncthreads();
-  int before = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < kScanThreads / kWave; ++i) {
-    const int x = wave_tot[i];
-    before += (i < wv) ? x : 0;
-    tot += x;
-  }
-  __syncthreads();
-  *total = tot;
-  return before + incl - v;
-}
-
-// Max of one int per thread over a 1024-thread block (all threads get it).
-__device__ int block_max_1024(int v) {
-  __shared__ int wave_max[kScanThreads / kWave];
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) v = max(v, __shfl_xor(v, d, kWave));
-  if ((threadIdx.x & (kWave - 1)) == 0) wave_max[threadIdx.x / kWave] = v;
-  __syncthreads();
-  int m = 0;
-#pragma unroll
-  for (int i = 0; i < kScanThreads / kWave; ++i) m = max(m, wave_max[i]);
-  __syncthreads();
-  return m;
-}
-
-// Histogram + scan in LDS: one block.  bins = T + 1 <= kLdsTokens.  Index loads go through a
-// buffer descriptor sized to the array, so a batch of loads is issued unconditionally (lanes past
-// N read 0 and are masked at the atomic) and stays in flight together.
-template <typename TI>
-__global__ __launch_bounds__(kScanThreads) void k_plan_count_scan_lds(
-    const TI* __restrict__ idx, int64_t N, int64_t T, int32_t* __restrict__ cursor,
-    int32_t* __restrict__ row_ptr, int32_t* __restrict__ status) {
-  __shared__ int hist[kLdsTokens];
-  const int nb = (int)T + 1;
-  for (int i = threadIdx.x; i < nb; i += kScanThreads) hist[i] = 0;
-  __syncthreads();
-  const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));
-  constexpr int kBatch = 16;
-  for (int64_t base = 0; base < N; base += (int64_t)kScanThreads * kBatch) {
-    TI v[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const uint32_t g = (uint32_t)(base + (int64_t)i * kScanThreads + threadIdx.x);
-      v[i] = __builtin_bit_cast(
-          TI, Raw<sizeof(TI)>::template ld<kCPolCached>(ri, g * (uint32_t)sizeof(TI)));
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int64_t g = base + (int64_t)i * kScanThreads + threadIdx.x;
-      const int64_t t = (int64_t)v[i];
-      if (g < N) atomicAdd(&hist[(t >= 0 && t < T) ? (int)t : (int)T], 1);
-    }
-  }
-  __syncthreads();
-  // Scan: each thread owns `per` consecutive bins; the prefixes go back into LDS and are copied
-  // out with coalesced stores (consecutive threads, consecutive bins).
-  const int per = (nb + kScanThreads - 1) / kScanThreads;
-  const int b0 = min(nb, (int)threadIdx.x * per);
-  const int b1 = min(nb, b0 + per);
-  const int invalid = hist[T];  // read before the scan's barrier; bin T is rewritten after it
-  int local = 0, longest = 0;
-  for (int b = b0; b < b1; ++b) {
-    local += hist[b];
-    if (b < nb - 1) longest = max(longest, hist[b]);
-  }
-  int total;
-  int run = block_exclusive_scan_1024(local, &total);
-  for (int b = b0; b < b1; ++b) {
-    const int c = hist[b];
-    hist[b] = run;
-    run += c;
-  }
-  // longest token segment (the out-of-range segment T is never ordered); the reduction's barriers
-  // also publish the prefixes written above
-  longest = block_max_1024(longest);
-  for (int b = threadIdx.x; b < nb; b += kScanThreads) {
-    const int v = hist[b];
-    row_ptr[b] = v;
-    cursor[b] = v;
-  }
-  if (threadIdx.x == 0) {
-    row_ptr[nb] = total;
-    status[kStatusInvalid] = invalid;
-    status[kStatusMisaligned] = 0;
-    status[kStatusLongest] = longest;
-  }
-}
-
-// ---- fallback for T + 1 > kLdsTokens ----------------------------------------------------------
-__global__ __launch_bounds__(kGroup) void k_plan_zero(int32_t* __restrict__ p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * kGroup + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
-__global__ __launch_bounds__(kGroup) void k_plan_count_global(const void* __restrict__ idx,
-                                                              int idx_dtype, int64_t N, int64_t T,
-                                                              int32_t* __restrict__ cnt) {
-  const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
-  if (g >= N) return;
-  const int64_t t = load_index(idx, idx_dtype, g);
-  atomicAdd(&cnt[(t >= 0 && t < T) ? t : T], 1);
-}
-
-// In-place: cnt[b] (counts) becomes the cursor (= row_ptr[b]).
-__global__ __launch_bounds__(kScanThreads) void k_plan_scan_global(int32_t* __restrict__ cnt,
-                                                                   int64_t T,
-                                                                   int32_t* __restrict__ row_ptr,
-                                                                   int32_t* __restrict__ status) {
-  const int64_t nb = T + 1;
-  constexpr int kPer = 16;
-  int carry = 0;
-  if (threadIdx.x == 0) {
-    status[kStatusInvalid] = cnt[T];
-    status[kStatusMisaligned] = 0;
-  }
-  __syncthreads();
-  int longest = 0;
-  for (int64_t base = 0; base < nb; base += (int64_t)kScanThreads * kPer) {
-    const int64_t b0 = base + (int64_t)threadIdx.x * kPer;
-    int v[kPer];
-    int local = 0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      v[i] = (b0 + i < nb) ? cnt[b0 + i] : 0;
-      local += v[i];
-      if (b0 + i < T) longest = max(longest, v[i]);
-    }
-    int total;
-    int run = carry + block_exclusive_scan_1024(local, &total);
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      if (b0 + i < nb) {
-        row_ptr[b0 + i] = run;
-        cnt[b0 + i] = run;
-      }
-      run += v[i];
-    }
-    carry += total;
-  }
-  longest = block_max_1024(longest);
-  if (threadIdx.x == 0) {
-    row_ptr[nb] = carry;
-    status[kStatusLongest] = longest;
-  }
-}
-
-// ---- fill -----------------------------------------------------------------------------------
 constexpr int kLdsExperts = 4096;  // expert offsets staged in LDS for the row -> expert search
-
-template <typename TI, typename TW>
-__global__ __launch_bounds__(kGroup) void k_plan_fill(
-    const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T,
-    const int64_t* __restrict__ ptr_table, const int64_t* __restrict__ offsets, int64_t E,
-    int64_t row_bytes, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ cursor,
-    Rec* __restrict__ rec_tmp, Rec* __restrict__ rec, int32_t* __restrict__ status) {
-  __shared__ int64_t off_lds[kLdsExperts + 1];
-  const bool lds_off = E <= kLdsExperts;
-  if (lds_off)
-    for (int i = threadIdx.x; i <= E; i += kGroup) off_lds[i] = offsets[i];
-  __syncthreads();
-  const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
-  if (g < N) {
-    const int64_t t = (int64_t)idx[g];
-    const int64_t b = (t >= 0 && t < T) ? t : T;
-    const int pos = atomicAdd(&cursor[b], 1);
-    const bool long_seg = b < T && row_ptr[b + 1] - row_ptr[b] > kWave;
-    const int64_t e = expert_of_row(lds_off ? off_lds : offsets, E, g);
-    Rec r;
-    r.src = (uint64_t)ptr_table[e] + (uint64_t)((g - (lds_off ? off_lds[e] : offsets[e])) * row_bytes);
-    r.w = ld1(w + g);
-    r.g = (int32_t)g;
-    (long_seg ? rec_tmp : rec)[pos] = r;
-    if (r.src & 15) atomicOr(&status[kStatusMisaligned], 1);
-  }
-}
-
-// Launched after the fill; exits at once unless some segment is longer than one wave (never for
-// top-k routing: the scan recorded the longest segment).  Otherwise each wave takes token
-// segments in turn (a small grid strides over them, so the early exit costs little dispatch).
-constexpr int kSortGroups = 64;
-
-__global__ __launch_bounds__(kGroup) void k_plan_sort_long(const int32_t* __restrict__ row_ptr,
-                                                           int64_t T,
-                                                           const int32_t* __restrict__ status,
-                                                           const Rec* __restrict__ scratch,
-                                                           Rec* __restrict__ rec) {
-  if (status[kStatusLongest] <= kWave) return;
-  const int lane = threadIdx.x & (kWave - 1);
-  for (int64_t b = (int64_t)blockIdx.x * kWavesPerGroup + uniform(threadIdx.x / kWave); b < T;
-       b += (int64_t)gridDim.x * kWavesPerGroup) {
-    const int beg = row_ptr[b];
-    const int c = row_ptr[b + 1] - beg;
-    if (c <= kWave) continue;
-    for (int i = lane; i < c; i += kWave) {
-      const Rec r = scratch[beg + i];
-      int rank = 0;
-      for (int m = 0; m < c; ++m) rank += (scratch[beg + m].g < r.g) ? 1 : 0;
-      rec[beg + rank] = r;
-    }
-  }
-}
 
 // ---- one-launch plan: token-sliced, stable --------------------------------------------------
 // P workgroups of 16 waves; workgroup p owns the token bins [p * bins, (p + 1) * bins) of the T + 1
@@ -565,47 +347,6 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   }
 }
 
-// ---- the bare CSR inverse (fmoe_invert_scatter_index) ---------------------------------------
-// Same count + scan as the plan.  The fill writes bare row numbers; then one wave per segment
-// writes its rows in ascending order.  Row numbers are distinct, so a row's place in its segment
-// is the count of smaller row numbers there.
-template <typename TI>
-__global__ __launch_bounds__(kGroup) void k_invert_fill(const TI* __restrict__ idx, int64_t N,
-                                                        int64_t T, int32_t* __restrict__ cursor,
-                                                        int32_t* __restrict__ tmp) {
-  const int64_t g = (int64_t)blockIdx.x * kGroup + threadIdx.x;
-  if (g >= N) return;
-  const int64_t t = (int64_t)idx[g];
-  tmp[atomicAdd(&cursor[(t >= 0 && t < T) ? t : T], 1)] = (int32_t)g;
-}
-
-// Segments b in [0, T] (b == T: out-of-range rows), one wave each, grid-strided.  A segment of up
-// to 64 rows is ranked in registers; a longer one from memory, quadratic in its length.
-__global__ __launch_bounds__(kGroup) void k_invert_order(const int32_t* __restrict__ row_ptr,
-                                                         int64_t T,
-                                                         const int32_t* __restrict__ tmp,
-                                                         int32_t* __restrict__ rows) {
-  const int lane = threadIdx.x & (kWave - 1);
-  for (int64_t b = (int64_t)blockIdx.x * kWavesPerGroup + uniform(threadIdx.x / kWave); b <= T;
-       b += (int64_t)gridDim.x * kWavesPerGroup) {
-    const int beg = row_ptr[b];
-    const int c = row_ptr[b + 1] - beg;
-    if (c <= kWave) {
-      const int v = lane < c ? tmp[beg + lane] : 0x7fffffff;
-      int rank = 0;
-      for (int m = 0; m < c; ++m) rank += (__shfl(v, m, kWave) < v) ? 1 : 0;
-      if (lane < c) rows[beg + rank] = v;
-    } else {
-      for (int i = lane; i < c; i += kWave) {
-        const int v = tmp[beg + i];
-        int rank = 0;
-        for (int m = 0; m < c; ++m) rank += (tmp[beg + m] < v) ? 1 : 0;
-        rows[beg + rank] = v;
-      }
-    }
-  }
-}
-
 // ---- plan of a combine fed by the dispatch permutation -------------------------------------
 // fmoe_permute_build already knows every token's rows: slot t * k + j sits at packed row
 // slot_pos[t * k + j].  When every slot is a row of the combine (N == T * k), token t's segment
@@ -693,33 +434,6 @@ __global__ __launch_bounds__(kGroup) void k_plan_from_slots(
 
 namespace {
 
-// Count + scan of the scatter index into row_ptr[T + 2] and cursor[T + 1] (= row_ptr[0..T]).
-int launch_count_scan(const void* d_indices, int idx_dtype, int64_t N, int64_t T, int32_t* cursor,
-                      int32_t* row_ptr, int32_t* status, hipStream_t s, const char* who) {
-  using namespace fmoe;
-  const int64_t nb = T + 1;
-  if (nb <= kLdsTokens && N < (int64_t(1) << 27)) {
-    if (idx_dtype == FMOE_I64)
-      hipLaunchKernelGGL(k_plan_count_scan_lds<int64_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int64_t*>(d_indices), N, T, cursor, row_ptr, status);
-    else
-      hipLaunchKernelGGL(k_plan_count_scan_lds<int32_t>, dim3(1), dim3(kScanThreads), 0, s,
-                         static_cast<const int32_t*>(d_indices), N, T, cursor, row_ptr, status);
-    return fmoe_host::check_launch(who);
-  }
-  hipLaunchKernelGGL(k_plan_zero, dim3((unsigned)((nb + kGroup - 1) / kGroup)), dim3(kGroup), 0,
-                     s, cursor, nb);
-  if (int rc = fmoe_host::check_launch(who)) return rc;
-  if (N > 0) {
-    hipLaunchKernelGGL(k_plan_count_global, dim3((unsigned)((N + kGroup - 1) / kGroup)),
-                       dim3(kGroup), 0, s, d_indices, idx_dtype, N, T, cursor);
-    if (int rc = fmoe_host::check_launch(who)) return rc;
-  }
-  hipLaunchKernelGGL(k_plan_scan_global, dim3(1), dim3(kScanThreads), 0, s, cursor, T, row_ptr,
-                     status);
-  return fmoe_host::check_launch(who);
-}
-
 // Grid of the one-launch plan, or false when its limits do not hold (row count aside: the caller
 // weighs N).
 bool tok_grid(int64_t N, int64_t T, int64_t E, int64_t* groups_out, int64_t* bins_out) {
@@ -757,18 +471,28 @@ int launch_plan_tok(const Meta& meta, const void* d_indices, int idx_dtype, cons
   return fmoe_host::check_launch("fmoe_build_plan(one launch)");
 }
 
-// Which plan builds the records: the stable one-launch plan within its limits, else the bucketed
-// plan, else the three launches.  Option "plan": 0 automatic, 1 three launches, 2 bucketed,
-// 3 one launch (each where its limits hold; the next in that order otherwise).
-enum PlanPath { kPathTok, kPathBucketed, kPathSplit };
+// Which plan builds the records by default: when the tokens average kRadixRowsPerToken rows or
+// more, the radix plan, whose cost does not depend on how the rows spread over the tokens (the
+// bucketed plan orders each bucket with one wave, about 25 ns per row, so one hot token costs it
+// milliseconds, and the one-launch plan has at most T + 1 workgroups); else the stable one-launch
+// plan up to kTokMaxRows rows, then the bucketed plan, then the radix plan, each where its limits
+// hold.  Top-k routing (k <= 64 rows per token) never takes the radix plan.  Option "plan":
+// 0 automatic, 1 radix, 2 bucketed, 3 one launch (each where its limits hold; the next in that
+// order otherwise).
+enum PlanPath { kPathTok, kPathBucketed, kPathRadix };
+constexpr int64_t kRadixRowsPerToken = 64;
+bool long_segments(int64_t N, int64_t T) { return N >= kRadixRowsPerToken * (T + 1); }
+bool bucketed_by_default(int64_t N, int64_t T) {
+  return fmoe::plan_geom(N, T).ok && !long_segments(N, T);
+}
 PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bins) {
   const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
   const bool tok = tok_grid(N, T, E, groups, bins);
   const bool bucketed = fmoe::plan_geom(N, T).ok;
-  if (algo == 1) return kPathSplit;
-  if (algo == 2) return bucketed ? kPathBucketed : kPathSplit;
-  if (tok && (algo == 3 || N <= fmoe::kTokMaxRows)) return kPathTok;
-  return bucketed ? kPathBucketed : kPathSplit;
+  if (algo == 1) return kPathRadix;
+  if (algo == 2) return bucketed ? kPathBucketed : kPathRadix;
+  if (tok && (algo == 3 || (N <= fmoe::kTokMaxRows && !long_segments(N, T)))) return kPathTok;
+  return bucketed_by_default(N, T) ? kPathBucketed : kPathRadix;
 }
 
 }  // namespace
@@ -812,13 +536,11 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   const PlanLayout L = plan_layout(N, T);
   char* ws = static_cast<char*>(d_workspace);
   int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
-  int32_t* cursor = reinterpret_cast<int32_t*>(ws + L.cursor);
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
-  Rec* rec_tmp = reinterpret_cast<Rec*>(ws + L.rec_tmp);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
 
-  // The stable one-launch plan, the bucketed plan or the three launches (pick_plan; tests compare
-  // the paths through the "plan" option).
+  // The stable one-launch plan, the bucketed plan or the radix plan (pick_plan; tests compare the
+  // paths through the "plan" option).
   const TokMetaGlobal meta{d_ptr_table, d_offsets};
   int64_t groups = 0, bins = 0;
   const PlanPath path = pick_plan(N, T, E, &groups, &bins);
@@ -830,30 +552,9 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
                                       T, E, row_bytes, d_workspace, false, nullptr, nullptr, s,
                                       "fmoe_build_plan");
 
-  if (int rc = launch_count_scan(d_indices, idx_dtype, N, T, cursor, row_ptr, status, s,
-                                 "fmoe_build_plan"))
-    return rc;
-  if (N == 0) return FMOE_OK;
-  const dim3 grid((unsigned)((N + kGroup - 1) / kGroup));
-#define FMOE_FILL(TI, TW)                                                                          \
-  hipLaunchKernelGGL((k_plan_fill<TI, TW>), grid, dim3(kGroup), 0, s,                              \
-                     static_cast<const TI*>(d_indices), static_cast<const TW*>(d_weights), N, T,   \
-                     d_ptr_table, d_offsets, E, row_bytes, row_ptr, cursor, rec_tmp, rec, status)
-  if (idx_dtype == FMOE_I64) {
-    if (w_dtype == FMOE_F32) FMOE_FILL(int64_t, float);
-    else if (w_dtype == FMOE_BF16) FMOE_FILL(int64_t, bf16_t);
-    else FMOE_FILL(int64_t, f16_t);
-  } else {
-    if (w_dtype == FMOE_F32) FMOE_FILL(int32_t, float);
-    else if (w_dtype == FMOE_BF16) FMOE_FILL(int32_t, bf16_t);
-    else FMOE_FILL(int32_t, f16_t);
-  }
-#undef FMOE_FILL
-  if (int rc = fmoe_host::check_launch("fmoe_build_plan(fill)")) return rc;
-  const int64_t sort_groups = std::min<int64_t>((T + kWavesPerGroup - 1) / kWavesPerGroup, kSortGroups);
-  hipLaunchKernelGGL(k_plan_sort_long, dim3((unsigned)sort_groups), dim3(kGroup), 0, s, row_ptr, T,
-                     status, rec_tmp, rec);
-  return fmoe_host::check_launch("fmoe_build_plan(sort)");
+  return fmoe_plan::launch_radix(&meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E,
+                                 row_bytes, d_workspace, row_ptr, false, nullptr, s,
+                                 "fmoe_build_plan");
 }
 
 extern "C" int fmoe_build_metadata_and_plan(
@@ -876,8 +577,8 @@ extern "C" int fmoe_build_metadata_and_plan(
   const bool small_table = E <= kMetaChunk;
   int64_t groups = 0, bins = 0;
   const bool sizes_ok = T >= 1 && T < (int64_t(1) << 30) && N < (int64_t(1) << 31);
-  const PlanPath path = sizes_ok ? pick_plan(N, T, E, &groups, &bins) : kPathSplit;
-  if (!small_table || path == kPathSplit) {
+  const PlanPath path = sizes_ok ? pick_plan(N, T, E, &groups, &bins) : kPathRadix;
+  if (!small_table || path == kPathRadix) {
     // the two calls (each validates its own arguments)
     if (int rc = fmoe_build_metadata(host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes,
                                      d_offsets, d_max_rows, stream))
@@ -1052,29 +753,13 @@ extern "C" int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, i
   FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
                "fmoe_invert_scatter_index: workspace not 256B-aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (fmoe_host::opt(fmoe_host::kOptPlan) != 1 && plan_geom(N, T).ok)  // else three launches
+  // the bucketed plan (option plan=2, or by default as for the records), else the radix plan
+  const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
+  if ((algo == 2 && plan_geom(N, T).ok) || ((algo == 0 || algo == 3) && bucketed_by_default(N, T)))
     return fmoe_plan::launch_bucketed(nullptr, nullptr, d_indices, idx_dtype, nullptr, FMOE_F32, N,
                                       T, 0, 0, d_workspace, true, d_rows, d_row_ptr, s,
                                       "fmoe_invert_scatter_index");
-  const PlanLayout L = plan_layout(N, T);
-  char* ws = static_cast<char*>(d_workspace);
-  int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
-  int32_t* cursor = reinterpret_cast<int32_t*>(ws + L.cursor);
-  int32_t* tmp = reinterpret_cast<int32_t*>(ws + L.rec_tmp);
-  if (int rc = launch_count_scan(d_indices, idx_dtype, N, T, cursor, d_row_ptr, status, s,
-                                 "fmoe_invert_scatter_index"))
-    return rc;
-  if (N == 0) return FMOE_OK;
-  const dim3 grid((unsigned)((N + kGroup - 1) / kGroup));
-  if (idx_dtype == FMOE_I64)
-    hipLaunchKernelGGL(k_invert_fill<int64_t>, grid, dim3(kGroup), 0, s,
-                       static_cast<const int64_t*>(d_indices), N, T, cursor, tmp);
-  else
-    hipLaunchKernelGGL(k_invert_fill<int32_t>, grid, dim3(kGroup), 0, s,
-                       static_cast<const int32_t*>(d_indices), N, T, cursor, tmp);
-  if (int rc = fmoe_host::check_launch("fmoe_invert_scatter_index(fill)")) return rc;
-  const int64_t groups = std::min<int64_t>((T + 1 + kWavesPerGroup - 1) / kWavesPerGroup, 2048);
-  hipLaunchKernelGGL(k_invert_order, dim3((unsigned)groups), dim3(kGroup), 0, s, d_row_ptr, T, tmp,
-                     d_rows);
-  return fmoe_host::check_launch("fmoe_invert_scatter_index(order)");
+  return fmoe_plan::launch_radix(nullptr, d_indices, idx_dtype, nullptr, FMOE_F32, N, T, 0, 0,
+                                 d_workspace, d_row_ptr, true, d_rows, s,
+                                 "fmoe_invert_scatter_index");
 }

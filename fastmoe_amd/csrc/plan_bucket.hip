@@ -26,31 +26,7 @@ constexpr int kBucketWaves = 4;
 constexpr int kBucketThreads = kBucketWaves * kWave;
 constexpr int kBucketCache = 8;      // chunks of 64 rows a k_plan_bucket wave keeps in registers
 constexpr int kLdsMetaExperts = 4096;  // expert tables staged in LDS up to this many experts
-
-// Exclusive scan of one int per thread over a 1024-thread block; *total gets the block sum.
-__device__ int part_exclusive_scan(int v, int* total) {
-  __shared__ int wave_tot[kPartWaves];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wv = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-  if (lane == kWave - 1) wave_tot[wv] = incl;
-  __syncthreads();
-  int before = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < kPartWaves; ++i) {
-    const int x = wave_tot[i];
-    before += (i < wv) ? x : 0;
-    tot += x;
-  }
-  __syncthreads();
-  *total = tot;
-  return before + incl - v;
-}
+static_assert(kPartThreads == kScanThreads, "k_plan_part scans with the 1024-thread block scan");
 
 __device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -125,7 +101,7 @@ __global__ __launch_bounds__(kPartThreads) void k_plan_part(
   if (bi < nbk)
     for (int w = 0; w < kPartWaves; ++w) tot += cnt[w * nbk + bi];
   int all;
-  const int pre = part_exclusive_scan(tot, &all);
+  const int pre = block_exclusive_scan_1024(tot, &all);
   if (bi < nbk) {
     int run = pre;
     for (int w = 0; w < kPartWaves; ++w) {

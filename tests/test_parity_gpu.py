@@ -116,7 +116,7 @@ def _set_bwd_variant(kernel_options, variant):
     kernel_options(**_BWD_VARIANTS[variant])
 
 
-_PLAN_PATHS = {"tok": 3, "bucketed": 2, "split": 1}  # values of the "plan" option
+_PLAN_PATHS = {"tok": 3, "bucketed": 2, "radix": 1}  # values of the "plan" option
 
 
 @pytest.mark.parametrize("variant", list(_BWD_VARIANTS))
@@ -496,10 +496,9 @@ def _plan_case(case: str):
                                   "wide_hist"])
 def test_plan_matches_oracle(case, path, kernel_options):
     """row_ptr, the records (source address, gate bits, g) and the status words equal the
-    oracle's inverse, for the one-launch plan, the bucketed plan (two launches) and the split
-    count/fill/order plan.  The first two write every segment in ascending g (the records equal
-    the oracle's stable inverse as they are); the split plan orders segments longer than 64 rows,
-    including when several workgroups each fill a piece of one segment."""
+    oracle's stable inverse, for the one-launch plan, the bucketed plan (two launches) and the
+    radix plan (count + scan, then a stable radix sort by token bin): each writes every segment in
+    ascending g, including when several workgroups each take a piece of one segment."""
     from oracle import cref
 
     kernel_options(plan=_PLAN_PATHS[path])
@@ -517,25 +516,15 @@ def test_plan_matches_oracle(case, path, kernel_options):
     np.testing.assert_array_equal(row_ptr, want_rp)
     g = (rec[:, 1] >> 32).numpy().astype(np.int32)
     seg_len = np.diff(want_rp)
-    for b in range(T):  # long segments are in ascending g
-        if seg_len[b] > 64:
-            assert np.all(np.diff(g[want_rp[b]:want_rp[b + 1]]) > 0), b
     st = ops.plan_status(plan).cpu().numpy()
     misaligned = int((D * experts[0].element_size()) % 16 != 0)
     assert st[0] == 0 and st[1] == misaligned
-    # the longest segment: recorded by the split and bucketed plans; -1 from the one-launch plan
+    # the longest segment: recorded by the radix and bucketed plans; -1 from the one-launch plan
     # (no workgroup sees every segment)
     assert st[2] == (-1 if path == "tok" else seg_len[:T].max())
     if case != "topk512":
         assert seg_len[:T].max() > 64
-    if path != "split":  # stable: every segment already in ascending g
-        np.testing.assert_array_equal(g, want_g)
-    # short segments may be unordered: order each segment by g before comparing
-    order = np.concatenate([np.arange(want_rp[b], want_rp[b + 1])[np.argsort(g[want_rp[b]:want_rp[b + 1]])]
-                            for b in range(T + 1)])
-    rec = rec[torch.from_numpy(order)]
-    g = (rec[:, 1] >> 32).numpy().astype(np.int32)
-    np.testing.assert_array_equal(g, want_g)
+    np.testing.assert_array_equal(g, want_g)  # stable: every segment in ascending g
     wbits = (rec[:, 1] & 0xFFFFFFFF).numpy().astype(np.uint32)
     np.testing.assert_array_equal(wbits, w.numpy()[want_g].view(np.uint32))
     off, _ = cref.metadata(meta.sizes)
@@ -776,7 +765,7 @@ def test_random_inplace_against_oracle():
             assert not bool(big[:, D:].any()), label  # the padding columns are never written
 
 
-@pytest.mark.parametrize("path", ["tok", "bucketed"])
+@pytest.mark.parametrize("path", list(_PLAN_PATHS))
 @pytest.mark.parametrize("T,N", [(1, 1), (1, 5000), (2, 3), (2, 4500), (1, 100_000)])
 def test_plan_few_tokens(T, N, path, kernel_options):
     """One or two tokens: a segment of thousands of rows (several partition slices feeding one
@@ -827,15 +816,16 @@ def _sorted_plan(plan, N, T):
 
 
 @pytest.mark.parametrize("case", ["e256", "e300", "e1", "empty_experts", "long", "i32_bf16w",
-                                  "big_n"])
+                                  "big_n", "big_n_long"])
 def test_metadata_and_plan_in_one_call_equals_two_calls(case):
     """fmoe_build_metadata_and_plan writes exactly what fmoe_build_metadata + fmoe_build_plan
-    write: the plan's own launches for up to 256 experts, the two calls otherwise (300 experts;
-    N > 2^20 rows is within the bucketed plan's limits)."""
+    write: the plan's own launches for up to 256 experts, the two calls otherwise (300 experts,
+    or the radix plan: N > 2^20 rows over 4096 tokens averages 256 rows per token; over 65536
+    tokens the bucketed plan takes them in the one call)."""
     gen = torch.Generator().manual_seed(31)
     D, dtype, idt, wdt = 8, torch.float32, torch.int64, torch.float32
-    if case == "big_n":
-        E, T, N, D = 16, 4096, (1 << 20) + 5, 1
+    if case in ("big_n", "big_n_long"):
+        E, T, N, D = 16, 65536 if case == "big_n" else 4096, (1 << 20) + 5, 1
     else:
         E, T, N = {"e256": (256, 512, 4096), "e300": (300, 512, 4096), "e1": (1, 64, 500),
                    "empty_experts": (40, 100, 700), "long": (8, 40, 3000),
@@ -875,13 +865,16 @@ def test_metadata_and_plan_in_one_call_equals_two_calls(case):
                 assert np.array_equal(graw[rp1[b]:rp1[b + 1]], g[rp1[b]:rp1[b + 1]])
 
 
+@pytest.mark.parametrize("path", ["auto", "radix"])
 @pytest.mark.parametrize("case", ["topk", "long", "one_token", "invalid_i32", "empty", "bigT"])
-def test_invert_scatter_index_matches_oracle(case):
+def test_invert_scatter_index_matches_oracle(case, path, kernel_options):
     """fmoe_invert_scatter_index: row_ptr and the row list equal the oracle's stable inverse
     exactly -- top-k routing, segments longer than 64 rows (one of 3000 rows), out-of-range int32
-    indices, no rows, and T above the LDS histogram (the global count path)."""
+    indices, no rows, and T above the LDS histogram (the global count path) -- through the
+    automatic (bucketed) path and the radix plan."""
     from oracle import cref
 
+    kernel_options(plan=0 if path == "auto" else _PLAN_PATHS["radix"])
     gen = torch.Generator().manual_seed(21)
     if case == "topk":
         _, T, idx, _, _ = _inputs("gigachat")
@@ -959,8 +952,8 @@ def test_many_experts_beyond_the_lds_tables():
 
 @pytest.mark.parametrize("path", list(_PLAN_PATHS))
 def test_large_token_count_plan_paths(path, kernel_options):
-    """T = 40000: the split plan's histogram exceeds its LDS (33792 bins), so it counts and scans
-    in global memory; the bucketed plan groups the 40001 bins into buckets of 64; the one-launch
+    """T = 40000: the radix plan's count exceeds its LDS histogram (33792 bins), so it counts and
+    scans in global memory (and sorts in two passes); the bucketed plan groups the 40001 bins into buckets of 64; the one-launch
     plan spreads them over 255 workgroups."""
     kernel_options(plan=_PLAN_PATHS[path])
     D, T, k = 16, 40000, 2
@@ -970,6 +963,48 @@ def test_large_token_count_plan_paths(path, kernel_options):
     xd, idd, wd = _to_dev(experts, idx, w)
     out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
     want, _, _ = oracle_fwd(experts, idx, w, T, torch.float32)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+def test_plan_beyond_bucketed_token_limit(idx_dtype):
+    """T = 5,000,000 token bins, above the bucketed plan's 2^22: the automatic choice takes the
+    radix plan (three 8-bit passes).  Random rows over all of T, one token with about 89,000 rows
+    (the regression case of linear time: an ordering pass quadratic in the segment length takes
+    minutes there) and out-of-range indices on both sides; the plan (exact stable order, status
+    words), the bare inverse and the forward against the oracle."""
+    from oracle import cref
+
+    gen = torch.Generator().manual_seed(97)
+    T, N, D = 5_000_000, 300_000, 4
+    idx = torch.randint(0, T, (N,), generator=gen)
+    idx[torch.randperm(N, generator=gen)[:100_000]] = 4_321_987
+    idx[::13] = T   # out of range, both sides (about 11% of the rows)
+    idx[5::29] = -3
+    idx = idx.to(idx_dtype)
+    w = torch.rand(N, generator=gen)
+    sizes = [N // 4, N // 2, N - N // 4 - N // 2]
+    experts = [torch.randn(n, D, generator=gen) for n in sizes]
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta, plan = ops.prepare_metadata_and_plan(xd, idd, wd, T)
+    lib = fastmoe_amd._abi.lib()
+    rp = plan[lib.fmoe_plan_row_ptr_offset(N, T):][: 4 * (T + 2)].view(torch.int32).cpu().numpy()
+    rec = plan[lib.fmoe_plan_records_offset(N, T):][: 16 * N].view(torch.int64).view(N, 2).cpu()
+    want_rp, want_g = cref.plan(idx.to(torch.int64).numpy(), T)
+    np.testing.assert_array_equal(rp, want_rp)
+    np.testing.assert_array_equal((rec[:, 1] >> 32).numpy().astype(np.int32), want_g)
+    np.testing.assert_array_equal((rec[:, 1] & 0xFFFFFFFF).numpy().astype(np.uint32),
+                                  w.numpy()[want_g].view(np.uint32))
+    seg = np.diff(want_rp)
+    assert seg[:T].max() > 80_000  # the hot token, less the rows sent out of range below
+    st = ops.plan_status(plan).cpu().numpy()
+    assert int(st[0]) == int(seg[T]) and int(st[1]) == 0 and int(st[2]) == int(seg[:T].max())
+    row_ptr, rows = fastmoe_amd.invert_scatter_index(idd, T)
+    np.testing.assert_array_equal(row_ptr.cpu().numpy(), want_rp)
+    np.testing.assert_array_equal(rows.cpu().numpy(), want_g)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
+    want, _, bad = oracle_fwd(experts, idx.to(torch.int64), w, T, torch.float32)
+    assert bad == seg[T]
     np.testing.assert_array_equal(bits(out), want.view(np.uint32))
 
 

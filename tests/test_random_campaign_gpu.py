@@ -76,7 +76,7 @@ def test_campaign_autograd(kernel_options):
         wdt = [torch.float32, torch.bfloat16][int(rng.integers(2))]
         idt = [torch.int64, torch.int32][int(rng.integers(2))]
         r, fused = rng.random(), bool(rng.random() < 0.25)
-        plan = 1 if r < 0.25 else (2 if r < 0.4 else 0)  # three launches / bucketed / automatic
+        plan = 1 if r < 0.25 else (2 if r < 0.4 else 0)  # radix / bucketed / automatic
         kernel_options(plan=plan, bwd_fused=1 if fused else 0)
         label = (f"autograd case {case}: T={T} N={N} E={E} D={D} {routing} {xdt} {wdt} {idt} "
                  f"plan={plan} fused={fused}")
@@ -147,7 +147,7 @@ def test_campaign_permutation_and_inplace(kernel_options):
             xdt, odt = DTS[int(rng.integers(3))], DTS[int(rng.integers(3))]
             mode = "atomic" if rng.random() < 0.4 else "det"
             r = rng.random()
-            plan = 1 if r < 0.25 else (2 if r < 0.4 else 0)  # three launches / bucketed / auto
+            plan = 1 if r < 0.25 else (2 if r < 0.4 else 0)  # radix / bucketed / auto
             kernel_options(plan=plan)
             sizes = _split(rng, N, E)
             idx = torch.from_numpy(rng.integers(0, T, N))
