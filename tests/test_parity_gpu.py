@@ -923,11 +923,13 @@ def test_metadata_matches_closed_forms():
         assert int(meta.max_rows_device.item()) == max(sizes)
 
 
-def test_many_experts_beyond_the_lds_tables():
+@pytest.mark.parametrize("path", ["auto", "radix"])
+def test_many_experts_beyond_the_lds_tables(path, kernel_options):
     """5000 experts (0-2 rows each): more than the plan's LDS expert tables (4096) and the
     metadata's kernel-argument table (256), so the plan looks experts up in global memory and
-    metadata and plan take separate calls; forward bits, grad_X bits and grad_w against the
-    oracle."""
+    metadata and plan take separate calls -- the automatic (bucketed) plan and the radix plan;
+    forward bits, grad_X bits and grad_w against the oracle."""
+    kernel_options(plan=0 if path == "auto" else _PLAN_PATHS["radix"])
     gen = torch.Generator().manual_seed(41)
     E, T, D = 5000, 700, 24
     sizes = torch.randint(0, 3, (E,), generator=gen).tolist()
@@ -952,9 +954,9 @@ def test_many_experts_beyond_the_lds_tables():
 
 @pytest.mark.parametrize("path", list(_PLAN_PATHS))
 def test_large_token_count_plan_paths(path, kernel_options):
-    """T = 40000: the radix plan's count exceeds its LDS histogram (33792 bins), so it counts and
-    scans in global memory (and sorts in two passes); the bucketed plan groups the 40001 bins into buckets of 64; the one-launch
-    plan spreads them over 255 workgroups."""
+    """T = 40000: the radix plan sorts in two 8-bit passes and scans row_ptr over three blocks of
+    16384 bins; the bucketed plan groups the 40001 bins into buckets of 64; the one-launch plan
+    spreads them over 255 workgroups."""
     kernel_options(plan=_PLAN_PATHS[path])
     D, T, k = 16, 40000, 2
     wl = Workload("bigT", T, D, 16, k, torch.float32, 13, False)
