@@ -234,24 +234,43 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   };
   constexpr int kBatchRows = kTokLoads * kWave * RPL;
   const int lim = min(r1, n_al);
-  if (r0 < lim) {  // wave-uniform
-    u32x4 cur[kTokLoads], nxt[kTokLoads];
-    load_batch(r0, cur);
-    for (int base = r0; base < lim; base += kBatchRows) {
-      // Unconditional: a prefetch under a branch makes the compiler wait for the first of these
-      // loads before it uses `cur` (one wait count must fit both paths), which serialises the
-      // batches on the memory latency.  Past the range the loads return zeros without traffic.
-      load_batch(base + kBatchRows, nxt);
+  // One batch: a batch that ends at or below lim needs no per-row range check.
+  auto count_batch = [&](int base, const u32x4* v) {
+    if (base + kBatchRows <= lim) {  // wave-uniform
 #pragma unroll
       for (int i = 0; i < kTokLoads; ++i) {
         const int g0 = base + (i * kWave + lane) * RPL;
         uint32_t b[RPL];
 #pragma unroll
-        for (int r = 0; r < RPL; ++r) b[r] = bin_at(g0 + r, lim, row_of(cur[i], r));
+        for (int r = 0; r < RPL; ++r) {
+          const int64_t t = (int64_t)row_of(v[i], r);
+          b[r] = (uint64_t)t < (uint64_t)T ? (uint32_t)t : (uint32_t)T;
+        }
         count_vec(g0, b);
       }
+    } else {
 #pragma unroll
-      for (int i = 0; i < kTokLoads; ++i) cur[i] = nxt[i];
+      for (int i = 0; i < kTokLoads; ++i) {
+        const int g0 = base + (i * kWave + lane) * RPL;
+        uint32_t b[RPL];
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) b[r] = bin_at(g0 + r, lim, row_of(v[i], r));
+        count_vec(g0, b);
+      }
+    }
+  };
+  if (r0 < lim) {  // wave-uniform
+    // Two batch buffers used in turn (no register copies, which would make each iteration wait
+    // for the next batch's loads), so one batch is always in flight while the other is counted.
+    // The loads are unconditional: past the range they return zeros without traffic.
+    u32x4 va[kTokLoads], vb[kTokLoads];
+    load_batch(r0, va);
+    for (int base = r0; base < lim; base += 2 * kBatchRows) {
+      load_batch(base + kBatchRows, vb);
+      count_batch(base, va);
+      if (base + kBatchRows >= lim) break;  // wave-uniform
+      load_batch(base + 2 * kBatchRows, va);
+      count_batch(base + kBatchRows, vb);
     }
   }
   if (r1 > n_al && r0 < r1) {  // wave-uniform: the rows past the last whole vector
