@@ -923,6 +923,38 @@ def test_metadata_matches_closed_forms():
         assert int(meta.max_rows_device.item()) == max(sizes)
 
 
+@pytest.mark.parametrize("D", [1, 256])
+@pytest.mark.parametrize("kind", ["sum", "row_broadcast"])
+def test_backward_of_an_expanded_grad_output(kind, D):
+    """grad_output as autograd hands it over from a reduction or a broadcast: ``out.sum()`` gives
+    an expanded all-ones tensor (strides (0, 0)), and a [1, D] row expanded to [T, D] has row
+    stride 0.  grad_X bit-exact and grad_w within 1e-6 of sum|terms| against the oracle."""
+    gen = torch.Generator().manual_seed(71 + D)
+    T, sizes = 40, [30, 0, 50, 20]
+    N = sum(sizes)
+    idx = torch.randint(0, T, (N,), generator=gen)
+    w = torch.rand(N, generator=gen)
+    experts = [torch.randn(n, D, generator=gen).to(torch.bfloat16) for n in sizes]
+    xs = [x.to(DEV).requires_grad_(True) for x in experts]
+    wd = w.to(DEV).requires_grad_(True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx.to(DEV), wd, (T, D))
+    if kind == "sum":
+        grads = torch.autograd.grad(out.sum(), [wd, *xs], allow_unused=True)
+        go = torch.ones(T, D).to(torch.bfloat16)
+    else:
+        row = torch.randn(1, D, generator=gen).to(torch.bfloat16)
+        god = row.to(DEV).expand(T, D)
+        assert god.stride(0) == 0
+        grads = torch.autograd.grad(out, [wd, *xs], god, allow_unused=True)
+        go = row.expand(T, D).contiguous()
+    torch.cuda.synchronize()
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, go)
+    got_gx = np.concatenate([to_np(g) for g, n in zip(grads[1:], sizes) if n])
+    np.testing.assert_array_equal(got_gx, want_gx)
+    scale = abs_dot(experts, idx, go, T)
+    assert np.all(np.abs(grads[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
+
+
 @pytest.mark.parametrize("path", ["auto", "radix"])
 def test_many_experts_beyond_the_lds_tables(path, kernel_options):
     """5000 experts (0-2 rows each): more than the plan's LDS expert tables (4096) and the
