@@ -245,13 +245,15 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const In in, co
 }
 
 // end[skey[i]] = i + 1 where place i is the last of its bin (the next place holds another bin, or
-// i = N - 1): exactly one store per non-empty bin.
+// i = N - 1): exactly one store per non-empty bin.  Bins lie in [0, T]; the check keeps the store
+// inside end[] whatever the buffer holds.
 __global__ __launch_bounds__(kRadixThreads) void k_radix_ends(const int32_t* __restrict__ skey,
-                                                              int64_t N, int32_t* __restrict__ end) {
+                                                              int64_t N, int64_t T,
+                                                              int32_t* __restrict__ end) {
   const int64_t i = (int64_t)blockIdx.x * kRadixThreads + threadIdx.x;
   if (i >= N) return;
   const int k = skey[i];
-  if (i == N - 1 || skey[i + 1] != k) end[k] = (int)(i + 1);
+  if ((uint32_t)k <= (uint32_t)T && (i == N - 1 || skey[i + 1] != k)) end[k] = (int)(i + 1);
 }
 
 // ---- row_ptr: exclusive max-scan of end[] over the T + 2 bins --------------------------------
@@ -434,7 +436,7 @@ int launch_radix(const TokMetaGlobal* gmeta, const void* d_indices, int idx_dtyp
   }
   if (N > 0) {
     hipLaunchKernelGGL(k_radix_ends, dim3((unsigned)((N + kRadixThreads - 1) / kRadixThreads)), block,
-                       0, s, skey, N, d_row_ptr);
+                       0, s, skey, N, T, d_row_ptr);
     if (int rc = fmoe_host::check_launch(who)) return rc;
   }
   if (nblk > 1) {
