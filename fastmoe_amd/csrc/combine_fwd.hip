@@ -444,6 +444,30 @@ static int launch_fwd_u(const FwdArgs& a) {
   return launch_fwd_k<TX, TO, V, U, RB>(a, chunks);
 }
 
+// Tile of the deterministic forward by the average rows per token r = N / T.  A batch issues its
+// R x U loads whether or not its rows exist (the spare slots read an empty range: no traffic, but
+// an issue slot each), so short segments take short batches: r <= 1.5 takes R = 2 (U = 4, with a
+// partly empty last chunk if D needs it, when D holds one chunk of 4 vectors per lane), r <= 3
+// takes R = 4.  Long segments (r >= 7) whose chunk
+// would be 2 vectors per lane take 1 with R = 8.  Measured with HIP events on one MI355X, bf16,
+// against the choice by D alone: T=16384, D=7168: k=1 129 -> 75 us, k=2 146 -> 109 us, k=8 355 ->
+// 349 us (Zipf) and 361 -> 354 us (top-k); D=5120, 3072, 6144 at k=8 about 2 % faster; D=4096 and
+// 16384 at k=2, 6 and 8 unchanged.
+static void pick_det_tile(const FwdArgs& a, int V, int* U, int* R) {
+  *U = pick_u(a.D, V);
+  *R = *U >= 4 ? 4 : 8;
+  if (fmoe_host::opt(fmoe_host::kOptFwdDetU) != 0 || a.N == 0) return;  // U forced: keep R by U
+  if (2 * a.N <= 3 * a.T && a.D >= (int64_t)kWave * V * 4) {  // r <= 1.5, a whole chunk of 4
+    *U = 4;
+    *R = 2;
+  } else if (a.N <= 3 * a.T) {                                  // r <= 3
+    if (*U >= 2) *R = 4;
+  } else if (a.N >= 7 * a.T && *U == 2) {                       // r >= 7
+    *U = 1;
+    *R = 8;
+  }
+}
+
 // Tile shapes (U vectors per lane per row, R rows per batch).  The "fwd_tile" option <U><R> (e.g.
 // 44) overrides the choice for tuning.
 template <typename TX, typename TO, int V>
@@ -456,8 +480,12 @@ static int launch_fwd_v(const FwdArgs& a) {
     int U = tile / 10, R = tile % 10;
     if (!((U == 4 && (R == 4 || R == 2)) || (U == 2 && (R == 8 || R == 4)) ||
           (U == 1 && R == 8))) {
-      U = pick_u(a.D, V);
-      R = U >= 4 ? 4 : 8;
+      if (a.mode == FMOE_MODE_DET) {
+        pick_det_tile(a, V, &U, &R);
+      } else {
+        U = pick_u(a.D, V);
+        R = U >= 4 ? 4 : 8;
+      }
     }
     if (U == 4 && R == 2) return launch_fwd_u<TX, TO, V, 4, 2>(a);
     if (U == 4) return launch_fwd_u<TX, TO, V, 4, 4>(a);

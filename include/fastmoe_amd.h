@@ -102,7 +102,8 @@ FMOE_API const char* fmoe_last_error(void);
  *   "bwd_fused"       [FMOE_BWD_FUSED] 1 = both backward gradients in one pass
  *   "gw_staged"       [FMOE_GW_STAGED] 0 = grad_w pass reads grad_out per wave, not through LDS
  *   "force_scalar"    [FMOE_FORCE_SCALAR] 1 = element-wise instead of 16-byte accesses
- *   "bwd_u", "fwd_tile", "fwd_atomic_tile", "fwd_det_u", "fwd_grid": tile shapes (0 = by D)
+ *   "bwd_u", "fwd_tile", "fwd_atomic_tile", "fwd_det_u", "fwd_grid": tile shapes (0 = by D,
+ *                                      and for "fwd_tile" by the rows per token too)
  *   "plan_groups"     [FMOE_PLAN_GROUPS] workgroups of the one-launch plan (0 = by N and T)
  * fmoe_set_option returns FMOE_EINVAL for an unknown name; *previous (if not NULL) gets the old
  * value.  Not synchronised with launches in flight on other threads.

@@ -923,6 +923,38 @@ def test_metadata_matches_closed_forms():
         assert int(meta.max_rows_device.item()) == max(sizes)
 
 
+@pytest.mark.parametrize("tile", [0, 44, 42, 28, 24, 18])
+def test_fwd_det_every_tile_shape(tile, kernel_options):
+    """The deterministic forward with each tile shape (option fwd_tile <U><R>: U vectors per lane
+    per row, R rows per batch; 0 = the automatic choice by D and the rows per token) is the oracle's
+    result bit for bit: segments of 1, 2 and 8 rows and ragged ones, D that the chunk divides and
+    D that leaves a partial chunk, bf16 and fp32, overwrite and in-place accumulation."""
+    kernel_options(fwd_tile=tile)
+    gen = torch.Generator().manual_seed(400 + tile)
+    for T, D, k, dt in [(300, 7168, 1, torch.bfloat16), (300, 7168, 2, torch.bfloat16),
+                        (200, 3072, 8, torch.bfloat16), (257, 4104, 2, torch.bfloat16),
+                        (150, 2048, 3, torch.float32), (64, 520, 1, torch.float32)]:
+        N = T * k
+        idx = torch.randperm(N, generator=gen) % T  # exactly k rows per token, scattered
+        if k == 3:
+            idx[::5] = torch.randint(0, 7, (len(idx[::5]),), generator=gen)  # ragged
+        w = torch.rand(N, generator=gen)
+        sizes = [N // 3, N - 2 * (N // 3), N // 3]
+        experts = [torch.randn(n, D, generator=gen).to(dt) for n in sizes]
+        xd, idd, wd = _to_dev(experts, idx, w)
+        label = f"tile {tile}: T={T} D={D} k={k} {dt}"
+        out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), mode="det")
+        want, _, _ = oracle_fwd(experts, idx, w, T, dt)
+        np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32
+                                      else want, err_msg=label)
+        init = torch.randn(T, D, generator=gen).to(dt)
+        acc = init.to(DEV)
+        fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D), out=acc, mode="det")
+        want, _, _ = oracle_fwd(experts, idx, w, T, dt, acc_init=init.float().numpy())
+        np.testing.assert_array_equal(bits(acc), want.view(np.uint32) if want.dtype == np.float32
+                                      else want, err_msg=label + " in place")
+
+
 @pytest.mark.parametrize("D", [1, 256])
 @pytest.mark.parametrize("kind", ["sum", "row_broadcast"])
 def test_backward_of_an_expanded_grad_output(kind, D):
