@@ -32,15 +32,16 @@ constexpr int kLdsExperts = 4096;  // expert offsets staged in LDS for the row -
 // P workgroups of 16 waves; workgroup p owns the token bins [p * bins, (p + 1) * bins) of the T + 1
 // (bin T: out-of-range rows), so every segment belongs to exactly one workgroup and the workgroups
 // never communicate.  Every workgroup streams all of idx (from L2 after the first): wave w takes
-// the w-th sixteenth of the rows, in ascending g, one row per lane per load, and
+// the w-th sixteenth of the rows, in ascending g, RPL rows per lane per 16-byte load, and
 //   * counts the rows whose bin lies below its workgroup's range (part of row_ptr of its first bin),
-//   * counts its rows of each of the range's bins in its own LDS row and stashes them (g, bin) in
-//     ascending g.
+//   * stashes its rows of the range (g, bin) in ascending g, then counts the stash per bin into
+//     its own LDS row.
 // The workgroup then scans its bins bin-major and wave-minor, which gives row_ptr and each wave's
 // first place in every bin, and each wave writes the records of its stashed rows: a row goes to its
 // wave's cursor for the bin plus its rank among the lower lanes with the same bin.  Every segment
 // thus comes out in ascending g with no ordering pass, in time linear in N per workgroup.  A wave
-// whose stash overflows (a heavily skewed index) re-streams its own rows in the fill instead.
+// whose stash overflows (a heavily skewed index) re-streams its own rows to count them and again
+// in the fill.
 // Every workgroup reading all of idx makes the total work N * P: beyond kTokMaxRows rows the
 // bucketed plan (plan_bucket.hip) takes over.
 constexpr int kTokWaves = kScanThreads / kWave;        // 16
@@ -136,8 +137,9 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T, int bins,
     const Meta meta, int64_t E, int64_t row_bytes, int32_t* __restrict__ row_ptr,
     Rec* __restrict__ rec, int32_t* __restrict__ status) {
-  __shared__ int cnt[kTokWaves * kTokBins];            // [wave][bin]: counts, then cursors
-  __shared__ int2 stash[kTokWaves * kTokWaveStash];    // per wave: (g, local bin), ascending g
+  __shared__ int cnt[kTokWaves * kTokBins];                 // [wave][bin]: counts, then cursors
+  __shared__ int2 stash[kTokWaves * (kTokWaveStash + 1)];   // per wave: (g, local bin), ascending
+                                                            // g, and a slot for overflowing rows
   __shared__ int off32[kTokExperts + 1];
   __shared__ uint64_t ptr_lds[kTokExperts];
   __shared__ int misaligned;
@@ -146,84 +148,89 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   const int lo = (int)blockIdx.x * bins;  // the host makes every range non-empty
   const int hi = min(nb, lo + bins);
   const int nloc = hi - lo;
+  const bool last = hi == nb;  // this workgroup owns bin T, the out-of-range rows
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  TokMetaRegs<Meta> mreg;
-  mreg.load(meta, ne);  // used after the pass over idx
-  for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) cnt[i] = 0;
-  if (threadIdx.x == 0) misaligned = 0;
-  __syncthreads();
 
   // 1. pass over this wave's rows [r0, r1) in ascending g.  Every workgroup reads all of idx, so
-  //    the pass is bound by the rate at which a CU issues vector loads, not by bytes: the index
-  //    is read with 16-byte loads, RPL consecutive rows per lane (a lane's rows, then the next
-  //    lane's, so the wave still sees its rows in ascending g).  The rows past the last whole
-  //    vector (fewer than RPL) are read one per lane after the pass.
+  //    the pass is bound by the CU's vector ALU, not by bytes: per row it takes the bin, one
+  //    compare for "in the range" and one for "below the range" (both as lane masks, the latter
+  //    only popcounted), and a row of the range costs a stash write at a slot found from the
+  //    masks.  The index is read with 16-byte loads, RPL consecutive rows per lane (a lane's rows,
+  //    then the next lane's, so the wave still sees its rows in ascending g).  The rows past the
+  //    last whole vector (fewer than RPL) are read one per lane after the pass.
   constexpr int RPL = 16 / (int)sizeof(TI);
   const int n32 = (int)N;
   const int n_al = n32 - n32 % RPL;  // rows in whole 16-byte vectors
   const int per = ((n32 + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;  // 64 | per
   const int r0 = min(n32, wave * per);
   const int r1 = min(n32, r0 + per);
-  int* mycnt = cnt + wave * nloc;
-  int2* mystash = stash + wave * kTokWaveStash;
+  const int lim = min(r1, n_al);
   const rsrc_t ri = make_rsrc(idx, (uint32_t)(N * (int64_t)sizeof(TI)));  // element loads
   const rsrc_t rv = make_rsrc(idx, (uint32_t)((int64_t)n_al * (int64_t)sizeof(TI)));  // vectors
-  int below = 0;   // rows of this lane whose bin precedes the range
-  int wcount = 0;  // rows of the range seen by this wave (wave-uniform)
-  auto bin_at = [&](int g, int lim, TI raw) -> uint32_t {  // 0xffffffff: not a row of this wave
-    const int64_t t = (int64_t)raw;
-    return g < lim ? ((uint64_t)t < (uint64_t)T ? (uint32_t)t : (uint32_t)T) : 0xffffffffu;
-  };
-  auto count_row = [&](int g, uint32_t b) {
-    below += b < (uint32_t)lo ? 1 : 0;
-    const uint32_t j = b - (uint32_t)lo;
-    const bool in = j < (uint32_t)nloc;
-    const uint64_t m = __ballot(in);
-    if (m) {  // wave-uniform
-      if (in) {
-        atomicAdd(&mycnt[j], 1);
-        const int slot = wcount + lanes_below(m);
-        if (slot < kTokWaveStash) mystash[slot] = make_int2(g, (int)j);
-      }
-      wcount += __popcll(m);
-    }
-  };
-  // rows g0 .. g0 + RPL - 1 of this lane: a row's stash slot counts the range's rows held by the
-  // lower lanes (all RPL of theirs) and by this lane's lower rows
-  auto count_vec = [&](int g0, const uint32_t* b) {
-    uint32_t j[RPL];
-    bool in[RPL];
-    uint64_t m[RPL];
-    uint64_t any = 0;
-#pragma unroll
-    for (int r = 0; r < RPL; ++r) {
-      below += b[r] < (uint32_t)lo ? 1 : 0;
-      j[r] = b[r] - (uint32_t)lo;
-      in[r] = j[r] < (uint32_t)nloc;
-      m[r] = __ballot(in[r]);
-      any |= m[r];
-    }
-    if (any) {  // wave-uniform
-      int slot = wcount;
-#pragma unroll
-      for (int r = 0; r < RPL; ++r) slot += lanes_below(m[r]);
-#pragma unroll
-      for (int r = 0; r < RPL; ++r) {
-        if (in[r]) {
-          atomicAdd(&mycnt[j[r]], 1);
-          if (slot < kTokWaveStash) mystash[slot] = make_int2(g0 + r, (int)j[r]);
-          ++slot;
-        }
-        wcount += __popcll(m[r]);
-      }
-    }
-  };
   auto load_batch = [&](int base, u32x4* v) {  // past n_al: zeros from the range check, no traffic
 #pragma unroll
     for (int i = 0; i < kTokLoads; ++i) {
       const int g0 = base + (i * kWave + lane) * RPL;
       v[i] = Raw<16>::template ld<kCPolCached>(rv, (uint32_t)g0 * (uint32_t)sizeof(TI));
+    }
+  };
+  // Two batch buffers used in turn (no register copies, which would make each iteration wait for
+  // the next batch's loads), so one batch is always in flight while the other is counted.  The
+  // first batch is issued before the LDS set-up and its barrier.
+  u32x4 va[kTokLoads], vb[kTokLoads];
+  if (r0 < lim) load_batch(r0, va);  // wave-uniform
+
+  TokMetaRegs<Meta> mreg;
+  mreg.load(meta, ne);  // used after the pass over idx
+  for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) cnt[i] = 0;
+  if (threadIdx.x == 0) misaligned = 0;
+  __syncthreads();
+
+  int* mycnt = cnt + wave * nloc;
+  int2* mystash = stash + wave * (kTokWaveStash + 1);
+  int below = 0;   // rows of this wave whose bin precedes the range (wave-uniform)
+  int wcount = 0;  // rows of the range seen by this wave (wave-uniform)
+  auto bin_at = [&](int g, int lim_g, TI raw) -> uint32_t {  // exact; 0xffffffff: not a row here
+    const int64_t t = (int64_t)raw;
+    return g < lim_g ? ((uint64_t)t < (uint64_t)T ? (uint32_t)t : (uint32_t)T) : 0xffffffffu;
+  };
+  // The local bin of a row of the range: lo_j is lo, kept out of the compiler's sight so that
+  // it does not fold the subtraction into the "below" compare (whose borrow it would then turn
+  // back into a lane mask with two more instructions per row).
+  uint32_t lo_j = (uint32_t)lo;
+  asm volatile("" : "+s"(lo_j));
+  // rows g0 .. g0 + RPL - 1 of this lane, bins b (0xffffffff: no row).  Per row two compares
+  // give lane masks, below = b < lo and in = b < hi and not below.  A row of the range goes to
+  // the stash slot that counts the range's rows of the lower lanes (all RPL of theirs) and of this
+  // lane's lower rows; a slot past the stash goes to the wave's overflow slot (the fill then
+  // re-reads the wave's rows).
+  auto count_vec = [&](int g0, const uint32_t* b) {
+    uint64_t m[RPL];
+    uint64_t any = 0;
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      const uint64_t mb = __ballot(b[r] < (uint32_t)lo);
+      m[r] = __ballot(b[r] < (uint32_t)hi) & ~mb;
+      below += __popcll(mb);
+      any |= m[r];
+    }
+    if (any) {  // wave-uniform
+      uint32_t slot = (uint32_t)wcount;
+#pragma unroll
+      for (int r = 0; r < RPL; ++r)
+        slot = __builtin_amdgcn_mbcnt_hi((uint32_t)(m[r] >> 32),
+                                         __builtin_amdgcn_mbcnt_lo((uint32_t)m[r], slot));
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) {
+        if (m[r]) {  // wave-uniform
+          const uint32_t j = b[r] - lo_j;
+          const bool in = j < (uint32_t)nloc;
+          if (in) mystash[min(slot, (uint32_t)kTokWaveStash)] = make_int2(g0 + r, (int)j);
+          slot += in ? 1u : 0u;
+          wcount += __popcll(m[r]);
+        }
+      }
     }
   };
   auto row_of = [](const u32x4& v, int r) -> TI {
@@ -233,21 +240,36 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       return (TI)v[r];
   };
   constexpr int kBatchRows = kTokLoads * kWave * RPL;
-  const int lim = min(r1, n_al);
-  // One batch: a batch that ends at or below lim needs no per-row range check.
-  auto count_batch = [&](int base, const u32x4* v) {
-    if (base + kBatchRows <= lim) {  // wave-uniform
+  // A whole batch below lim whose rows are all below 2^32 as unsigned 64-bit values (int64: every
+  // high word zero; int32 always) takes the low word as the bin as it is: a value of T or more,
+  // or a negative int32, is then neither in a range that ends at or below T nor below it, so only
+  // the workgroup of bin T clamps it to T.  Anything else takes the exact per-row path.
+  auto count_fast = [&](int base, const u32x4* v, auto owns_invalid) {
 #pragma unroll
-      for (int i = 0; i < kTokLoads; ++i) {
-        const int g0 = base + (i * kWave + lane) * RPL;
-        uint32_t b[RPL];
+    for (int i = 0; i < kTokLoads; ++i) {
+      const int g0 = base + (i * kWave + lane) * RPL;
+      uint32_t b[RPL];
 #pragma unroll
-        for (int r = 0; r < RPL; ++r) {
-          const int64_t t = (int64_t)row_of(v[i], r);
-          b[r] = (uint64_t)t < (uint64_t)T ? (uint32_t)t : (uint32_t)T;
-        }
-        count_vec(g0, b);
+      for (int r = 0; r < RPL; ++r) {
+        const uint32_t x = sizeof(TI) == 8 ? v[i][2 * r] : v[i][r];
+        b[r] = decltype(owns_invalid)::value ? min(x, (uint32_t)T) : x;
       }
+      count_vec(g0, b);
+    }
+  };
+  auto count_batch = [&](int base, const u32x4* v) {
+    bool exact = base + kBatchRows > lim;  // wave-uniform
+    if constexpr (sizeof(TI) == 8) {
+      if (!exact) {
+        uint32_t high = 0;
+#pragma unroll
+        for (int i = 0; i < kTokLoads; ++i) high |= v[i][1] | v[i][3];
+        exact = __ballot(high != 0) != 0;
+      }
+    }
+    if (!exact) {
+      if (last) count_fast(base, v, std::true_type{});
+      else count_fast(base, v, std::false_type{});
     } else {
 #pragma unroll
       for (int i = 0; i < kTokLoads; ++i) {
@@ -260,11 +282,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     }
   };
   if (r0 < lim) {  // wave-uniform
-    // Two batch buffers used in turn (no register copies, which would make each iteration wait
-    // for the next batch's loads), so one batch is always in flight while the other is counted.
     // The loads are unconditional: past the range they return zeros without traffic.
-    u32x4 va[kTokLoads], vb[kTokLoads];
-    load_batch(r0, va);
     for (int base = r0; base < lim; base += 2 * kBatchRows) {
       load_batch(base + kBatchRows, vb);
       count_batch(base, va);
@@ -275,12 +293,23 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   }
   if (r1 > n_al && r0 < r1) {  // wave-uniform: the rows past the last whole vector
     const int g = max(r0, n_al) + lane;
-    count_row(g, bin_at(g, r1,
-                        __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
-                                                   ri, (uint32_t)g * (uint32_t)sizeof(TI)))));
+    const uint32_t b = bin_at(g, r1, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
+                                                     ri, (uint32_t)g * (uint32_t)sizeof(TI))));
+    // one row per lane: the slot rule of count_vec with a single row
+    const uint64_t mb = __ballot(b < (uint32_t)lo);
+    const uint64_t m = __ballot(b < (uint32_t)hi) & ~mb;
+    below += __popcll(mb);
+    if (m) {  // wave-uniform
+      const uint32_t slot = (uint32_t)wcount + (uint32_t)lanes_below(m);
+      const uint32_t j = b - lo_j;
+      if (j < (uint32_t)nloc) mystash[min(slot, (uint32_t)kTokWaveStash)] = make_int2(g, (int)j);
+      wcount += __popcll(m);
+    }
   }
   mreg.store(meta, ne, off32, ptr_lds);
-  // The gates of the stashed rows, loaded before the scan so that their latency overlaps it.
+  // This wave's rows per bin, counted from the stash (or, when it overflowed, from its rows
+  // again), and the gates of the stashed rows, loaded before the scan so that their latency
+  // overlaps it.
   constexpr int kStashChunks = kTokWaveStash / kWave;
   int2 se[kStashChunks];
   float sw[kStashChunks];
@@ -291,6 +320,15 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       const bool act = at < wcount;
       se[q] = act ? mystash[at] : make_int2(0, 0);
       sw[q] = act ? ld1(w + se[q].x) : 0.f;
+      if (act) atomicAdd(&mycnt[se[q].y], 1);
+    }
+  } else {
+    for (int base = r0; base < r1; base += kWave) {
+      const int g = base + lane;
+      const uint32_t j = bin_at(g, r1, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
+                                                                  ri, (uint32_t)g * (uint32_t)sizeof(TI)))) -
+                         (uint32_t)lo;
+      if (j < (uint32_t)nloc) atomicAdd(&mycnt[j], 1);
     }
   }
   __syncthreads();  // the expert table and every wave's counts
@@ -313,7 +351,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   if (bj < nloc)
     for (int v = 0; v < kTokWaves; ++v) tot += cnt[v * nloc + bj];
   int rows_below;
-  const int excl = tok_scan_and_sum(tot, below, &rows_below);
+  const int excl = tok_scan_and_sum(tot, lane == 0 ? below : 0, &rows_below);
   if (bj < nloc) {
     int run = rows_below + excl;
     row_ptr[lo + bj] = run;
