@@ -50,6 +50,42 @@ __host__ __device__ inline PlanGeom plan_geom(int64_t N, int64_t T) {
   return g;
 }
 
+// ---- ranged plan geometry ---------------------------------------------------------------------
+// Two launches for larger N: the rows are partitioned by token range in slices of kRangeSlice rows
+// (k_plan_split, one row per thread, stable within each range), then one 1024-thread workgroup per
+// range of at most kRangeMaxBins consecutive bins gathers the range's rows, slice after slice, and
+// orders them like the one-launch plan (k_plan_range).  A row's range is bin / bins, computed as
+// (bin * magic) >> 32 with magic = ceil(2^32 / bins): exact for bin < 2^32 / bins, which
+// T + 1 <= kRangeMaxBinsTotal guarantees.
+constexpr int kRangeSlice = 1024;                 // rows per slice (one per thread)
+constexpr int kRangeMaxSlices = 1024;             // slices: N <= 2^20
+constexpr int kRangeGroups = 256;                 // ranges aimed at (about one per CU)
+constexpr int kRangeMaxBins = 512;                // bins per range (the per-wave LDS counters)
+constexpr int64_t kRangeMaxBinsTotal = int64_t(kRangeGroups) * kRangeMaxBins;
+
+struct RangeGeom {
+  int Q;           // ranges (>= 1), each non-empty
+  int bins;        // bins per range
+  uint64_t magic;  // ceil(2^32 / bins)
+  int G1;          // slices (>= 1)
+  bool ok;         // within the ranged plan's limits
+};
+
+__host__ __device__ inline RangeGeom range_geom(int64_t N, int64_t T) {
+  RangeGeom r;
+  const int64_t nb = T + 1;
+  int64_t q = nb < kRangeGroups ? nb : kRangeGroups;
+  const int64_t bins = (nb + q - 1) / q;
+  q = (nb + bins - 1) / bins;
+  r.Q = (int)q;
+  r.bins = (int)bins;
+  r.magic = ((uint64_t(1) << 32) + (uint64_t)bins - 1) / (uint64_t)bins;
+  const int64_t g1 = (N + kRangeSlice - 1) / kRangeSlice;
+  r.G1 = (int)(g1 > 1 ? g1 : 1);
+  r.ok = nb <= kRangeMaxBinsTotal && bins <= kRangeMaxBins && g1 <= kRangeMaxSlices;
+  return r;
+}
+
 // ---- radix plan geometry ----------------------------------------------------------------------
 // Beyond the bucketed plan's limits: a stable least-significant-digit radix sort of the rows by
 // token bin (plan_radix.hip), 8-bit digits, in tiles of whole 1024-row chunks -- about
@@ -90,7 +126,8 @@ __host__ __device__ inline RadixGeom radix_geom(int64_t N, int64_t T) {
 //   radix    the radix plan's digit totals (kRadixMaxPasses x 256 int32) and per-tile digit
 //            table (256 x ntiles int32)
 struct PlanLayout {
-  int64_t status, cursor, row_ptr, rec_tmp, part, bcnt, bpre, rec, radix_tot, radix_hist, total;
+  int64_t status, cursor, row_ptr, rec_tmp, part, bcnt, bpre, rcnt, rpre, rec, radix_tot, radix_hist,
+      total;
 };
 
 __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
@@ -105,7 +142,13 @@ __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
   L.part = L.rec_tmp;
   L.bcnt = L.part + up(N * 8);
   L.bpre = L.bcnt + up(tab);
-  const int64_t tmp_end = std::max(L.rec_tmp + up(N * 16), L.bpre + up(tab));
+  // the ranged plan's per-range, per-slice row counts and prefixes follow its partition
+  const RangeGeom rg = range_geom(N, T);
+  const int64_t rtab = (int64_t)rg.Q * rg.G1 * 4;
+  L.rcnt = L.part + up(N * 8);
+  L.rpre = L.rcnt + up(rtab);
+  const int64_t tmp_end =
+      std::max(std::max(L.rec_tmp + up(N * 16), L.bpre + up(tab)), L.rpre + up(rtab));
   L.rec = tmp_end;
   L.radix_tot = L.rec + up(N * 16);
   L.radix_hist = L.radix_tot + up(kRadixMaxPasses * kRadixDigits * 4);

@@ -9,10 +9,12 @@
 //   rec[N]          : 16-byte records {source row address, fp32 gate, g}, ascending g in every
 //                     segment
 //
-// Three builders, each linear in N + T and each writing every segment in ascending g:
-//   * one launch (k_plan_tok), up to kTokMaxRows rows: token-sliced workgroups that each stream
-//     all of idx and fill their own segments stably (below);
-//   * two launches (plan_bucket.hip), larger N: partition the rows by token bucket, then order
+// Four builders, each linear in N + T and each writing every segment in ascending g:
+//   * one launch (k_plan_tok), below 2^16 rows: token-sliced workgroups that each stream all of
+//     idx and fill their own segments stably (below);
+//   * the ranged plan (k_plan_split + k_plan_range), up to 2^20 rows and 2^17 tokens: partition
+//     the rows by token range, then one token-sliced workgroup per range reads only its rows;
+//   * two launches (plan_bucket.hip), beyond that: partition the rows by token bucket, then order
 //     each bucket with one wave;
 //   * the radix plan (plan_radix.hip), beyond 2^22 tokens: count + scan (one 1024-thread
 //     workgroup histograms idx in LDS, or zero / global-atomic count / one-block scan for larger
@@ -52,6 +54,9 @@ constexpr int kTokGroups = 256;
 constexpr int kTokExperts = 4096;                      // expert tables staged in LDS
 constexpr int64_t kTokMaxRows = int64_t(1) << 17;
 constexpr int kTokLoads = 8;                           // 16-byte index loads per lane per batch
+static_assert(kTokBins == kRangeMaxBins, "a range of the ranged plan is a token-sliced workgroup");
+static_assert(kRangeMaxSlices <= kScanThreads, "k_plan_range reads one slice per thread");
+static_assert(kRangeSlice == kScanThreads, "k_plan_split takes one row per thread");
 
 // The expert table of a plan workgroup, loaded into registers when the workgroup starts and
 // written to LDS after the pass over idx, so that its load latency overlaps the pass instead of
@@ -132,17 +137,125 @@ __device__ __forceinline__ int tok_scan_and_sum(int v, int s, int* sum_s) {
   return before + incl - v;
 }
 
+// LDS of a token-sliced plan workgroup (k_plan_tok, k_plan_range).
+struct TokLds {
+  int cnt[kTokWaves * kTokBins];                // [wave][bin]: counts, then cursors
+  int2 stash[kTokWaves * (kTokWaveStash + 1)];  // per wave: (g, local bin) in ascending g, and a
+                                                // slot for the rows past the stash
+  int off32[kTokExperts + 1];
+  uint64_t ptr_lds[kTokExperts];
+  int misaligned;
+};
+
+// The end of a token-sliced plan workgroup, after each wave has stashed its rows of the range
+// [lo, lo + nloc) in ascending g (wcount of them; past kTokWaveStash the stash holds only the
+// first): count them per bin, scan the bins into row_ptr (rows_part: this thread's share of the
+// rows before the range, summed over the workgroup) and the per-wave cursors, and write each row's
+// record at its wave's cursor for the bin plus its rank among the lower lanes of the same bin.
+// rows(fn) replays this wave's rows in ascending g, calling fn(act, g, j) once per 64 rows with
+// every lane: used when the stash overflowed.
+template <typename TW, typename Meta, typename Rows>
+__device__ __forceinline__ void tok_finish(TokLds& L, const TokMetaRegs<Meta>& mreg,
+                                           const Meta& meta, int ne, int64_t row_bytes,
+                                           const TW* __restrict__ w, int lo, int nloc, int nb,
+                                           int wcount, int rows_part, int32_t* __restrict__ row_ptr,
+                                           Rec* __restrict__ rec, int32_t* __restrict__ status,
+                                           Rows rows) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  int* mycnt = L.cnt + wave * nloc;
+  const int2* mystash = L.stash + wave * (kTokWaveStash + 1);
+  mreg.store(meta, ne, L.off32, L.ptr_lds);
+  // This wave's rows per bin, counted from the stash (or, when it overflowed, from its rows
+  // again), and the gates of the stashed rows, loaded before the scan so that their latency
+  // overlaps it.
+  constexpr int kStashChunks = kTokWaveStash / kWave;
+  int2 se[kStashChunks];
+  float sw[kStashChunks];
+  if (wcount <= kTokWaveStash) {  // wave-uniform
+#pragma unroll
+    for (int q = 0; q < kStashChunks; ++q) {
+      const int at = q * kWave + lane;
+      const bool act = at < wcount;
+      se[q] = act ? mystash[at] : make_int2(0, 0);
+      sw[q] = act ? ld1(w + se[q].x) : 0.f;
+      if (act) atomicAdd(&mycnt[se[q].y], 1);
+    }
+  } else {
+    rows([&](bool act, int, uint32_t j) {
+      if (act) atomicAdd(&mycnt[j], 1);
+    });
+  }
+  __syncthreads();  // the expert table and every wave's counts
+
+  if (blockIdx.x == 0) {
+    // a source row is misaligned iff its expert's base is, or the expert has two or more rows
+    // and the row length is not a multiple of 16 bytes
+    int mis = 0;
+    for (int e = threadIdx.x; e < ne; e += kScanThreads) {
+      const int n = L.off32[e + 1] - L.off32[e];
+      if (n > 0 && ((L.ptr_lds[e] & 15) || (n > 1 && (row_bytes & 15)))) mis = 1;
+    }
+    if (mis) L.misaligned = 1;  // read after the next barrier
+  }
+
+  // thread j owns bin j of the range: its rows over all waves, row_ptr, and each wave's first
+  // place in it (the cursors)
+  const int bj = threadIdx.x;
+  int tot = 0;
+  if (bj < nloc)
+    for (int v = 0; v < kTokWaves; ++v) tot += L.cnt[v * nloc + bj];
+  int rows_before;
+  const int excl = tok_scan_and_sum(tot, rows_part, &rows_before);
+  const int hi = lo + nloc;
+  if (bj < nloc) {
+    int run = rows_before + excl;
+    row_ptr[lo + bj] = run;
+    if (lo + bj == nb - 1) status[kStatusInvalid] = tot;  // the out-of-range bin
+    for (int v = 0; v < kTokWaves; ++v) {
+      const int c = L.cnt[v * nloc + bj];
+      L.cnt[v * nloc + bj] = run;
+      run += c;
+    }
+    if (hi == nb && bj == nloc - 1) row_ptr[nb] = run;  // == N
+  }
+  __syncthreads();  // the cursors (and the misaligned flag)
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    status[kStatusMisaligned] = L.misaligned;
+    status[kStatusLongest] = -1;  // not recorded: no workgroup sees every segment
+  }
+
+  // fill: each wave its rows in ascending g -- from the stash, or replayed if it overflowed
+  const int jbits = nloc > 1 ? 32 - __builtin_clz((unsigned)(nloc - 1)) : 0;
+  auto place = [&](bool act, int g, int j, float wg) {
+    const uint64_t m = match_key(act, j, jbits);
+    if (act) {
+      const int rank = lanes_below(m);
+      const int pos = mycnt[j] + rank;
+      if (rank == 0) mycnt[j] = pos + __popcll(m);
+      const int e = expert_of_row32(L.off32, ne, g);
+      Rec r;
+      r.src = L.ptr_lds[e] + (uint64_t)((int64_t)(g - L.off32[e]) * row_bytes);
+      r.w = wg;
+      r.g = g;
+      rec[pos] = r;
+    }
+  };
+  if (wcount <= kTokWaveStash) {  // wave-uniform
+#pragma unroll
+    for (int q = 0; q < kStashChunks; ++q)
+      if (q * kWave < wcount) place(q * kWave + lane < wcount, se[q].x, se[q].y, sw[q]);
+  } else {
+    rows([&](bool act, int g, uint32_t j) { place(act, g, (int)j, act ? ld1(w + g) : 0.f); });
+  }
+}
+
 template <typename TI, typename TW, typename Meta>
 __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     const TI* __restrict__ idx, const TW* __restrict__ w, int64_t N, int64_t T, int bins,
     const Meta meta, int64_t E, int64_t row_bytes, int32_t* __restrict__ row_ptr,
     Rec* __restrict__ rec, int32_t* __restrict__ status) {
-  __shared__ int cnt[kTokWaves * kTokBins];                 // [wave][bin]: counts, then cursors
-  __shared__ int2 stash[kTokWaves * (kTokWaveStash + 1)];   // per wave: (g, local bin), ascending
-                                                            // g, and a slot for overflowing rows
-  __shared__ int off32[kTokExperts + 1];
-  __shared__ uint64_t ptr_lds[kTokExperts];
-  __shared__ int misaligned;
+  __shared__ TokLds L;
   const int nb = (int)T + 1;
   const int ne = (int)E;
   const int lo = (int)blockIdx.x * bins;  // the host makes every range non-empty
@@ -183,12 +296,11 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
 
   TokMetaRegs<Meta> mreg;
   mreg.load(meta, ne);  // used after the pass over idx
-  for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) cnt[i] = 0;
-  if (threadIdx.x == 0) misaligned = 0;
+  for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) L.cnt[i] = 0;
+  if (threadIdx.x == 0) L.misaligned = 0;
   __syncthreads();
 
-  int* mycnt = cnt + wave * nloc;
-  int2* mystash = stash + wave * (kTokWaveStash + 1);
+  int2* mystash = L.stash + wave * (kTokWaveStash + 1);
   int below = 0;   // rows of this wave whose bin precedes the range (wave-uniform)
   int wcount = 0;  // rows of the range seen by this wave (wave-uniform)
   auto bin_at = [&](int g, int lim_g, TI raw) -> uint32_t {  // exact; 0xffffffff: not a row here
@@ -306,102 +418,165 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       wcount += __popcll(m);
     }
   }
-  mreg.store(meta, ne, off32, ptr_lds);
-  // This wave's rows per bin, counted from the stash (or, when it overflowed, from its rows
-  // again), and the gates of the stashed rows, loaded before the scan so that their latency
-  // overlaps it.
-  constexpr int kStashChunks = kTokWaveStash / kWave;
-  int2 se[kStashChunks];
-  float sw[kStashChunks];
-  if (wcount <= kTokWaveStash) {  // wave-uniform
-#pragma unroll
-    for (int q = 0; q < kStashChunks; ++q) {
-      const int at = q * kWave + lane;
-      const bool act = at < wcount;
-      se[q] = act ? mystash[at] : make_int2(0, 0);
-      sw[q] = act ? ld1(w + se[q].x) : 0.f;
-      if (act) atomicAdd(&mycnt[se[q].y], 1);
-    }
-  } else {
+  // this wave's rows again, for a stash that overflowed
+  auto rows = [&](auto fn) {
     for (int base = r0; base < r1; base += kWave) {
       const int g = base + lane;
       const uint32_t j = bin_at(g, r1, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
                                                                   ri, (uint32_t)g * (uint32_t)sizeof(TI)))) -
                          (uint32_t)lo;
-      if (j < (uint32_t)nloc) atomicAdd(&mycnt[j], 1);
-    }
-  }
-  __syncthreads();  // the expert table and every wave's counts
-
-  if (blockIdx.x == 0) {
-    // a source row is misaligned iff its expert's base is, or the expert has two or more rows
-    // and the row length is not a multiple of 16 bytes
-    int mis = 0;
-    for (int e = threadIdx.x; e < ne; e += kScanThreads) {
-      const int n = off32[e + 1] - off32[e];
-      if (n > 0 && ((ptr_lds[e] & 15) || (n > 1 && (row_bytes & 15)))) mis = 1;
-    }
-    if (mis) misaligned = 1;  // read after the next barrier
-  }
-
-  // 2. thread j owns bin j of the range: its rows over all waves, row_ptr, and each wave's first
-  //    place in it (the cursors)
-  const int bj = threadIdx.x;
-  int tot = 0;
-  if (bj < nloc)
-    for (int v = 0; v < kTokWaves; ++v) tot += cnt[v * nloc + bj];
-  int rows_below;
-  const int excl = tok_scan_and_sum(tot, lane == 0 ? below : 0, &rows_below);
-  if (bj < nloc) {
-    int run = rows_below + excl;
-    row_ptr[lo + bj] = run;
-    if (lo + bj == nb - 1) status[kStatusInvalid] = tot;  // the out-of-range bin
-    for (int v = 0; v < kTokWaves; ++v) {
-      const int c = cnt[v * nloc + bj];
-      cnt[v * nloc + bj] = run;
-      run += c;
-    }
-    if (hi == nb && bj == nloc - 1) row_ptr[nb] = run;  // == N
-  }
-  __syncthreads();  // the cursors (and the misaligned flag)
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    status[kStatusMisaligned] = misaligned;
-    status[kStatusLongest] = -1;  // not recorded: no workgroup sees every segment
-  }
-
-  // 3. fill: each wave its rows in ascending g -- from the stash, or again from idx if the stash
-  //    overflowed
-  const int jbits = nloc > 1 ? 32 - __builtin_clz((unsigned)(nloc - 1)) : 0;
-  auto place = [&](bool act, int g, int j, float wg) {
-    const uint64_t m = match_key(act, j, jbits);
-    if (act) {
-      const int rank = lanes_below(m);
-      const int pos = mycnt[j] + rank;
-      if (rank == 0) mycnt[j] = pos + __popcll(m);
-      const int e = expert_of_row32(off32, ne, g);
-      Rec r;
-      r.src = ptr_lds[e] + (uint64_t)((int64_t)(g - off32[e]) * row_bytes);
-      r.w = wg;
-      r.g = g;
-      rec[pos] = r;
+      fn(j < (uint32_t)nloc, g, j);
     }
   };
-  if (wcount <= kTokWaveStash) {  // wave-uniform
+  tok_finish(L, mreg, meta, ne, row_bytes, w, lo, nloc, nb, wcount, lane == 0 ? below : 0,
+             row_ptr, rec, status, rows);
+}
+
+// ---- ranged plan: two launches, each CU reading only its share of idx -----------------------
+// The one-launch plan has every workgroup read all of idx, N * 8 bytes through each CU's L1, which
+// bounds it from about 2^16 rows up.  The ranged plan reads idx once:
+//   k_plan_split  one 1024-thread workgroup per slice of kRangeSlice rows, one row per thread.  A
+//                 row's range is bin / bins (range_geom).  Each wave counts its rows per range by
+//                 ballot match, the workgroup scans the counts range-major and wave-minor, and each
+//                 row goes to the slice's range-major partition at its wave's cursor plus its rank
+//                 among the lower lanes of the same range, so the rows of one range keep ascending
+//                 g.  Per range and slice it writes the row count and the rows of lower ranges,
+//                 range-major (rcnt[q][s], rpre[q][s]).
+//   k_plan_range  one 1024-thread workgroup per range.  The range's rows are, slice after slice,
+//                 part[s * S + rpre[q][s] ..] (rcnt[q][s] of them), in ascending g; the rows before
+//                 the range number sum_s rpre[q][s].  Wave v takes the v-th sixteenth of the
+//                 range's rows in order and stashes them as the one-launch plan's pass does; the
+//                 workgroup then ends like it (tok_finish).
+template <typename TI>
+__global__ __launch_bounds__(kScanThreads) void k_plan_split(
+    const TI* __restrict__ idx, int64_t N, int64_t T, int Q, uint64_t magic, int G1,
+    int2* __restrict__ part, int32_t* __restrict__ rcnt, int32_t* __restrict__ rpre) {
+  __shared__ int cnt[kTokWaves * kRangeGroups];  // [wave][range]: counts, then cursors
+  const int wave = threadIdx.x / kWave;
+  const int s = blockIdx.x;
+  const int64_t g = (int64_t)s * kRangeSlice + threadIdx.x;
+  const bool act = g < N;
+  int bin = 0, q = 0;
+  if (act) {
+    const int64_t t = (int64_t)idx[g];
+    bin = (uint64_t)t < (uint64_t)T ? (int)t : (int)T;
+    q = (int)(((uint64_t)(uint32_t)bin * magic) >> 32);
+  }
+  for (int i = threadIdx.x; i < kTokWaves * Q; i += kScanThreads) cnt[i] = 0;
+  __syncthreads();
+  const int qbits = Q > 1 ? 32 - __builtin_clz((unsigned)(Q - 1)) : 0;
+  const uint64_t m = match_key(act, q, qbits);
+  const int rank = lanes_below(m);
+  if (act && rank == 0) cnt[wave * Q + q] = __popcll(m);  // one writer per (wave, range)
+  __syncthreads();
+  // thread i owns range i: the slice's rows in it, the slice's rows in lower ranges, and each
+  // wave's first place in it
+  const int qi = threadIdx.x;
+  int tot = 0;
+  if (qi < Q)
+    for (int v = 0; v < kTokWaves; ++v) tot += cnt[v * Q + qi];
+  int all;
+  const int pre = block_exclusive_scan_1024(tot, &all);
+  if (qi < Q) {
+    int run = pre;
+    for (int v = 0; v < kTokWaves; ++v) {
+      const int c = cnt[v * Q + qi];
+      cnt[v * Q + qi] = run;
+      run += c;
+    }
+    rcnt[(int64_t)qi * G1 + s] = tot;
+    rpre[(int64_t)qi * G1 + s] = pre;
+  }
+  __syncthreads();
+  if (act) part[(int64_t)s * kRangeSlice + cnt[wave * Q + q] + rank] = make_int2((int)g, bin);
+}
+
+template <typename TW, typename Meta>
+__global__ __launch_bounds__(kScanThreads) void k_plan_range(
+    const int2* __restrict__ part, const int32_t* __restrict__ rcnt,
+    const int32_t* __restrict__ rpre, int G1, int64_t T, int bins, const TW* __restrict__ w,
+    const Meta meta, int64_t E, int64_t row_bytes, int32_t* __restrict__ row_ptr,
+    Rec* __restrict__ rec, int32_t* __restrict__ status) {
+  __shared__ TokLds L;
+  __shared__ int first[kRangeMaxSlices + 1];  // rows of this range in the slices before s
+  __shared__ int at[kRangeMaxSlices];         // partition index of slice s's first row of it
+  const int nb = (int)T + 1;
+  const int ne = (int)E;
+  const int q = blockIdx.x;
+  const int lo = q * bins;  // the host makes every range non-empty
+  const int nloc = min(nb, lo + bins) - lo;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  // this range's rows in every slice: thread s reads slice s's count and prefix
+  const int sl = threadIdx.x;
+  int c = 0, p = 0;
+  if (sl < G1) {
+    c = rcnt[(int64_t)q * G1 + sl];
+    p = rpre[(int64_t)q * G1 + sl];
+  }
+  TokMetaRegs<Meta> mreg;
+  mreg.load(meta, ne);  // used after the gather
+  for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) L.cnt[i] = 0;
+  if (threadIdx.x == 0) L.misaligned = 0;
+  int before;  // rows of lower ranges: the sum over the slices
+  const int excl = tok_scan_and_sum(c, p, &before);
+  if (sl < G1) {
+    first[sl] = excl;
+    at[sl] = sl * kRangeSlice + p;
+    if (sl == G1 - 1) first[G1] = excl + c;
+  }
+  __syncthreads();
+  const int nrows = first[G1];
+
+  // Wave v takes rows [p0, p1) of the range in order; row i is in the last slice a with
+  // first[a] <= i (first[G1] = nrows > i).
+  const int per = ((nrows + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;
+  const int p0 = min(nrows, wave * per);
+  const int p1 = min(nrows, p0 + per);
+  auto fetch = [&](int i) -> int2 {
+    int a = 0, b = G1;
+    while (b - a > 1) {
+      const int mid = (a + b) >> 1;
+      if (first[mid] <= i) a = mid; else b = mid;
+    }
+    return part[at[a] + (i - first[a])];
+  };
+  int2* mystash = L.stash + wave * (kTokWaveStash + 1);
+  int wcount = 0;  // wave-uniform
+  constexpr int kGather = 4;  // chunks of 64 rows in flight
+  for (int base = p0; base < p1; base += kGather * kWave) {
+    int2 v[kGather];
 #pragma unroll
-    for (int q = 0; q < kStashChunks; ++q)
-      if (q * kWave < wcount) place(q * kWave + lane < wcount, se[q].x, se[q].y, sw[q]);
-  } else {
-    for (int base = r0; base < r1; base += kWave) {
-      const int g = base + lane;
-      const uint32_t b = bin_at(
-          g, r1, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
-                                            ri, (uint32_t)g * (uint32_t)sizeof(TI))));
-      const uint32_t j = b - (uint32_t)lo;
-      const bool in = j < (uint32_t)nloc;
-      const float wg = in ? ld1(w + g) : 0.f;
-      place(in, g, (int)j, wg);
+    for (int k = 0; k < kGather; ++k) {
+      const int i = base + k * kWave + lane;
+      v[k] = i < p1 ? fetch(i) : make_int2(0, -1);
+    }
+#pragma unroll
+    for (int k = 0; k < kGather; ++k) {
+      const bool in = v[k].y >= 0;
+      const uint64_t m = __ballot(in);
+      if (in) {
+        const uint32_t slot = (uint32_t)wcount + (uint32_t)lanes_below(m);
+        mystash[min(slot, (uint32_t)kTokWaveStash)] = make_int2(v[k].x, v[k].y - lo);
+      }
+      wcount += __popcll(m);
     }
   }
+  auto rows = [&](auto fn) {  // kGather chunks in flight, as in the gather
+    for (int base = p0; base < p1; base += kGather * kWave) {
+      int2 v[kGather];
+#pragma unroll
+      for (int k = 0; k < kGather; ++k) {
+        const int i = base + k * kWave + lane;
+        v[k] = i < p1 ? fetch(i) : make_int2(0, lo);
+      }
+#pragma unroll
+      for (int k = 0; k < kGather; ++k)
+        if (base + k * kWave < p1) fn(base + k * kWave + lane < p1, v[k].x, (uint32_t)(v[k].y - lo));
+    }
+  };
+  tok_finish(L, mreg, meta, ne, row_bytes, w, lo, nloc, nb, wcount, threadIdx.x == 0 ? before : 0,
+             row_ptr, rec, status, rows);
 }
 
 // ---- plan of a combine fed by the dispatch permutation -------------------------------------
@@ -528,28 +703,68 @@ int launch_plan_tok(const Meta& meta, const void* d_indices, int idx_dtype, cons
   return fmoe_host::check_launch("fmoe_build_plan(one launch)");
 }
 
+// The ranged plan: k_plan_split, then k_plan_range (range_geom(N, T).ok and E <= kTokExperts,
+// checked by the caller).
+template <typename Meta>
+int launch_plan_ranged(const Meta& meta, const void* d_indices, int idx_dtype,
+                       const void* d_weights, int w_dtype, int64_t N, int64_t T, int64_t E,
+                       int64_t row_bytes, void* d_workspace, hipStream_t s) {
+  using namespace fmoe;
+  const RangeGeom g = range_geom(N, T);
+  const PlanLayout L = plan_layout(N, T);
+  char* ws = static_cast<char*>(d_workspace);
+  int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
+  int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
+  Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
+  int2* part = reinterpret_cast<int2*>(ws + L.part);
+  int32_t* rcnt = reinterpret_cast<int32_t*>(ws + L.rcnt);
+  int32_t* rpre = reinterpret_cast<int32_t*>(ws + L.rpre);
+  if (idx_dtype == FMOE_I64)
+    hipLaunchKernelGGL(k_plan_split<int64_t>, dim3((unsigned)g.G1), dim3(kScanThreads), 0, s,
+                       static_cast<const int64_t*>(d_indices), N, T, g.Q, g.magic, g.G1, part,
+                       rcnt, rpre);
+  else
+    hipLaunchKernelGGL(k_plan_split<int32_t>, dim3((unsigned)g.G1), dim3(kScanThreads), 0, s,
+                       static_cast<const int32_t*>(d_indices), N, T, g.Q, g.magic, g.G1, part,
+                       rcnt, rpre);
+  if (int rc = fmoe_host::check_launch("fmoe_build_plan(ranged, split)")) return rc;
+#define FMOE_RANGE(TW)                                                                         \
+  hipLaunchKernelGGL((k_plan_range<TW, Meta>), dim3((unsigned)g.Q), dim3(kScanThreads), 0, s,  \
+                     part, rcnt, rpre, g.G1, T, g.bins, static_cast<const TW*>(d_weights), meta, \
+                     E, row_bytes, row_ptr, rec, status)
+  if (w_dtype == FMOE_F32) FMOE_RANGE(float);
+  else if (w_dtype == FMOE_BF16) FMOE_RANGE(bf16_t);
+  else FMOE_RANGE(f16_t);
+#undef FMOE_RANGE
+  return fmoe_host::check_launch("fmoe_build_plan(ranged)");
+}
+
 // Which plan builds the records by default: when the tokens average kRadixRowsPerToken rows or
 // more, the radix plan, whose cost does not depend on how the rows spread over the tokens (the
-// bucketed plan orders each bucket with one wave, about 25 ns per row, so one hot token costs it
-// milliseconds, and the one-launch plan has at most T + 1 workgroups); else the stable one-launch
-// plan up to kTokMaxRows rows, then the bucketed plan, then the radix plan, each where its limits
-// hold.  Top-k routing (k <= 64 rows per token) never takes the radix plan.  Option "plan":
-// 0 automatic, 1 radix, 2 bucketed, 3 one launch (each where its limits hold; the next in that
-// order otherwise).
-enum PlanPath { kPathTok, kPathBucketed, kPathRadix };
+// others give a token's rows to one workgroup or wave); else the one-launch plan below
+// kRangedMinRows rows, where reading all of idx in every workgroup costs less than a second
+// launch; then the ranged plan, the bucketed plan and the radix plan, each where its limits hold.
+// Top-k routing (k <= 64 rows per token) never takes the radix plan.  Option "plan": 0 automatic,
+// 1 radix, 2 bucketed, 3 one launch, 4 ranged (a forced path whose limits do not hold falls back
+// to the automatic choice).
+enum PlanPath { kPathTok, kPathRanged, kPathBucketed, kPathRadix };
 constexpr int64_t kRadixRowsPerToken = 64;
+constexpr int64_t kRangedMinRows = int64_t(1) << 16;
 bool long_segments(int64_t N, int64_t T) { return N >= kRadixRowsPerToken * (T + 1); }
-bool bucketed_by_default(int64_t N, int64_t T) {
-  return fmoe::plan_geom(N, T).ok && !long_segments(N, T);
-}
 PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bins) {
   const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
   const bool tok = tok_grid(N, T, E, groups, bins);
+  const bool ranged = fmoe::range_geom(N, T).ok && E <= fmoe::kTokExperts;
   const bool bucketed = fmoe::plan_geom(N, T).ok;
   if (algo == 1) return kPathRadix;
   if (algo == 2) return bucketed ? kPathBucketed : kPathRadix;
-  if (tok && (algo == 3 || (N <= fmoe::kTokMaxRows && !long_segments(N, T)))) return kPathTok;
-  return bucketed_by_default(N, T) ? kPathBucketed : kPathRadix;
+  if (algo == 3 && tok) return kPathTok;
+  if (algo == 4 && ranged) return kPathRanged;
+  if (long_segments(N, T)) return kPathRadix;
+  if (tok && N < kRangedMinRows) return kPathTok;
+  if (ranged) return kPathRanged;
+  if (tok && N <= fmoe::kTokMaxRows) return kPathTok;
+  return bucketed ? kPathBucketed : kPathRadix;
 }
 
 }  // namespace
@@ -604,6 +819,9 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   if (path == kPathTok)
     return launch_plan_tok(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
                            groups, bins, row_ptr, rec, status, s);
+  if (path == kPathRanged)
+    return launch_plan_ranged(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
+                              d_workspace, s);
   if (path == kPathBucketed)
     return fmoe_plan::launch_bucketed(&meta, nullptr, d_indices, idx_dtype, d_weights, w_dtype, N,
                                       T, E, row_bytes, d_workspace, false, nullptr, nullptr, s,
@@ -667,6 +885,9 @@ extern "C" int fmoe_build_metadata_and_plan(
   TokMetaArgs meta;
   fill_host_table(&meta, host_ptrs, host_rows, E, d_ptr_table, d_chunk_sizes, d_offsets,
                   d_max_rows);
+  if (path == kPathRanged)
+    return launch_plan_ranged(meta, d_indices, idx_dtype, d_weights, w_dtype, N, T, E, row_bytes,
+                              d_workspace, static_cast<hipStream_t>(stream));
   if (path == kPathBucketed)
     return fmoe_plan::launch_bucketed(nullptr, &meta, d_indices, idx_dtype, d_weights, w_dtype, N,
                                       T, E, row_bytes, d_workspace, false, nullptr, nullptr,
@@ -810,9 +1031,11 @@ extern "C" int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, i
   FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
                "fmoe_invert_scatter_index: workspace not 256B-aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // the bucketed plan (option plan=2, or by default as for the records), else the radix plan
+  // the bucketed plan (option plan=2, or by default unless the tokens average 64 rows or more),
+  // else the radix plan
   const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
-  if ((algo == 2 && plan_geom(N, T).ok) || ((algo == 0 || algo == 3) && bucketed_by_default(N, T)))
+  const bool bucketed = plan_geom(N, T).ok;
+  if (bucketed && (algo == 2 || (algo != 1 && !long_segments(N, T))))
     return fmoe_plan::launch_bucketed(nullptr, nullptr, d_indices, idx_dtype, nullptr, FMOE_F32, N,
                                       T, 0, 0, d_workspace, true, d_rows, d_row_ptr, s,
                                       "fmoe_invert_scatter_index");

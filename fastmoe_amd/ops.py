@@ -443,8 +443,8 @@ def invert_scatter_index(indices: torch.Tensor, num_tokens: int):
 def plan_status(plan: torch.Tensor) -> torch.Tensor:
     """The plan's int32 status words [invalid_index_count, misaligned_flag, longest_segment]
     (a device view).  longest_segment counts the rows of the busiest token when the plan was built
-    by the bucketed or radix plan or from a slot map, and is -1 for the one-launch plan, which
-    never sees every segment in one place."""
+    by the bucketed or radix plan or from a slot map, and is -1 for the one-launch and ranged
+    plans, whose workgroups never see every segment in one place."""
     off = _abi.lib().fmoe_plan_status_offset()
     return plan[off: off + 12].view(torch.int32)
 

@@ -95,10 +95,11 @@ FMOE_API const char* fmoe_last_error(void);
  * starting value once, when the library loads.  Launches read the option table, never the
  * environment.  Options select among variants that compute the same results (tests compare them):
  *   "plan"            [FMOE_PLAN]      0 = automatic (the radix plan when the tokens average 64
- *                                      rows or more; else one launch up to 2^17 rows, two up to
- *                                      2^22 tokens, the radix plan beyond), 1 = radix (a stable
- *                                      radix sort by token; FMOE_PLAN_SPLIT=1), 2 = bucketed (two
- *                                      launches), 3 = one launch
+ *                                      rows or more; else one launch below 2^16 rows, the ranged
+ *                                      plan up to 2^20 rows and 2^17 tokens, then the bucketed
+ *                                      plan up to 2^22 tokens, the radix plan beyond), 1 = radix (a
+ *                                      stable radix sort by token), 2 = bucketed (two launches),
+ *                                      3 = one launch, 4 = ranged (two launches)
  *   "bwd_fused"       [FMOE_BWD_FUSED] 1 = both backward gradients in one pass
  *   "gw_staged"       [FMOE_GW_STAGED] 0 = grad_w pass reads grad_out per wave, not through LDS
  *   "force_scalar"    [FMOE_FORCE_SCALAR] 1 = element-wise instead of 16-byte accesses
@@ -133,9 +134,11 @@ FMOE_API int fmoe_build_metadata(const int64_t* host_ptrs, const int64_t* host_r
  * Plan: token-major inverse of the scatter index.  For each token t, the packed rows g with
  * idx[g] == t, each as a 16-byte record {source row address, fp32 gate, g}, in ascending g.  Rows
  * with an out-of-range index form one extra segment (number T).  Time is linear in N + T: one
- * launch up to 2^17 rows, two up to 2^22 tokens, and a stable radix sort of the rows by token
- * (3 launches per 8 bits of T, plus 3 to 5) beyond that or when the tokens average 64 rows or
- * more, whose time does not depend on how the rows spread (option "plan" selects a path).
+ * launch below 2^16 rows, two (the ranged plan: partition by token range, then a workgroup per
+ * range) up to 2^20 rows and 2^17 tokens, two (the bucketed plan) up to 2^22 tokens, and a stable
+ * radix sort of the rows by token (3 launches per 8 bits of T, plus 3 to 5) beyond that or when
+ * the tokens average 64 rows or more, whose time does not depend on how the rows spread (option
+ * "plan" selects a path).
  *
  * Workspace: fmoe_plan_workspace_bytes(N, T) bytes of device memory, 256-byte aligned, owned by the
  * caller; no zero-fill is needed.  Layout (byte offsets from the workspace base):
@@ -162,7 +165,7 @@ FMOE_API int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d
  * in the reference, which builds metadata per call in prepare_grouped_metadata, ops.py:200-271,
  * and needs no inverse).  Outputs and workspace exactly as those two calls; num_rows is the sum
  * of host_rows.  With at most 256 experts the plan's own kernels also write the metadata, the
- * (address, rows) table riding in their arguments: one launch up to 2^17 rows, two beyond (up to
+ * (address, rows) table riding in their arguments: one launch below 2^16 rows, two beyond (up to
  * 2^22 tokens); otherwise it makes the two calls.
  */
 FMOE_API int fmoe_build_metadata_and_plan(const int64_t* host_ptrs, const int64_t* host_rows,

@@ -116,7 +116,8 @@ def _set_bwd_variant(kernel_options, variant):
     kernel_options(**_BWD_VARIANTS[variant])
 
 
-_PLAN_PATHS = {"tok": 3, "bucketed": 2, "radix": 1}  # values of the "plan" option
+_PLAN_PATHS = {"tok": 3, "ranged": 4, "bucketed": 2, "radix": 1}  # values of the "plan" option
+_NO_LONGEST = ("tok", "ranged")  # plans whose workgroups never see every segment
 
 
 @pytest.mark.parametrize("variant", list(_BWD_VARIANTS))
@@ -496,9 +497,10 @@ def _plan_case(case: str):
                                   "wide_hist"])
 def test_plan_matches_oracle(case, path, kernel_options):
     """row_ptr, the records (source address, gate bits, g) and the status words equal the
-    oracle's stable inverse, for the one-launch plan, the bucketed plan (two launches) and the
-    radix plan (count + scan, then a stable radix sort by token bin): each writes every segment in
-    ascending g, including when several workgroups each take a piece of one segment."""
+    oracle's stable inverse, for the one-launch plan, the ranged plan (partition by token range,
+    then a workgroup per range), the bucketed plan (two launches) and the radix plan (count +
+    scan, then a stable radix sort by token bin): each writes every segment in ascending g,
+    including when several workgroups each take a piece of one segment."""
     from oracle import cref
 
     kernel_options(plan=_PLAN_PATHS[path])
@@ -519,9 +521,9 @@ def test_plan_matches_oracle(case, path, kernel_options):
     st = ops.plan_status(plan).cpu().numpy()
     misaligned = int((D * experts[0].element_size()) % 16 != 0)
     assert st[0] == 0 and st[1] == misaligned
-    # the longest segment: recorded by the radix and bucketed plans; -1 from the one-launch plan
-    # (no workgroup sees every segment)
-    assert st[2] == (-1 if path == "tok" else seg_len[:T].max())
+    # the longest segment: recorded by the radix and bucketed plans; -1 from the one-launch and
+    # ranged plans (no workgroup sees every segment)
+    assert st[2] == (-1 if path in _NO_LONGEST else seg_len[:T].max())
     if case != "topk512":
         assert seg_len[:T].max() > 64
     np.testing.assert_array_equal(g, want_g)  # stable: every segment in ascending g
@@ -577,6 +579,50 @@ def test_plan_one_launch_any_group_count(groups, idx_dtype, kernel_options):
     assert st[0] == int(bad.sum()) and st[1] == 0
 
 
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+@pytest.mark.parametrize("T,N,hot", [(16384, 131072, 0), (32768, 65536, 0), (1000, 100_003, 0),
+                                     (70000, 200_000, 0), (4096, 50_000, 20_000)])
+def test_plan_ranged_matches_oracle(T, N, hot, idx_dtype, kernel_options):
+    """The ranged plan (k_plan_split partitions the rows by token range in 1024-row slices, then
+    a workgroup per range orders its rows) is the oracle's stable inverse at the sizes it is
+    chosen for: the skewed and detatomic shapes (bins per range 65 and 129, found by the
+    multiply-shift division), a ragged last slice (N not a multiple of 1024), more token bins than
+    256 ranges of 256 bins hold, int32 and int64 indices, 2% of them out of range on both sides;
+    with `hot` rows piled onto token 7, that range's waves overflow their stashes and replay their
+    rows.  The forward reading the plan is bit-exact."""
+    from oracle import cref
+
+    kernel_options(plan=_PLAN_PATHS["ranged"])
+    gen = torch.Generator().manual_seed(T + N)
+    D = 4
+    idx = torch.randint(0, T, (N,), generator=gen)
+    if hot:
+        idx[torch.randperm(N, generator=gen)[:hot]] = 7
+    bad = torch.rand(N, generator=gen) < 0.02
+    idx = torch.where(bad, torch.where(torch.rand(N, generator=gen) < 0.5,
+                                       torch.full_like(idx, T), torch.full_like(idx, -3)), idx)
+    idx = idx.to(idx_dtype)
+    w = torch.rand(N, generator=gen)
+    cuts = torch.sort(torch.randint(0, N + 1, (31,), generator=gen)).values.tolist()
+    sizes = [b - a for a, b in zip([0] + cuts, cuts + [N])]
+    experts = [torch.randn(n, D, generator=gen) for n in sizes]
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta, plan = ops.prepare_metadata_and_plan(xd, idd, wd, T)
+    lib = fastmoe_amd._abi.lib()
+    rp = plan[lib.fmoe_plan_row_ptr_offset(N, T):][: 4 * (T + 2)].view(torch.int32).cpu().numpy()
+    rec = plan[lib.fmoe_plan_records_offset(N, T):][: 16 * N].view(torch.int64).view(N, 2).cpu()
+    want_rp, want_g = cref.plan(idx.to(torch.int64).numpy(), T)
+    np.testing.assert_array_equal(rp, want_rp)
+    np.testing.assert_array_equal((rec[:, 1] >> 32).numpy().astype(np.int32), want_g)
+    wbits = (rec[:, 1] & 0xFFFFFFFF).numpy().astype(np.uint32)
+    np.testing.assert_array_equal(wbits, w.numpy()[want_g].view(np.uint32))
+    st = ops.plan_status(plan).cpu().numpy()
+    assert st[0] == int(bad.sum()) and st[1] == 0 and st[2] == -1
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
+    want, _, _ = oracle_fwd(experts, idx.to(torch.int64), w, T, torch.float32)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+
+
 def test_bwd_f16_grad_x_rounds_twice_like_the_reference():
     """f16 experts, fp32 gates: grad_X is the fp32 product rounded to fp32 and then to f16
     (index_select * w, then autograd's cast; ops.py:344-353).  The inputs include elements where
@@ -608,7 +654,7 @@ def test_random_shapes_against_oracle(plan, kernel_options):
     """40 seeded random cases: tokens, experts (some empty), rows, D, every dtype combination,
     int32/int64 indices, and out-of-range indices mixed in; forward bits, grad_X bits and grad_w
     (1e-6 of sum|terms|) against the oracle, through the autograd path, with each of the
-    three plans."""
+    four plans."""
     kernel_options(plan=_PLAN_PATHS[plan])
     rng = np.random.default_rng(2026)
     dts = [torch.float32, torch.bfloat16, torch.float16]
@@ -796,7 +842,7 @@ def test_plan_few_tokens(T, N, path, kernel_options):
     np.testing.assert_array_equal(g, want_g)  # every segment in ascending g
     st = ops.plan_status(plan).cpu().numpy()
     assert int(st[0]) == int((want_rp[T + 1] - want_rp[T]))
-    assert int(st[2]) == (-1 if path == "tok" else int(np.diff(want_rp)[:T].max()))
+    assert int(st[2]) == (-1 if path in _NO_LONGEST else int(np.diff(want_rp)[:T].max()))
     out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
     want, _, bad = oracle_fwd(experts, idx, w, T, torch.float32)
     assert bad == want_rp[T + 1] - want_rp[T]
