@@ -156,18 +156,28 @@ __host__ __device__ inline PlanLayout plan_layout(int64_t N, int64_t T) {
   return L;
 }
 
+// ---- wave scans -------------------------------------------------------------------------------
+// Inclusive prefix sum over the 64 lanes of a wave with gfx9 DPP: row_shr 1, 2, 4, 8 scan each row
+// of 16 lanes (a lane with no source lane adds 0), row_bcast:15 adds row 0's total to row 1 and
+// row 2's to row 3, row_bcast:31 adds the first 32 lanes' total to rows 2 and 3.  Six register
+// moves instead of six LDS permutes.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
+  return x;
+}
+
 // ---- 1024-thread block reductions -------------------------------------------------------------
 // Exclusive scan of one int per thread over a 1024-thread block; *total gets the block sum.
 __device__ __forceinline__ int block_exclusive_scan_1024(int v, int* total) {
   __shared__ int wave_tot[kScanThreads / kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
+  const int incl = wave_incl_sum(v);
   if (lane == kWave - 1) wave_tot[wv] = incl;
   __syncthreads();
   int before = 0, tot = 0;

@@ -114,14 +114,8 @@ __device__ __forceinline__ int tok_scan_and_sum(int v, int s, int* sum_s) {
   __shared__ int wave_v[kTokWaves], wave_s[kTokWaves];
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) s += __shfl_xor(s, d, kWave);
+  const int incl = wave_incl_sum(v);
+  s = wave_incl_sum(s);  // the wave's sum in its last lane
   if (lane == kWave - 1) {
     wave_v[wv] = incl;
     wave_s[wv] = s;

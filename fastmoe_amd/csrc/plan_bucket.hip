@@ -28,15 +28,7 @@ constexpr int kBucketCache = 8;      // chunks of 64 rows a k_plan_bucket wave k
 constexpr int kLdsMetaExperts = 4096;  // expert tables staged in LDS up to this many experts
 static_assert(kPartThreads == kScanThreads, "k_plan_part scans with the 1024-thread block scan");
 
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(v, d, kWave);
-    if (lane >= d) v += o;
-  }
-  return v;
-}
+__device__ __forceinline__ int wave_incl_scan(int v) { return wave_incl_sum(v); }
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
   for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
