@@ -37,6 +37,7 @@ from __future__ import annotations
 import array
 import contextlib
 import ctypes
+import operator
 import os
 from typing import Optional, Sequence
 
@@ -155,14 +156,21 @@ class GroupedMetadata(tuple):
                 and tuple(checked[4]) == self.ptrs)
 
 
+# Per-tensor property readers for map(): unbound C accessors, without a Python-level loop body.
+_DTYPE_OF = torch.Tensor.dtype.__get__
+_SHAPE_OF = torch.Tensor.shape.__get__
+_ROWS_OF, _COLS_OF = operator.itemgetter(0), operator.itemgetter(1)
+
+
 def _check_experts(expert_tensors: Sequence[torch.Tensor]):
     """Validate the expert buffers; returns (dtype, device, hidden, sizes, ptrs).
 
     Every buffer must be a 2-D [rows, D] tensor of one float dtype on one GPU, row-contiguous
     (``is_contiguous()`` on a 2-D tensor is exactly the layout the kernels address: strides (D, 1)
     for several rows, a unit column stride for one row, anything for no rows).  With hundreds of
-    experts this runs on every call, so each property is read once per tensor in a comprehension;
-    only a failing list is walked again, to name the first offending buffer.
+    experts this runs on every call, so each property is read once per tensor through ``map``
+    over the tensor type's own accessors; only a failing list is walked again, to name the first
+    offending buffer.
     """
     if len(expert_tensors) == 0:
         raise ValueError("fastmoe_amd: expert_tensors is empty")
@@ -173,13 +181,14 @@ def _check_experts(expert_tensors: Sequence[torch.Tensor]):
     if ref.dim() != 2:
         raise ValueError(f"fastmoe_amd: expert tensors must be 2-D [rows, D], got {tuple(ref.shape)}")
     dtype, device, hidden = ref.dtype, ref.device, ref.shape[1]
-    shapes = [t.shape for t in expert_tensors]
-    if ({t.dtype for t in expert_tensors} != {dtype}
-            or {t.device for t in expert_tensors} != {device}
-            or not all([len(sh) == 2 and sh[1] == hidden for sh in shapes])
-            or not all([t.is_contiguous() for t in expert_tensors])):
+    shapes = list(map(_SHAPE_OF, expert_tensors))
+    if (set(map(_DTYPE_OF, expert_tensors)) != {dtype}
+            or set(map(torch.Tensor.get_device, expert_tensors)) != {ref.get_device()}
+            or set(map(len, shapes)) != {2} or set(map(_COLS_OF, shapes)) != {hidden}
+            or not all(map(torch.Tensor.is_contiguous, expert_tensors))):
         _explain_bad_expert(expert_tensors, dtype, device, hidden)
-    return dtype, device, hidden, [sh[0] for sh in shapes], [t.data_ptr() for t in expert_tensors]
+    return (dtype, device, hidden, list(map(_ROWS_OF, shapes)),
+            list(map(torch.Tensor.data_ptr, expert_tensors)))
 
 
 def _explain_bad_expert(expert_tensors, dtype, device, hidden) -> None:
@@ -629,7 +638,7 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
         launch("bwd" if gx_ptr and gw_ptr else ("bwd_gx" if gx_ptr else "bwd_gw"), gx_ptr, gw_ptr)
     if need_x:
         parts = torch.split(gx, list(sizes))
-        grads_x = [p if n else None for p, n in zip(parts, needs_x)]
+        grads_x = parts if all(needs_x) else [p if n else None for p, n in zip(parts, needs_x)]
     else:
         grads_x = [None] * len(sizes)
     return (gw.view(ctx.w_shape) if gw is not None else None), grads_x
