@@ -109,6 +109,31 @@ def test_noalloc_equals_workspace_entry_points_two_calls_second_smaller(out_dtyp
 
 
 @pytest.mark.gpu
+def test_noalloc_ranged_plan_then_smaller_call():
+    """72,000 rows (at least 2^16: the metadata and plan take the ranged plan's two launches, its
+    partition and tables in the static buffer), then a call of 192 rows reusing that buffer; both
+    equal the workspace entry points bit for bit and the oracle."""
+    print("noalloc: ranged-plan call, then a smaller one", flush=True)
+    big = _case(12000, 64, 64, 6, torch.bfloat16, 13)
+    small = _case(96, 520, 8, 2, torch.bfloat16, 14)
+    dev = big["xs"][0].device
+    want, got, keep = [], [], []
+    for c in (big, small):
+        o = torch.zeros((c["T"], c["D"]), dtype=torch.bfloat16, device=dev)
+        keep.append(_with_workspace(c, o, 0))
+        want.append(o)
+    for c in (big, small):
+        o = torch.full((c["T"], c["D"]), 5.0, dtype=torch.bfloat16, device=dev)
+        _noalloc(c, o, 0)
+        got.append(o)
+    torch.cuda.synchronize()
+    for c, g, wnt in zip((big, small), got, want):
+        assert np.array_equal(bits(g), bits(wnt))
+        exp, _, _ = oracle_fwd(c["xs_cpu"], c["idx_cpu"], c["w_cpu"], c["T"], torch.bfloat16)
+        assert np.array_equal(bits(g), _as_bits(exp))
+
+
+@pytest.mark.gpu
 def test_noalloc_accumulates_into_padded_out_with_int32_indices():
     print("noalloc: accumulate, padded fp32 out, int32 indices", flush=True)
     big = _case(700, 1000, 40, 4, torch.bfloat16, 13, torch.int32)
