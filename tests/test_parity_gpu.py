@@ -388,9 +388,10 @@ def test_edge_invalid_indices_dropped_and_flagged(variant, kernel_options):
     assert np.all(g[0].cpu().numpy()[[1, 3, 5]] == 0)
 
 
-@pytest.mark.parametrize("D", [100, 8, 1, 4096 + 8])
+@pytest.mark.parametrize("D", [100, 8, 1, 4096 + 8, 65536 + 8, 131072])
 def test_edge_odd_hidden_sizes(D):
-    """D not a multiple of the 16-byte vector (scalar path) and partial column chunks."""
+    """D not a multiple of the 16-byte vector (scalar path), partial column chunks, and wide rows
+    (32 to 64 column chunks per token, rows of up to 512 KiB in fp32)."""
     T = 33
     gen = torch.Generator().manual_seed(D)
     sizes = [5, 17, 0, 11]
