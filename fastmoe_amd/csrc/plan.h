@@ -54,14 +54,19 @@ __host__ __device__ inline PlanGeom plan_geom(int64_t N, int64_t T) {
 // Two launches for larger N: the rows are partitioned by token range in slices of kRangeSlice rows
 // (k_plan_split, one row per thread, stable within each range), then one 1024-thread workgroup per
 // range of at most kRangeMaxBins consecutive bins gathers the range's rows, slice after slice, and
-// orders them like the one-launch plan (k_plan_range).  A row's range is bin / bins, computed as
-// (bin * magic) >> 32 with magic = ceil(2^32 / bins): exact for bin < 2^32 / bins, which
-// T + 1 <= kRangeMaxBinsTotal guarantees.
+// orders them like the one-launch plan (k_plan_range).  There are about kRangeGroups ranges (one
+// per CU), more when the bins or the rows would not fit (a range's workgroup stashes up to
+// kRangeRows rows without re-reading them), at most kRangeMaxGroups.  A row's range is bin / bins,
+// computed as (bin * magic) >> 32 with magic = ceil(2^32 / bins): exact for bin < 2^32 / bins,
+// which T + 1 <= kRangeMaxBinsTotal guarantees.
 constexpr int kRangeSlice = 1024;                 // rows per slice (one per thread)
-constexpr int kRangeMaxSlices = 1024;             // slices: N <= 2^20
+constexpr int kRangeMaxSlices = 4096;             // slices: N <= 2^22
+constexpr int kRangeSlicesPerThread = 4;          // k_plan_range reads 4 slices' words per thread
 constexpr int kRangeGroups = 256;                 // ranges aimed at (about one per CU)
+constexpr int kRangeMaxGroups = 1024;             // ranges at most (k_plan_split's LDS counters)
 constexpr int kRangeMaxBins = 512;                // bins per range (the per-wave LDS counters)
-constexpr int64_t kRangeMaxBinsTotal = int64_t(kRangeGroups) * kRangeMaxBins;
+constexpr int kRangeRows = 4096;                  // rows a range's stashes hold (16 waves x 256)
+constexpr int64_t kRangeMaxBinsTotal = int64_t(kRangeMaxGroups) * kRangeMaxBins;
 
 struct RangeGeom {
   int Q;           // ranges (>= 1), each non-empty
@@ -75,14 +80,20 @@ __host__ __device__ inline RangeGeom range_geom(int64_t N, int64_t T) {
   RangeGeom r;
   const int64_t nb = T + 1;
   int64_t q = nb < kRangeGroups ? nb : kRangeGroups;
+  const int64_t by_bins = (nb + kRangeMaxBins - 1) / kRangeMaxBins;
+  const int64_t by_rows = (N + kRangeRows - 1) / kRangeRows;
+  q = q > by_bins ? q : by_bins;
+  q = q > by_rows ? q : by_rows;
+  q = q < nb ? q : nb;
   const int64_t bins = (nb + q - 1) / q;
   q = (nb + bins - 1) / bins;
-  r.Q = (int)q;
+  r.Q = (int)(q < kRangeMaxGroups ? q : kRangeMaxGroups);
   r.bins = (int)bins;
   r.magic = ((uint64_t(1) << 32) + (uint64_t)bins - 1) / (uint64_t)bins;
   const int64_t g1 = (N + kRangeSlice - 1) / kRangeSlice;
-  r.G1 = (int)(g1 > 1 ? g1 : 1);
-  r.ok = nb <= kRangeMaxBinsTotal && bins <= kRangeMaxBins && g1 <= kRangeMaxSlices;
+  r.G1 = (int)(g1 > 1 ? (g1 < kRangeMaxSlices ? g1 : kRangeMaxSlices) : 1);
+  r.ok = nb <= kRangeMaxBinsTotal && bins <= kRangeMaxBins && q <= kRangeMaxGroups &&
+         g1 <= kRangeMaxSlices;
   return r;
 }
 

@@ -12,7 +12,7 @@
 // Four builders, each linear in N + T and each writing every segment in ascending g:
 //   * one launch (k_plan_tok), below 2^16 rows: token-sliced workgroups that each stream all of
 //     idx and fill their own segments stably (below);
-//   * the ranged plan (k_plan_split + k_plan_range), up to 2^20 rows and 2^17 tokens: partition
+//   * the ranged plan (k_plan_split + k_plan_range), up to 2^21 rows and 2^19 tokens: partition
 //     the rows by token range, then one token-sliced workgroup per range reads only its rows;
 //   * two launches (plan_bucket.hip), beyond that: partition the rows by token bucket, then order
 //     each bucket with one wave;
@@ -55,7 +55,9 @@ constexpr int kTokExperts = 4096;                      // expert tables staged i
 constexpr int64_t kTokMaxRows = int64_t(1) << 17;
 constexpr int kTokLoads = 8;                           // 16-byte index loads per lane per batch
 static_assert(kTokBins == kRangeMaxBins, "a range of the ranged plan is a token-sliced workgroup");
-static_assert(kRangeMaxSlices <= kScanThreads, "k_plan_range reads one slice per thread");
+static_assert(kRangeMaxSlices <= kScanThreads * kRangeSlicesPerThread,
+              "k_plan_range reads kRangeSlicesPerThread slices per thread");
+static_assert(kRangeMaxGroups <= kScanThreads, "k_plan_split scans one range per thread");
 static_assert(kRangeSlice == kScanThreads, "k_plan_split takes one row per thread");
 
 // The expert table of a plan workgroup, loaded into registers when the workgroup starts and
@@ -445,7 +447,7 @@ template <typename TI>
 __global__ __launch_bounds__(kScanThreads) void k_plan_split(
     const TI* __restrict__ idx, int64_t N, int64_t T, int Q, uint64_t magic, int G1,
     int2* __restrict__ part, int32_t* __restrict__ rcnt, int32_t* __restrict__ rpre) {
-  __shared__ int cnt[kTokWaves * kRangeGroups];  // [wave][range]: counts, then cursors
+  __shared__ int cnt[kTokWaves * kRangeMaxGroups];  // [wave][range]: counts, then cursors
   const int wave = threadIdx.x / kWave;
   const int s = blockIdx.x;
   const int64_t g = (int64_t)s * kRangeSlice + threadIdx.x;
@@ -494,6 +496,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_range(
   __shared__ TokLds L;
   __shared__ int first[kRangeMaxSlices + 1];  // rows of this range in the slices before s
   __shared__ int at[kRangeMaxSlices];         // partition index of slice s's first row of it
+  constexpr int SPT = kRangeSlicesPerThread;
   const int nb = (int)T + 1;
   const int ne = (int)E;
   const int q = blockIdx.x;
@@ -501,23 +504,33 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_range(
   const int nloc = min(nb, lo + bins) - lo;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  // this range's rows in every slice: thread s reads slice s's count and prefix
-  const int sl = threadIdx.x;
-  int c = 0, p = 0;
-  if (sl < G1) {
-    c = rcnt[(int64_t)q * G1 + sl];
-    p = rpre[(int64_t)q * G1 + sl];
+  // this range's rows in every slice: thread t reads the count and prefix of slices
+  // [t * SPT, t * SPT + SPT)
+  const int s0 = (int)threadIdx.x * SPT;
+  int c[SPT], p[SPT];
+  int csum = 0, psum = 0;
+#pragma unroll
+  for (int r = 0; r < SPT; ++r) {
+    const bool in = s0 + r < G1;
+    c[r] = in ? rcnt[(int64_t)q * G1 + s0 + r] : 0;
+    p[r] = in ? rpre[(int64_t)q * G1 + s0 + r] : 0;
+    csum += c[r];
+    psum += p[r];
   }
   TokMetaRegs<Meta> mreg;
   mreg.load(meta, ne);  // used after the gather
   for (int i = threadIdx.x; i < kTokWaves * nloc; i += kScanThreads) L.cnt[i] = 0;
   if (threadIdx.x == 0) L.misaligned = 0;
   int before;  // rows of lower ranges: the sum over the slices
-  const int excl = tok_scan_and_sum(c, p, &before);
-  if (sl < G1) {
-    first[sl] = excl;
-    at[sl] = sl * kRangeSlice + p;
-    if (sl == G1 - 1) first[G1] = excl + c;
+  int run = tok_scan_and_sum(csum, psum, &before);
+#pragma unroll
+  for (int r = 0; r < SPT; ++r) {
+    if (s0 + r < G1) {
+      first[s0 + r] = run;
+      at[s0 + r] = (s0 + r) * kRangeSlice + p[r];
+      run += c[r];
+      if (s0 + r == G1 - 1) first[G1] = run;
+    }
   }
   __syncthreads();
   const int nrows = first[G1];
@@ -737,13 +750,16 @@ int launch_plan_ranged(const Meta& meta, const void* d_indices, int idx_dtype,
 // more, the radix plan, whose cost does not depend on how the rows spread over the tokens (the
 // others give a token's rows to one workgroup or wave); else the one-launch plan below
 // kRangedMinRows rows, where reading all of idx in every workgroup costs less than a second
-// launch; then the ranged plan, the bucketed plan and the radix plan, each where its limits hold.
+// launch; then the ranged plan up to kRangedMaxRows rows (beyond, its ranges outnumber the CUs,
+// one workgroup each, and the bucketed plan is faster), the bucketed plan and the radix plan, each
+// where its limits hold.
 // Top-k routing (k <= 64 rows per token) never takes the radix plan.  Option "plan": 0 automatic,
 // 1 radix, 2 bucketed, 3 one launch, 4 ranged (a forced path whose limits do not hold falls back
 // to the automatic choice).
 enum PlanPath { kPathTok, kPathRanged, kPathBucketed, kPathRadix };
 constexpr int64_t kRadixRowsPerToken = 64;
 constexpr int64_t kRangedMinRows = int64_t(1) << 16;
+constexpr int64_t kRangedMaxRows = int64_t(1) << 21;
 bool long_segments(int64_t N, int64_t T) { return N >= kRadixRowsPerToken * (T + 1); }
 PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bins) {
   const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
@@ -756,7 +772,7 @@ PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bi
   if (algo == 4 && ranged) return kPathRanged;
   if (long_segments(N, T)) return kPathRadix;
   if (tok && N < kRangedMinRows) return kPathTok;
-  if (ranged) return kPathRanged;
+  if (ranged && N <= kRangedMaxRows) return kPathRanged;
   if (tok && N <= fmoe::kTokMaxRows) return kPathTok;
   return bucketed ? kPathBucketed : kPathRadix;
 }

@@ -96,7 +96,7 @@ FMOE_API const char* fmoe_last_error(void);
  * environment.  Options select among variants that compute the same results (tests compare them):
  *   "plan"            [FMOE_PLAN]      0 = automatic (the radix plan when the tokens average 64
  *                                      rows or more; else one launch below 2^16 rows, the ranged
- *                                      plan up to 2^20 rows and 2^17 tokens, then the bucketed
+ *                                      plan up to 2^21 rows and 2^19 tokens, then the bucketed
  *                                      plan up to 2^22 tokens, the radix plan beyond), 1 = radix (a
  *                                      stable radix sort by token), 2 = bucketed (two launches),
  *                                      3 = one launch, 4 = ranged (two launches)
@@ -135,7 +135,7 @@ FMOE_API int fmoe_build_metadata(const int64_t* host_ptrs, const int64_t* host_r
  * idx[g] == t, each as a 16-byte record {source row address, fp32 gate, g}, in ascending g.  Rows
  * with an out-of-range index form one extra segment (number T).  Time is linear in N + T: one
  * launch below 2^16 rows, two (the ranged plan: partition by token range, then a workgroup per
- * range) up to 2^20 rows and 2^17 tokens, two (the bucketed plan) up to 2^22 tokens, and a stable
+ * range) up to 2^21 rows and 2^19 tokens, two (the bucketed plan) up to 2^22 tokens, and a stable
  * radix sort of the rows by token (3 launches per 8 bits of T, plus 3 to 5) beyond that or when
  * the tokens average 64 rows or more, whose time does not depend on how the rows spread (option
  * "plan" selects a path).

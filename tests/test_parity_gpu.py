@@ -583,7 +583,8 @@ def test_plan_one_launch_any_group_count(groups, idx_dtype, kernel_options):
 @pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
 @pytest.mark.parametrize("T,N,hot", [(16384, 131072, 0), (32768, 65536, 0), (1000, 100_003, 0),
                                      (70000, 200_000, 0), (4096, 50_000, 20_000),
-                                     (131071, 1 << 20, 0)])
+                                     (131071, 1 << 20, 0), (262143, (1 << 21) + 3, 0),
+                                     ((1 << 19) - 1, (1 << 22) - 5, 0)])
 def test_plan_ranged_matches_oracle(T, N, hot, idx_dtype, kernel_options):
     """The ranged plan (k_plan_split partitions the rows by token range in 1024-row slices, then
     a workgroup per range orders its rows) is the oracle's stable inverse at the sizes it is
@@ -591,8 +592,9 @@ def test_plan_ranged_matches_oracle(T, N, hot, idx_dtype, kernel_options):
     multiply-shift division), a ragged last slice (N not a multiple of 1024), more token bins than
     256 ranges of 256 bins hold, int32 and int64 indices, 2% of them out of range on both sides;
     with `hot` rows piled onto token 7, that range's waves overflow their stashes and replay their
-    rows; T + 1 = 2^17 bins over 2^20 rows is the plan's limit (256 ranges of 512 bins, 1024
-    slices).  The forward reading the plan is bit-exact."""
+    rows; T + 1 = 2^17 bins over 2^20 rows (256 ranges of 512 bins, 1024 slices), 2^18 bins over
+    2^21 rows (513 ranges) and 2^19 bins over 2^22 rows (the plan's limit: 1024 ranges of 512
+    bins, 4096 slices).  The forward reading the plan is bit-exact."""
     from oracle import cref
 
     kernel_options(plan=_PLAN_PATHS["ranged"])
