@@ -4,7 +4,7 @@ Each test draws a fixed number of cases from a seeded generator with log-uniform
 cases small, some up to tens of thousands of rows or tokens) and checks every case against the
 C oracle with the bars of tests/test_parity_gpu.py:
   * autograd forward + backward over uniform, top-k and Zipf-skewed routing, up to 600 experts
-    (beyond the 256 that one launch of metadata + plan takes), both plan paths and both backward
+    (beyond the 256 that one launch of metadata + plan takes), every plan path and both backward
     forms: forward bits, grad_X bits, grad_w within 1e-6 of sum|grad_out * X|;
   * the dispatch permutation (fwd + bwd) up to 4096 experts, and in-place calls into fp32 / bf16 /
     f16 outputs with prior contents and padded rows (det bit-exact, atomic within the two-order
@@ -76,7 +76,9 @@ def test_campaign_autograd(kernel_options):
         wdt = [torch.float32, torch.bfloat16][int(rng.integers(2))]
         idt = [torch.int64, torch.int32][int(rng.integers(2))]
         r, fused = rng.random(), bool(rng.random() < 0.25)
-        plan = 1 if r < 0.25 else (2 if r < 0.4 else 0)  # radix / bucketed / automatic
+        # radix / bucketed / one launch / ranged / automatic (a forced path whose limits do not
+        # hold falls back to the automatic choice)
+        plan = 1 if r < 0.2 else (2 if r < 0.3 else (3 if r < 0.45 else (4 if r < 0.65 else 0)))
         kernel_options(plan=plan, bwd_fused=1 if fused else 0)
         label = (f"autograd case {case}: T={T} N={N} E={E} D={D} {routing} {xdt} {wdt} {idt} "
                  f"plan={plan} fused={fused}")
