@@ -29,7 +29,8 @@ from typing import NamedTuple, Optional
 import torch
 
 from . import _abi
-from .ops import (_FLOAT_CODES, _INDEX_CODES, _launch_fwd, _require_cuda, _span, _stream_handle,
+from .ops import (_FLOAT_CODES, _INDEX_CODES, _check_experts, _launch_fwd,
+                  _metadata_and_plan_from_slots, _require_cuda, _span, _stream_handle,
                   _validate_default, prepare_metadata_and_plan)
 
 __all__ = ["PermutedTokens", "permute_tokens"]
@@ -46,13 +47,37 @@ class PermutedTokens(NamedTuple):
     slot_pos: torch.Tensor             # int32 [T*k], packed row of slot t*k + j
 
 
-def _unit_gate_combine(rows: torch.Tensor, rev: torch.Tensor, num_tokens: int) -> torch.Tensor:
-    """out[t] = sum of rows[g] with rev[g] == t, in ascending g, fp32, rounded once."""
+# Unit gates of the backward combine, kept per (device, rows): built once, outside any graph a
+# caller captures after its warm-up steps, instead of a fill kernel in every backward.
+_ONES: dict = {}
+
+
+def _unit_gates(n: int, dev: torch.device) -> torch.Tensor:
+    key = (dev, n)
+    ones = _ONES.get(key)
+    if ones is None:
+        if len(_ONES) >= 8:
+            _ONES.clear()
+        ones = _ONES[key] = torch.ones(n, dtype=torch.float32, device=dev)
+    return ones
+
+
+def _unit_gate_combine(rows: torch.Tensor, rev: torch.Tensor, slot_pos: torch.Tensor,
+                       num_tokens: int, top_k: int) -> torch.Tensor:
+    """out[t] = sum of rows[g] with rev[g] == t, in ascending g, fp32, rounded once.
+
+    Token t's rows are the packed rows of its slots, slot_pos[t * k + j], so the plan comes from
+    the slot map (one thread per slot) when k <= 64; the forward orders each token's rows by g, so
+    the sum is the same as from the plan of rev."""
     out = torch.empty((num_tokens, rows.shape[1]), dtype=rows.dtype, device=rows.device)
     if rows.shape[0] == 0:
         return out.zero_()
-    ones = torch.ones(rows.shape[0], dtype=torch.float32, device=rows.device)
-    meta, plan = prepare_metadata_and_plan([rows], rev, ones, num_tokens, validate=False)
+    ones = _unit_gates(rows.shape[0], rows.device)
+    if top_k <= 64 and rows.shape[0] == num_tokens * top_k:
+        meta, plan = _metadata_and_plan_from_slots([rows], _check_experts([rows]), slot_pos, ones,
+                                                   num_tokens, top_k)
+    else:
+        meta, plan = prepare_metadata_and_plan([rows], rev, ones, num_tokens, validate=False)
     _launch_fwd(meta, _abi.MODE_DET, plan, None, None, out, accumulate=False)
     return out
 
@@ -109,7 +134,7 @@ class _TokenPermute(torch.autograd.Function):
         T, k = ctx.num_tokens, ctx.top_k
         grad_x = grad_w = None
         if ctx.needs_input_grad[0] and g_out is not None:
-            grad_x = _unit_gate_combine(g_out.contiguous(), rev, T)
+            grad_x = _unit_gate_combine(g_out.contiguous(), rev, slot_pos, T, k)
         if ctx.needs_input_grad[1] and g_sorted_w is not None:
             gs = g_sorted_w.contiguous()
             grad_w = torch.empty(T * k, dtype=gs.dtype, device=gs.device)
