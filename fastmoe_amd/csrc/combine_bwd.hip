@@ -291,20 +291,21 @@ static int launch_bwd_k(const BwdArgs& a) {
   return fmoe_host::check_launch("fmoe_combine_bwd");
 }
 
-// The "bwd_fused" option runs both gradients in one pass (kept for measurement).
-template <typename TX, int V, int U>
-static int launch_bwd_u(const BwdArgs& a) {
-  if (a.gx && a.gw) {
-    if (fmoe_host::opt(fmoe_host::kOptBwdFused)) return launch_bwd_k<TX, V, U, true, true>(a);
-    if (int rc = launch_bwd_k<TX, V, U, true, false>(a)) return rc;  // grad_X: write pass
-    return launch_bwd_k<TX, V, U, false, true>(a);                   // grad_w: read pass
-  }
-  if (a.gx) return launch_bwd_k<TX, V, U, true, false>(a);
-  return launch_bwd_k<TX, V, U, false, true>(a);
+template <typename TX, int V, bool GX, bool GW>
+static int launch_bwd_v(const BwdArgs& a, int U) {
+  if (U == 4) return launch_bwd_k<TX, V, 4, GX, GW>(a);
+  if (U == 2) return launch_bwd_k<TX, V, 2, GX, GW>(a);
+  return launch_bwd_k<TX, V, 1, GX, GW>(a);
 }
 
-// U 16-byte vectors per lane per column step: 4 unless D is small (option "bwd_u" = 1|2|4
-// overrides).
+// U, the 16-byte vectors per lane per column step, is chosen per pass from the row length in
+// bytes (option "bwd_u" = 1|2|4 sets both).  grad_X (and the fused pass): 4 from 8 KiB rows, 2
+// from 4 KiB, else 1.  grad_w: 4 -- the LDS-staged pass, whose column step is 8 KiB -- only from
+// 24 KiB rows, 2 from 4 KiB, else 1.  The staged pass hides its per-step barrier only over several
+// steps; at rows of 8 KiB (one step) it takes about twice as long as the per-wave pass at U = 2
+// (bf16, T = 4096, top-8, HIP events: 72.9 against 37.6 µs at D = 4096, 104.2 against 82.2 µs at
+// D = 7168, 173.6 against 179.5 µs at D = 16384 where it is kept).  The "bwd_fused" option runs
+// both gradients in one pass (kept for measurement).
 template <typename TX>
 static int launch_bwd_x(const BwdArgs& a) {
   constexpr int V = vec16<TX>();
@@ -312,13 +313,24 @@ static int launch_bwd_x(const BwdArgs& a) {
   const bool vec_ok = (a.D % V == 0) && ((uintptr_t)a.gout % 16 == 0) &&
                       ((a.gstride * eb) % 16 == 0) && ((uintptr_t)a.gx % 16 == 0) &&
                       fmoe_host::opt(fmoe_host::kOptForceScalar) == 0;
-  if (!vec_ok) return launch_bwd_u<TX, 1, 4>(a);
-  int U = (int)fmoe_host::opt(fmoe_host::kOptBwdU);
-  if (U != 1 && U != 2 && U != 4)
-    U = a.D >= (int64_t)kWave * V * 4 * 2 ? 4 : (a.D >= (int64_t)kWave * V * 2 * 2 ? 2 : 1);
-  if (U == 4) return launch_bwd_u<TX, V, 4>(a);
-  if (U == 2) return launch_bwd_u<TX, V, 2>(a);
-  return launch_bwd_u<TX, V, 1>(a);
+  const bool fused = fmoe_host::opt(fmoe_host::kOptBwdFused) != 0;
+  if (!vec_ok) {
+    if (a.gx && a.gw && fused) return launch_bwd_k<TX, 1, 4, true, true>(a);
+    if (a.gx)
+      if (int rc = launch_bwd_k<TX, 1, 4, true, false>(a)) return rc;
+    return a.gw ? launch_bwd_k<TX, 1, 4, false, true>(a) : FMOE_OK;
+  }
+  const int64_t row_bytes = a.D * eb;
+  int ux = (int)fmoe_host::opt(fmoe_host::kOptBwdU);
+  int uw = ux;
+  if (ux != 1 && ux != 2 && ux != 4) {
+    ux = row_bytes >= 8192 ? 4 : (row_bytes >= 4096 ? 2 : 1);
+    uw = row_bytes >= 24576 ? 4 : (row_bytes >= 4096 ? 2 : 1);
+  }
+  if (a.gx && a.gw && fused) return launch_bwd_v<TX, V, true, true>(a, ux);
+  if (a.gx)
+    if (int rc = launch_bwd_v<TX, V, true, false>(a, ux)) return rc;  // grad_X: write pass
+  return a.gw ? launch_bwd_v<TX, V, false, true>(a, uw) : FMOE_OK;    // grad_w: read pass
 }
 
 }  // namespace fmoe

@@ -10,11 +10,11 @@ namespace fmoe_host {
 // when the library loads, else from the measured-best default; launches read the table, not the
 // environment.
 enum Opt {
-  kOptPlan = 0,      // "plan": 0 automatic, 1 radix, 2 bucketed, 3 one launch
+  kOptPlan = 0,      // "plan": 0 automatic, 1 radix, 2 bucketed, 3 one launch, 4 ranged
   kOptBwdFused,      // "bwd_fused": 1 = both gradients in one backward pass
   kOptGwStaged,      // "gw_staged": 0 = grad_w pass reads grad_out per wave instead of via LDS
   kOptForceScalar,   // "force_scalar": 1 = element-wise (unvectorised) kernels
-  kOptBwdU,          // "bwd_u": backward vectors per lane per column step (0 = by D)
+  kOptBwdU,          // "bwd_u": backward vectors per lane per column step (0 = per pass, by D)
   kOptFwdTile,       // "fwd_tile": forward tile <U><R> (0 = by D)
   kOptFwdAtomicTile, // "fwd_atomic_tile"
   kOptFwdDetU,       // "fwd_det_u": forward vectors per lane per row (0 = by D)

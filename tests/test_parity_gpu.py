@@ -146,9 +146,10 @@ def test_bwd_grad_x_bitexact_grad_w_close(name, variant, kernel_options):
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 16384), (torch.float32, 4104),
                                      (torch.float16, 8200)])
 def test_bwd_grad_w_staged_equals_per_wave(dtype, D, kernel_options):
-    """The grad_w pass shares grad_out through LDS for tokens of 1-8 rows and reads it per wave
-    otherwise (longer segments, the out-of-range segment, or FMOE_GW_STAGED=0): both give the same
-    bits, and both meet the oracle's 1e-6 bar.  Row lengths are not multiples of the LDS slice."""
+    """At U = 4 the grad_w pass shares grad_out through LDS for tokens of 1-8 rows and reads it
+    per wave otherwise (longer segments, the out-of-range segment, or FMOE_GW_STAGED=0): both give
+    the same bits, and both meet the oracle's 1e-6 bar.  Row lengths are not multiples of the LDS
+    slice.  U = 4 is set: by row length the pass takes it only from 24 KiB rows."""
     rng = np.random.default_rng(17)
     T, E = 300, 37
     per_token = rng.integers(0, 13, T)          # 0..12 rows: both paths occur
@@ -164,7 +165,7 @@ def test_bwd_grad_w_staged_equals_per_wave(dtype, D, kernel_options):
     xd, idd, wd = _to_dev(experts, idx, w)
     got = {}
     for staged in ("1", "0"):
-        kernel_options(gw_staged=int(staged))
+        kernel_options(gw_staged=int(staged), bwd_u=4)
         wg = wd.clone().requires_grad_(True)
         out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wg, (T, D))
         (got[staged],) = torch.autograd.grad(out, [wg], go.to(DEV))
