@@ -74,6 +74,17 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _c_int, _c_i64, _c_vp, _c_vp, _c_int, _c_vp],
     ),
+    "fmoe_combine_small_max_rows": (_c_i64, []),
+    "fmoe_combine_fwd_small": (
+        _c_int,
+        [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_int, _c_vp, _c_int,
+         _c_i64, _c_i64, _c_int, _c_vp, _c_int, _c_i64, _c_int, _c_vp, _c_vp],
+    ),
+    "fmoe_combine_bwd_small": (
+        _c_int,
+        [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_int, _c_vp, _c_int,
+         _c_i64, _c_i64, _c_int, _c_vp, _c_int, _c_i64, _c_vp, _c_vp, _c_int, _c_vp],
+    ),
     "fmoe_permute_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "fmoe_permute_build": (
         _c_int,

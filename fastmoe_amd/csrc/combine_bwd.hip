@@ -18,7 +18,7 @@
 // (read streams only) run as two back-to-back launches rather than one fused kernel: HBM loses
 // about a tenth of its throughput when a kernel interleaves this much reading and writing at fine
 // grain, which costs more than reading grad_out (T * D, one k-th of X at top-k) a second time.
-#include "common.h"
+#include "plan.h"
 
 namespace fmoe {
 
@@ -268,6 +268,37 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_bwd_tok(const int32_t* __
   }
 }
 
+// Small inputs (at most kSmallRows rows) without a plan: one wave per packed row g, which
+// needs nothing but its own token id, expert and gate -- grad_X[g] = round(grad_out[t] * w[g])
+// and grad_w[g] = <X[g], grad_out[t]> with bwd_row_body, both in one launch.  With U chosen as for
+// the grad_w pass, both gradients equal the planned passes' bit for bit.
+template <typename TX, int V, int U, bool GX, bool GW, bool AL>
+__global__ __launch_bounds__(kGroup) void k_bwd_small(const HostTable meta,
+                                                      const void* __restrict__ idx, int idx_dtype,
+                                                      const void* __restrict__ w, int w_dtype,
+                                                      uint32_t N, uint32_t T,
+                                                      const TX* __restrict__ gout, int64_t gstride,
+                                                      TX* __restrict__ gx, void* __restrict__ gw,
+                                                      int gw_dtype, uint32_t D) {
+  __shared__ int off_lds[kMetaChunk + 1];
+  __shared__ uint64_t ptr_lds[kMetaChunk];
+  small_table_to_lds(meta, off_lds, ptr_lds);
+  __syncthreads();
+  const uint32_t row_bytes = D * (uint32_t)sizeof(TX);
+  for (uint32_t g = blockIdx.x * kWavesPerGroup + (uint32_t)uniform(threadIdx.x / kWave); g < N;
+       g += gridDim.x * kWavesPerGroup) {
+    const int64_t t = load_index(idx, idx_dtype, g);
+    if (t < 0 || t >= (int64_t)T) {  // out of range: zero gradients, as the plan's segment T
+      bwd_zero_row<TX, V, GX, GW>(g, gx, gw, gw_dtype, D);
+      continue;
+    }
+    const int e = expert_of_row32(off_lds, meta.count, (int)g);
+    const uint64_t src = ptr_lds[e] + (uint64_t)(g - (uint32_t)off_lds[e]) * (uint64_t)row_bytes;
+    bwd_row_body<TX, V, U, GX, GW, AL>(src, load_weight(w, w_dtype, g), (uint32_t)t, g, gout,
+                                       gstride, gx, gw, gw_dtype, D);
+  }
+}
+
 struct BwdArgs {
   const int32_t* status;
   const int32_t* row_ptr;
@@ -382,5 +413,124 @@ extern "C" int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t nu
     case FMOE_F16: return launch_bwd_x<f16_t>(a);
   }
   fmoe_host::set_error("fmoe_combine_bwd: bad x dtype %d", x_dtype);
+  return FMOE_EINVAL;
+}
+
+namespace fmoe {
+namespace {
+
+struct SmallBwdArgs {
+  HostTable meta;
+  const void* idx;
+  int idx_dtype;
+  const void* w;
+  int w_dtype;
+  int64_t N, T, D;
+  const void* gout;
+  int64_t gstride;
+  void* gx;
+  void* gw;
+  int gw_dtype;
+  bool aligned;
+  hipStream_t s;
+};
+
+template <typename TX, int V, int U, bool GX, bool GW, bool AL>
+int launch_bwd_small_k(const SmallBwdArgs& a) {
+  const unsigned blocks = (unsigned)((a.N + kWavesPerGroup - 1) / kWavesPerGroup);
+  hipLaunchKernelGGL((k_bwd_small<TX, V, U, GX, GW, AL>), dim3(blocks), dim3(kGroup), 0, a.s,
+                     a.meta, a.idx, a.idx_dtype, a.w, a.w_dtype, (uint32_t)a.N, (uint32_t)a.T,
+                     static_cast<const TX*>(a.gout), a.gstride, static_cast<TX*>(a.gx), a.gw,
+                     a.gw_dtype, (uint32_t)a.D);
+  return fmoe_host::check_launch("fmoe_combine_bwd_small");
+}
+
+template <typename TX, int V, int U, bool AL>
+int launch_bwd_small_g(const SmallBwdArgs& a) {
+  if (a.gx && a.gw) return launch_bwd_small_k<TX, V, U, true, true, AL>(a);
+  if (a.gx) return launch_bwd_small_k<TX, V, U, true, false, AL>(a);
+  return launch_bwd_small_k<TX, V, U, false, true, AL>(a);
+}
+
+// The planned passes' vector width and, for grad_w's reduction order, the grad_w pass's U.
+template <typename TX>
+int launch_bwd_small_x(const SmallBwdArgs& a) {
+  constexpr int V = vec16<TX>();
+  const int eb = (int)sizeof(TX);
+  const bool vec_ok = (a.D % V == 0) && ((uintptr_t)a.gout % 16 == 0) &&
+                      ((a.gstride * eb) % 16 == 0) && ((uintptr_t)a.gx % 16 == 0) &&
+                      fmoe_host::opt(fmoe_host::kOptForceScalar) == 0;
+  if (!vec_ok) return launch_bwd_small_g<TX, 1, 4, true>(a);
+  const int64_t row_bytes = a.D * eb;
+  int U = (int)fmoe_host::opt(fmoe_host::kOptBwdU);
+  if (U != 1 && U != 2 && U != 4) U = row_bytes >= 24576 ? 4 : (row_bytes >= 4096 ? 2 : 1);
+  if (!a.aligned) {
+    if (U == 4) return launch_bwd_small_g<TX, V, 4, false>(a);
+    if (U == 2) return launch_bwd_small_g<TX, V, 2, false>(a);
+    return launch_bwd_small_g<TX, V, 1, false>(a);
+  }
+  if (U == 4) return launch_bwd_small_g<TX, V, 4, true>(a);
+  if (U == 2) return launch_bwd_small_g<TX, V, 2, true>(a);
+  return launch_bwd_small_g<TX, V, 1, true>(a);
+}
+
+}  // namespace
+}  // namespace fmoe
+
+extern "C" int fmoe_combine_bwd_small(const int64_t* host_ptrs, const int64_t* host_rows,
+                                      int64_t num_experts, const void* d_indices, int idx_dtype,
+                                      const void* d_weights, int w_dtype, int64_t num_tokens,
+                                      int64_t hidden, int x_dtype, const void* d_grad_out,
+                                      int gout_dtype, int64_t gout_row_stride, void* d_grad_x,
+                                      void* d_grad_w, int gw_dtype, void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  FMOE_REQUIRE(num_tokens >= 1 && hidden >= 1, "fmoe_combine_bwd_small: bad sizes T=%lld D=%lld",
+               (long long)num_tokens, (long long)hidden);
+  if (num_tokens >= (int64_t(1) << 30) || hidden * 4 >= (int64_t(1) << 31)) {
+    fmoe_host::set_error("fmoe_combine_bwd_small: T=%lld / D=%lld exceed the 32-bit counters",
+                         (long long)num_tokens, (long long)hidden);
+    return FMOE_ERANGE;
+  }
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(x_dtype), "fmoe_combine_bwd_small: bad x dtype %d",
+               x_dtype);
+  FMOE_REQUIRE(gout_dtype == x_dtype,
+               "fmoe_combine_bwd_small: grad_out dtype %d must equal the expert dtype %d",
+               gout_dtype, x_dtype);
+  FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype), "fmoe_combine_bwd_small: bad index dtype %d",
+               idx_dtype);
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_combine_bwd_small: bad weight dtype %d",
+               w_dtype);
+  FMOE_REQUIRE(d_grad_w == nullptr || fmoe_host::is_float_dtype(gw_dtype),
+               "fmoe_combine_bwd_small: bad grad_w dtype %d", gw_dtype);
+  FMOE_REQUIRE(gout_row_stride >= 0, "fmoe_combine_bwd_small: negative grad_out row stride");
+  SmallBwdArgs a{};
+  const int64_t xb = x_dtype == FMOE_F32 ? 4 : 2;
+  int64_t N = 0;
+  if (int rc = small_host_table("fmoe_combine_bwd_small", host_ptrs, host_rows, num_experts,
+                                hidden * xb, &a.meta, &N, &a.aligned))
+    return rc;
+  if (N == 0 || (d_grad_x == nullptr && d_grad_w == nullptr)) return FMOE_OK;
+  FMOE_REQUIRE(d_indices && d_weights && d_grad_out,
+               "fmoe_combine_bwd_small: null indices / weights / grad_out");
+  a.idx = d_indices;
+  a.idx_dtype = idx_dtype;
+  a.w = d_weights;
+  a.w_dtype = w_dtype;
+  a.N = N;
+  a.T = num_tokens;
+  a.D = hidden;
+  a.gout = d_grad_out;
+  a.gstride = gout_row_stride;
+  a.gx = d_grad_x;
+  a.gw = d_grad_w;
+  a.gw_dtype = gw_dtype;
+  a.s = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case FMOE_F32: return launch_bwd_small_x<float>(a);
+    case FMOE_BF16: return launch_bwd_small_x<bf16_t>(a);
+    case FMOE_F16: return launch_bwd_small_x<f16_t>(a);
+  }
+  fmoe_host::set_error("fmoe_combine_bwd_small: bad x dtype %d", x_dtype);
   return FMOE_EINVAL;
 }

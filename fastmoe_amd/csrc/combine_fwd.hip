@@ -24,7 +24,7 @@
 // requests, but every add rounds to 16 bits (the reference kernel's behaviour with a bf16 output).
 #include <algorithm>
 
-#include "common.h"
+#include "plan.h"
 
 namespace fmoe {
 
@@ -127,6 +127,135 @@ __global__ __launch_bounds__(kGroup) void k_fwd_det(const int32_t* __restrict__ 
     else
       fwd_det_body<TX, TO, V, U, RB, false>(row_ptr, rec, out, out_stride, D, t, chunk,
                                             accumulate);
+  }
+}
+
+// ---- small inputs: the deterministic forward without a plan --------------------------------
+// For at most kSmallRows rows the plan is not worth its own launch.  Every workgroup stages the
+// token id of each row in LDS (-1 for an index outside [0, T)); a wave owns one (token, column
+// chunk) unit as in k_fwd_det and finds the token's rows by ballots over the staged ids in
+// ascending row order, compacting them through a 128-entry window and taking them 64 at a time.
+// Lanes look up their row's expert in an LDS copy of the argument table.  The rows are added in
+// ascending g with k_fwd_det's arithmetic, so the result is the same, bit for bit.
+static_assert(kMetaChunk == kGroup, "one expert per thread copies the argument table");
+template <typename TX, typename TO, int V, int U, bool AL>
+__global__ __launch_bounds__(kGroup) void k_fwd_small(const HostTable meta,
+                                                      const void* __restrict__ idx, int idx_dtype,
+                                                      const void* __restrict__ w, int w_dtype,
+                                                      uint32_t N, uint32_t T, uint32_t D,
+                                                      uint32_t chunks, TO* __restrict__ out,
+                                                      int64_t out_stride, int accumulate,
+                                                      int32_t* __restrict__ status) {
+  using VX = Vec<TX, V>;
+  using VO = Vec<TO, V>;
+  using raw_t = typename VX::raw_t;
+  constexpr int CW = kWave * V * U;
+  constexpr int R = AL ? 4 : 1;  // rows per batch of loads (one at a time for element loads)
+  __shared__ int tok[kSmallRows];
+  __shared__ int win[kWavesPerGroup][2 * kWave];
+  __shared__ int off_lds[kMetaChunk + 1];
+  __shared__ uint64_t ptr_lds[kMetaChunk];
+  __shared__ int invalid;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = uniform(tid / kWave);
+  if (tid == 0) invalid = 0;
+  small_table_to_lds(meta, off_lds, ptr_lds);
+  __syncthreads();
+  int bad = 0;
+  for (uint32_t g = tid; g < N; g += kGroup) {
+    const int64_t v = load_index(idx, idx_dtype, g);
+    const bool ok = v >= 0 && v < (int64_t)T;
+    tok[g] = ok ? (int)v : -1;
+    bad += ok ? 0 : 1;
+  }
+  if (blockIdx.x == 0 && bad) atomicAdd(&invalid, bad);
+  __syncthreads();
+  if (blockIdx.x == 0 && tid == 0) status[kStatusInvalid] = invalid;
+
+  const uint32_t xrow_bytes = D * (uint32_t)sizeof(TX);
+  const int ne = meta.count;
+  const uint32_t units = T * chunks;
+  for (uint32_t unit = blockIdx.x * kWavesPerGroup + (uint32_t)wave; unit < units;
+       unit += gridDim.x * kWavesPerGroup) {
+    const uint32_t t = unit / chunks;
+    const uint32_t chunk = unit - t * chunks;
+    const uint32_t col0 = chunk * CW + (uint32_t)lane * V;
+    uint32_t xoff[U], ooff[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      xoff[u] = (col0 + (uint32_t)u * kWave * V) * (uint32_t)sizeof(TX);
+      ooff[u] = (col0 + (uint32_t)u * kWave * V) * (uint32_t)sizeof(TO);
+    }
+    const rsrc_t ro = make_rsrc(out + (int64_t)t * out_stride, D * (uint32_t)sizeof(TO));
+    float acc[U][V];
+    if (accumulate) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) VO::cvt(VO::ld(ro, ooff[u]), acc[u]);
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[u][v] = 0.f;
+    }
+    int have = 0;  // rows in the window (wave-uniform)
+    int seen = 0;
+    for (uint32_t base = 0; base < N; base += kWave) {
+      const uint32_t g = base + (uint32_t)lane;
+      const bool hit = g < N && tok[g] == (int)t;
+      const uint64_t m = __ballot(hit);
+      if (hit) win[wave][have + lanes_below(m)] = (int)g;
+      have += __builtin_popcountll(m);
+      const bool last = base + kWave >= N;
+      while (have >= kWave || (last && have > 0)) {
+        const int cnt = have < kWave ? have : kWave;
+        LaneRecs lr;
+        lr.g = lane < cnt ? win[wave][lane] : 0;
+        if (lane < cnt) {
+          const int e = expert_of_row32(off_lds, ne, lr.g);
+          const uint64_t src =
+              ptr_lds[e] + (uint64_t)(uint32_t)(lr.g - off_lds[e]) * (uint64_t)xrow_bytes;
+          lr.src_lo = (uint32_t)src;
+          lr.src_hi = (uint32_t)(src >> 32);
+          lr.w_bits = __float_as_uint(load_weight(w, w_dtype, lr.g));
+        } else {
+          lr.src_lo = lr.src_hi = lr.w_bits = 0;
+        }
+        const int rest = have - cnt;  // at most 63 rows carried to the window's front
+        const int carry = lane < rest ? win[wave][cnt + lane] : 0;
+        if (lane < rest) win[wave][lane] = carry;
+        have = rest;
+        seen += cnt;
+        for (int i = 0; i < cnt; i += R) {
+          raw_t a[R][U];
+          float wr[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int ir = min(i + r, cnt - 1);
+            const rsrc_t rx = make_rsrc(lr.src(ir), i + r < cnt ? xrow_bytes : 0u);
+            wr[r] = lr.w(ir);
+#pragma unroll
+            for (int u = 0; u < U; ++u) a[r][u] = load_x<TX, V, AL>(rx, xoff[u]);
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            if (i + r < cnt) {
+#pragma unroll
+              for (int u = 0; u < U; ++u) {
+                float x[V];
+                VX::cvt(a[r][u], x);
+#pragma unroll
+                for (int v = 0; v < V; ++v) acc[u][v] = acc[u][v] + x[v] * wr[r];
+              }
+            }
+          }
+        }
+      }
+    }
+    if (accumulate && seen == 0) continue;  // nothing routed here: out keeps its contents
+#pragma unroll
+    for (int u = 0; u < U; ++u)  // columns >= D: dropped by range check
+      VO::template st<FMOE_OUT_CPOL>(ro, ooff[u], acc[u]);
   }
 }
 
@@ -517,6 +646,69 @@ static int launch_fwd_x(const FwdArgs& a, int out_dtype) {
   return FMOE_EINVAL;
 }
 
+
+// The small path: a grid of at most kSmallGroups workgroups strides over the (token, chunk) units,
+// so that the ids are staged at most that many times.
+constexpr unsigned kSmallGroups = 1024;
+
+struct SmallFwdArgs {
+  HostTable meta;
+  const void* idx;
+  int idx_dtype;
+  const void* w;
+  int w_dtype;
+  int64_t N, T, D;
+  void* out;
+  int64_t out_stride;
+  int accumulate;
+  int32_t* status;
+  bool aligned;
+  hipStream_t s;
+};
+
+template <typename TX, typename TO, int V, int U, bool AL>
+static int launch_small_k(const SmallFwdArgs& a) {
+  const int64_t CW = (int64_t)kWave * V * U;
+  const int64_t chunks = (a.D + CW - 1) / CW;
+  unsigned blocks;
+  if (int rc = grid_for(a.T * chunks, "fmoe_combine_fwd_small", &blocks)) return rc;
+  blocks = std::min(blocks, kSmallGroups);
+  hipLaunchKernelGGL((k_fwd_small<TX, TO, V, U, AL>), dim3(blocks), dim3(kGroup), 0, a.s, a.meta,
+                     a.idx, a.idx_dtype, a.w, a.w_dtype, (uint32_t)a.N, (uint32_t)a.T,
+                     (uint32_t)a.D, (uint32_t)chunks, static_cast<TO*>(a.out), a.out_stride,
+                     a.accumulate, a.status);
+  return fmoe_host::check_launch("fmoe_combine_fwd_small");
+}
+
+// 16-byte vectors when the output layout allows them (as launch_fwd_t), U by D (pick_u); rows
+// that are not 16-byte aligned take element loads one vector per lane.
+template <typename TX, typename TO>
+static int launch_small_t(const SmallFwdArgs& a) {
+  constexpr int V = vec16<TX>();
+  const int ob = (int)sizeof(TO) == 4 ? 4 : 2;
+  const int64_t vb = (int64_t)V * ob;
+  const bool vec_ok = (a.D % V == 0) && ((uintptr_t)a.out % vb == 0) &&
+                      ((a.out_stride * ob) % vb == 0) &&
+                      fmoe_host::opt(fmoe_host::kOptForceScalar) == 0;
+  if (!vec_ok) return launch_small_k<TX, TO, 1, 4, true>(a);
+  if (!a.aligned) return launch_small_k<TX, TO, V, 1, false>(a);
+  const int U = pick_u(a.D, V);
+  if (U == 4) return launch_small_k<TX, TO, V, 4, true>(a);
+  if (U == 2) return launch_small_k<TX, TO, V, 2, true>(a);
+  return launch_small_k<TX, TO, V, 1, true>(a);
+}
+
+template <typename TX>
+static int launch_small_x(const SmallFwdArgs& a, int out_dtype) {
+  switch (out_dtype) {
+    case FMOE_F32: return launch_small_t<TX, float>(a);
+    case FMOE_BF16: return launch_small_t<TX, bf16_t>(a);
+    case FMOE_F16: return launch_small_t<TX, f16_t>(a);
+  }
+  fmoe_host::set_error("fmoe_combine_fwd_small: bad out dtype %d", out_dtype);
+  return FMOE_EINVAL;
+}
+
 }  // namespace fmoe
 
 extern "C" int64_t fmoe_combine_fwd_workspace_bytes(int mode, int64_t num_tokens, int64_t hidden,
@@ -630,4 +822,60 @@ extern "C" int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indi
                                        a.s)
              : launch_acc_pass<f16_t>(false, acc, d_out, out_row_stride, hidden, num_tokens, 1,
                                       a.s);
+}
+
+extern "C" int64_t fmoe_combine_small_max_rows(void) { return fmoe::kSmallRows; }
+
+extern "C" int fmoe_combine_fwd_small(const int64_t* host_ptrs, const int64_t* host_rows,
+                                      int64_t num_experts, const void* d_indices, int idx_dtype,
+                                      const void* d_weights, int w_dtype, int64_t num_tokens,
+                                      int64_t hidden, int x_dtype, void* d_out, int out_dtype,
+                                      int64_t out_row_stride, int accumulate, int32_t* d_status,
+                                      void* stream) {
+  using namespace fmoe;
+  fmoe_host::clear_error();
+  FMOE_REQUIRE(num_tokens >= 1 && hidden >= 1, "fmoe_combine_fwd_small: bad sizes T=%lld D=%lld",
+               (long long)num_tokens, (long long)hidden);
+  if (num_tokens >= (int64_t(1) << 30) || hidden * 4 >= (int64_t(1) << 31)) {
+    fmoe_host::set_error("fmoe_combine_fwd_small: T=%lld / D=%lld exceed the 32-bit counters",
+                         (long long)num_tokens, (long long)hidden);
+    return FMOE_ERANGE;
+  }
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(x_dtype), "fmoe_combine_fwd_small: bad x dtype %d",
+               x_dtype);
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(out_dtype), "fmoe_combine_fwd_small: bad out dtype %d",
+               out_dtype);
+  FMOE_REQUIRE(fmoe_host::is_index_dtype(idx_dtype), "fmoe_combine_fwd_small: bad index dtype %d",
+               idx_dtype);
+  FMOE_REQUIRE(fmoe_host::is_float_dtype(w_dtype), "fmoe_combine_fwd_small: bad weight dtype %d",
+               w_dtype);
+  FMOE_REQUIRE(d_out && d_status, "fmoe_combine_fwd_small: null out / status");
+  FMOE_REQUIRE(out_row_stride >= hidden, "fmoe_combine_fwd_small: out row stride %lld < D %lld",
+               (long long)out_row_stride, (long long)hidden);
+  SmallFwdArgs a{};
+  const int64_t xb = x_dtype == FMOE_F32 ? 4 : 2;
+  int64_t N = 0;
+  if (int rc = small_host_table("fmoe_combine_fwd_small", host_ptrs, host_rows, num_experts,
+                                hidden * xb, &a.meta, &N, &a.aligned))
+    return rc;
+  FMOE_REQUIRE(N == 0 || (d_indices && d_weights), "fmoe_combine_fwd_small: null indices/weights");
+  a.idx = d_indices;
+  a.idx_dtype = idx_dtype;
+  a.w = d_weights;
+  a.w_dtype = w_dtype;
+  a.N = N;
+  a.T = num_tokens;
+  a.D = hidden;
+  a.out = d_out;
+  a.out_stride = out_row_stride;
+  a.accumulate = accumulate ? 1 : 0;
+  a.status = d_status;
+  a.s = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case FMOE_F32: return launch_small_x<float>(a, out_dtype);
+    case FMOE_BF16: return launch_small_x<bf16_t>(a, out_dtype);
+    case FMOE_F16: return launch_small_x<f16_t>(a, out_dtype);
+  }
+  fmoe_host::set_error("fmoe_combine_fwd_small: bad x dtype %d", x_dtype);
+  return FMOE_EINVAL;
 }

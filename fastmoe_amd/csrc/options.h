@@ -20,6 +20,8 @@ enum Opt {
   kOptFwdDetU,       // "fwd_det_u": forward vectors per lane per row (0 = by D)
   kOptFwdGrid,       // "fwd_grid": forward workgroups (0 = one wave per unit)
   kOptPlanGroups,    // "plan_groups": workgroups of the one-launch plan (0 = by N and T)
+  kOptSmall,         // "small": the host's choice of the one-launch small path (0 = by size,
+                     // 1 = never, 2 = whenever its limits allow)
   kOptCount
 };
 int64_t opt(int o);

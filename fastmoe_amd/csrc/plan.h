@@ -263,6 +263,56 @@ inline void fill_host_table(TokMetaArgs* m, const int64_t* host_ptrs, const int6
   m->max_rows = max_rows;
 }
 
+// ---- small inputs without a plan (fmoe_combine_fwd_small / fmoe_combine_bwd_small) ------------
+// Rows of the small path: every forward workgroup stages their token ids in LDS.
+constexpr int kSmallRows = 4096;
+
+// Host side of the small path: checks the (address, rows) pairs as fmoe_build_metadata does, fills
+// the argument table, returns the row count and whether every row is 16-byte aligned (the plan's
+// misaligned-flag rule: a nonempty expert's address, and row_bytes when it has several rows).
+inline int small_host_table(const char* who, const int64_t* host_ptrs, const int64_t* host_rows,
+                            int64_t E, int64_t row_bytes, HostTable* t, int64_t* n_rows,
+                            bool* aligned) {
+  FMOE_REQUIRE(host_ptrs && host_rows, "%s: null host table", who);
+  FMOE_REQUIRE(E >= 1 && E <= kMetaChunk, "%s: num_experts must be in [1, %d] (got %lld)", who,
+               kMetaChunk, (long long)E);
+  int64_t run = 0, mx = 0;
+  bool al = true;
+  for (int64_t e = 0; e < kMetaChunk; ++e) {
+    const int64_t n = e < E ? host_rows[e] : 0;
+    FMOE_REQUIRE(n >= 0, "%s: expert %lld has invalid row count %lld", who, (long long)e,
+                 (long long)n);
+    FMOE_REQUIRE(n == 0 || host_ptrs[e] != 0, "%s: expert %lld has rows but a null address", who,
+                 (long long)e);
+    if (n > kSmallRows - run) {
+      fmoe_host::set_error("%s: more than %d rows (the small path's limit)", who, kSmallRows);
+      return FMOE_ERANGE;
+    }
+    t->ptr[e] = e < E ? host_ptrs[e] : 0;
+    t->off[e] = (int32_t)run;
+    if (n > 0 && ((host_ptrs[e] & 15) || (n > 1 && (row_bytes & 15)))) al = false;
+    run += n;
+    mx = std::max(mx, n);
+  }
+  t->off[kMetaChunk] = (int32_t)run;
+  t->count = (int32_t)E;
+  t->max_rows = (int32_t)mx;
+  *n_rows = run;
+  *aligned = al;
+  return FMOE_OK;
+}
+
+// The argument table into LDS, one expert per thread (E <= kMetaChunk == the workgroup size).
+__device__ __forceinline__ void small_table_to_lds(const HostTable& t, int* off_lds,
+                                                   uint64_t* ptr_lds) {
+  const int e = threadIdx.x;
+  if (e < t.count) {
+    off_lds[e] = t.off[e];
+    ptr_lds[e] = (uint64_t)t.ptr[e];
+  }
+  if (e == 0) off_lds[t.count] = t.off[t.count];
+}
+
 // Largest e in [0, E) with off[e] <= g (int32 offsets, off[0] == 0 <= g < off[E]).
 __device__ __forceinline__ int expert_of_row32(const int* __restrict__ off, int E, int g) {
   int lo = 0, hi = E;  // invariant: off[lo] <= g < off[hi]

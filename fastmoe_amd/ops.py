@@ -500,6 +500,58 @@ def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
     _abi.check(rc, "fmoe_combine_fwd")
 
 
+# The one-launch small path (fmoe_combine_fwd_small / fmoe_combine_bwd_small): deterministic calls
+# of at most fmoe_combine_small_max_rows() rows over at most 256 experts, with no plan.  What it
+# saves is a training step's launches: its backward is one launch (both gradients, no plan) where
+# the planned step has metadata + plan, the grad_X pass and the grad_w pass.  A forward alone
+# gains nothing (a graph of one small kernel costs what one of two does), and each forward wave
+# scans the token id of every row, so the cost grows with T * N.  By default it is taken for calls
+# that a backward may follow, while T * N <= _SMALL_SCAN_LIMIT (graph-replayed fwd+bwd steps on
+# one MI355X: 17.6 -> 15.3 us at T=256, D=512, top-2, fp32; 24.3 -> 18.9 us at T=64, D=7168,
+# top-8, bf16; 31.9 -> 33.7 us at T=256, D=7168, top-8, past the limit).
+_SMALL_MAX_EXPERTS = 256
+_SMALL_SCAN_LIMIT = 1 << 17
+_SMALL_MAX_ROWS: list = []
+
+
+def _use_small(rows: int, num_tokens: int, num_experts: int, backward: bool) -> bool:
+    choice = _abi.option("small")
+    if choice == 1 or _abi.option("plan") != 0 or num_experts > _SMALL_MAX_EXPERTS or rows < 1:
+        return False
+    if not _SMALL_MAX_ROWS:
+        _SMALL_MAX_ROWS.append(int(_abi.lib().fmoe_combine_small_max_rows()))
+    if rows > _SMALL_MAX_ROWS[0]:
+        return False
+    return choice == 2 or (backward and rows * num_tokens <= _SMALL_SCAN_LIMIT)
+
+
+def _small_tables(checked) -> tuple:
+    """The (address, rows) host tables of the small path, from _check_experts' result."""
+    return _host_table(checked[4]), _host_table(checked[3])
+
+
+def _launch_fwd_small(tables, num_experts: int, idx: torch.Tensor, w: torch.Tensor,
+                      x_dtype: torch.dtype, out: torch.Tensor, accumulate: bool) -> torch.Tensor:
+    """fmoe_combine_fwd_small into ``out``; returns its status word (rows with an index outside
+    [0, T)) on the device."""
+    T, D = out.shape
+    status = torch.empty(1, dtype=torch.int32, device=out.device)
+    with torch.cuda.device(out.device), _span("fwd_small"):
+        rc = _abi.lib().fmoe_combine_fwd_small(
+            tables[0], tables[1], num_experts, idx.data_ptr(), _INDEX_CODES[idx.dtype],
+            w.data_ptr(), _FLOAT_CODES[w.dtype], T, D, _FLOAT_CODES[x_dtype], out.data_ptr(),
+            _FLOAT_CODES[out.dtype], out.stride(0) if T > 1 else D, 1 if accumulate else 0,
+            status.data_ptr(), _stream_handle(out.device))
+    _abi.check(rc, "fmoe_combine_fwd_small")
+    return status
+
+
+def _check_small_status(status: torch.Tensor, num_tokens: int) -> None:
+    bad = int(status[0])
+    if bad:
+        raise IndexError(f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})")
+
+
 def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None, *, mode=None,
                            validate=None):
     """In-place combine into ``out`` (accumulates; mirrors ops.py:277-310)."""
@@ -510,8 +562,16 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
         idx, w = _routing_args(indices, weights, metadata.num_rows, metadata.device)
     else:
         checked = _check_experts(expert_tensors)
-        idx, w = _routing_args(indices, weights, sum(checked[3]), checked[1])
-        if code == _abi.MODE_DET and sum(checked[3]) > 0:
+        rows = sum(checked[3])
+        idx, w = _routing_args(indices, weights, rows, checked[1])
+        if code == _abi.MODE_DET and _use_small(rows, T, len(checked[3]), backward=False):
+            _check_out(out, None, checked[2], checked[1])
+            status = _launch_fwd_small(_small_tables(checked), len(checked[3]), idx, w,
+                                       checked[0], out, accumulate=True)
+            if _validate_default(validate):
+                _check_small_status(status, T)
+            return out
+        if code == _abi.MODE_DET and rows > 0:
             metadata, plan = _metadata_and_plan(expert_tensors, checked, idx, w, T, validate)
         else:
             metadata = _metadata(expert_tensors, checked)
@@ -544,10 +604,18 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
     rows = sum(sizes)
     idx, w = _routing_args(indices, weights, rows, dev)
     use_slots = slots is not None and rows == T * slots[1] and slots[1] <= 64
-    plan = None
+    plan = meta = small = None
     if rows == 0:
         meta = _metadata(expert_tensors, checked)
         out = torch.zeros(shape, dtype=dtype, device=dev)
+    elif code == _abi.MODE_DET and _use_small(
+            rows, T, len(sizes), w_grad or any(getattr(ctx, "needs_input_grad", ()))):
+        # one launch, no plan; the backward is one launch too
+        small = _small_tables(checked)
+        out = torch.empty(shape, dtype=dtype, device=dev)
+        status = _launch_fwd_small(small, len(sizes), idx, w, dtype, out, accumulate=False)
+        if _validate_default(validate):
+            _check_small_status(status, T)
     elif code == _abi.MODE_DET:
         # metadata and plan in one call; every output row is written exactly once (tokens
         # without rows get zeros), so out needs no zero-fill
@@ -572,8 +640,9 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
     else:
         ctx.save_for_backward(idx, w)
     ctx.plan = plan
+    ctx.small = small
     # what a deferred plan needs (device arrays only: no reference to the expert tensors)
-    ctx.meta_arrays = (meta.ptr_table, meta.offsets_full) if plan is None else None
+    ctx.meta_arrays = (meta.ptr_table, meta.offsets_full) if plan is None and meta else None
     ctx.slots = (slots[0], slots[1]) if (use_slots and plan is None) else None
     ctx.sizes = sizes
     ctx.hidden = hidden
@@ -599,7 +668,8 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
               for n, need in zip(sizes, needs_x)]
         return gw, gx
     plan = ctx.plan
-    if plan is None:  # atomic forward: the plan now
+    small = getattr(ctx, "small", None)
+    if plan is None and small is None:  # atomic forward: the plan now
         ptr_table, offsets_full = ctx.meta_arrays
         if ctx.slots is not None:
             plan = _build_plan_from_slots_raw(ptr_table, offsets_full, len(sizes), N,
@@ -629,7 +699,16 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
 
     gx_ptr = gx.data_ptr() if gx is not None else None
     gw_ptr = gw.data_ptr() if gw is not None else None
-    if gx_ptr and gw_ptr and not _abi.option("bwd_fused"):
+    if small is not None:
+        # both gradients (or either) in one launch, no plan
+        with torch.cuda.device(dev), _span("bwd_small"):
+            rc = lib.fmoe_combine_bwd_small(
+                small[0], small[1], len(sizes), idx.data_ptr(), _INDEX_CODES[idx.dtype],
+                w.data_ptr(), _FLOAT_CODES[w.dtype], T, D, _FLOAT_CODES[ctx.x_dtype],
+                go.data_ptr(), _FLOAT_CODES[go.dtype], go.stride(0) if T > 1 else D, gx_ptr,
+                gw_ptr, _FLOAT_CODES[w.dtype], stream)
+        _abi.check(rc, "fmoe_combine_bwd_small")
+    elif gx_ptr and gw_ptr and not _abi.option("bwd_fused"):
         # The grad_X (write) and grad_w (read) passes, one call each -- the same two launches
         # fmoe_combine_bwd makes when given both outputs, issued separately so each is timed.
         launch("bwd_gx", gx_ptr, None)

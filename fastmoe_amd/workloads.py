@@ -138,6 +138,7 @@ def kernel_bytes(T: int, D: int, N: int, x_bytes: int, out_bytes: int,
     bwd_gx               : read grad_out (T*D) + write grad_X (N*D) + read idx and w per row
     bwd_gw               : read grad_out (T*D) + read X (N*D) + read idx, write grad_w per row
     bwd                  : both gradients in one pass (as ``algorithmic_bytes``)
+    fwd_small, bwd_small : the one-launch small path's forward and backward (as fwd_det, bwd)
     permute_gather       : read x (T*D) + write the packed rows (N*D) + read slot_pos per slot
     """
     fwd, bwd = algorithmic_bytes(T, D, N, x_bytes, out_bytes, gate_bytes)
@@ -148,4 +149,6 @@ def kernel_bytes(T: int, D: int, N: int, x_bytes: int, out_bytes: int,
         "bwd_gx": T * D * x_bytes + N * D * x_bytes + N * (8 + gate_bytes),
         "bwd_gw": T * D * x_bytes + N * D * x_bytes + N * (8 + gate_bytes),
         "bwd": bwd,
+        "fwd_small": fwd,
+        "bwd_small": bwd,
     }

@@ -27,6 +27,8 @@
  *   fmoe_combine_fwd       <- _launch_grouped_kernel + Triton  src/fastmoe/kernels/ops.py:277-310
  *                             _grouped_weighted_scatter_add_kernel  ops.py:57-194
  *   fmoe_combine_bwd       <- GroupedWeightedScatterAdd.backward    ops.py:333-359
+ *   fmoe_combine_fwd_small / fmoe_combine_bwd_small <- the same three, for at most 4096 rows:
+ *                             one launch per direction and no plan
  *   fmoe_build_plan        <- no counterpart: the token-major inverse of the scatter index that the
  *                             deterministic combine and the backward read (ops.py:344 gathers by
  *                             scatter index on the fly instead)
@@ -106,6 +108,9 @@ FMOE_API const char* fmoe_last_error(void);
  *   "bwd_u", "fwd_tile", "fwd_atomic_tile", "fwd_det_u", "fwd_grid": tile shapes (0 = by D,
  *                                      and for "fwd_tile" by the rows per token too)
  *   "plan_groups"     [FMOE_PLAN_GROUPS] workgroups of the one-launch plan (0 = by N and T)
+ *   "small"           [FMOE_SMALL]     the Python host's use of fmoe_combine_fwd_small /
+ *                                      fmoe_combine_bwd_small: 0 = by size, 1 = never, 2 = whenever
+ *                                      their limits allow (the library itself does not read it)
  * fmoe_set_option returns FMOE_EINVAL for an unknown name; *previous (if not NULL) gets the old
  * value.  Not synchronised with launches in flight on other threads.
  */
@@ -282,6 +287,37 @@ FMOE_API int fmoe_combine_fwd_noalloc(const int64_t* host_ptrs, const int64_t* h
 FMOE_API int fmoe_combine_bwd(const void* d_plan, int64_t num_rows, int64_t num_tokens, int64_t hidden,
                      int x_dtype, const void* d_grad_out, int gout_dtype, int64_t gout_row_stride,
                      void* d_grad_x, void* d_grad_w, int gw_dtype, void* stream);
+
+/*
+ * Small inputs: the deterministic forward and the backward of at most
+ * fmoe_combine_small_max_rows() rows (4096) over at most 256 experts, one launch each and no plan
+ * (they replace the same reference code as fmoe_combine_fwd in FMOE_MODE_DET and
+ * fmoe_combine_bwd: src/fastmoe/kernels/ops.py:57-194, :277-310 and :333-359).  Results equal
+ * fmoe_build_metadata_and_plan + fmoe_combine_fwd(FMOE_MODE_DET) and fmoe_combine_bwd bit for bit;
+ * the saving is the plan's launch, which dominates such calls.
+ *
+ * host_ptrs / host_rows / num_experts : the experts' (address, rows) pairs, as in
+ *              fmoe_build_metadata (read on the host, passed in the kernel arguments).
+ * d_indices, d_weights : [N] scatter index (FMOE_I64 / FMOE_I32) and gates (any float dtype).
+ * fmoe_combine_fwd_small: out, out_row_stride, accumulate and the dtypes as in fmoe_combine_fwd;
+ *              d_status [1] int32 receives the number of rows whose index lies outside [0, T)
+ *              (those rows are skipped), written by the launch.
+ * fmoe_combine_bwd_small: d_grad_out, d_grad_x, d_grad_w and the dtypes as in fmoe_combine_bwd;
+ *              both outputs (or either) come from one kernel.
+ * More rows or experts return FMOE_ERANGE / FMOE_EINVAL before touching the GPU.
+ */
+FMOE_API int64_t fmoe_combine_small_max_rows(void);
+FMOE_API int fmoe_combine_fwd_small(const int64_t* host_ptrs, const int64_t* host_rows,
+                           int64_t num_experts, const void* d_indices, int idx_dtype,
+                           const void* d_weights, int w_dtype, int64_t num_tokens, int64_t hidden,
+                           int x_dtype, void* d_out, int out_dtype, int64_t out_row_stride,
+                           int accumulate, int32_t* d_status, void* stream);
+FMOE_API int fmoe_combine_bwd_small(const int64_t* host_ptrs, const int64_t* host_rows,
+                           int64_t num_experts, const void* d_indices, int idx_dtype,
+                           const void* d_weights, int w_dtype, int64_t num_tokens, int64_t hidden,
+                           int x_dtype, const void* d_grad_out, int gout_dtype,
+                           int64_t gout_row_stride, void* d_grad_x, void* d_grad_w, int gw_dtype,
+                           void* stream);
 
 /*
  * Dispatch-side permutation: the routing slots of T tokens x top_k choices grouped by expert

@@ -115,6 +115,36 @@ def test_combine_entry_points_reject_bad_arguments():
     assert rc == _abi.EINVAL
 
 
+def test_small_entry_points_reject_calls_beyond_their_limits():
+    """fmoe_combine_fwd_small / _bwd_small check their limits on the host, before any launch."""
+    lib = _abi.lib()
+    dev = 0x10000
+    limit = lib.fmoe_combine_small_max_rows()
+    assert limit == 4096
+    one = (ctypes.c_int64 * 1)(dev * 256)
+
+    def fwd(rows, E=1, ptrs=one, status=dev, idt=_abi.I64, T=4):
+        return lib.fmoe_combine_fwd_small(ptrs, rows, E, dev, idt, dev, _abi.F32, T, 8, _abi.F32,
+                                          dev, _abi.F32, 8, 0, status, None)
+
+    assert fwd((ctypes.c_int64 * 1)(limit + 1)) == _abi.ERANGE
+    assert b"small path" in lib.fmoe_last_error()
+    assert fwd((ctypes.c_int64 * 1)(-1)) == _abi.EINVAL
+    assert fwd((ctypes.c_int64 * 1)(4), ptrs=(ctypes.c_int64 * 1)(0)) == _abi.EINVAL  # null rows
+    assert fwd((ctypes.c_int64 * 1)(4), status=None) == _abi.EINVAL
+    assert fwd((ctypes.c_int64 * 1)(4), idt=_abi.F32) == _abi.EINVAL
+    assert fwd((ctypes.c_int64 * 1)(4), T=1 << 30) == _abi.ERANGE
+    many = (ctypes.c_int64 * 257)(*([dev * 256] * 257))
+    rows = (ctypes.c_int64 * 257)(*([1] * 257))
+    assert fwd(rows, E=257, ptrs=many) == _abi.EINVAL
+    rc = lib.fmoe_combine_bwd_small(many, rows, 257, dev, _abi.I64, dev, _abi.F32, 4, 8, _abi.F32,
+                                    dev, _abi.F32, 8, dev, None, _abi.F32, None)
+    assert rc == _abi.EINVAL and b"num_experts" in lib.fmoe_last_error()
+    rc = lib.fmoe_combine_bwd_small(one, (ctypes.c_int64 * 1)(4), 1, dev, _abi.I64, dev, _abi.F32,
+                                    4, 8, _abi.BF16, dev, _abi.F32, 8, dev, None, _abi.F32, None)
+    assert rc == _abi.EINVAL and b"grad_out dtype" in lib.fmoe_last_error()
+
+
 def test_metadata_and_plan_entry_points_reject_bad_arguments():
     """The one-call metadata + plan entry points check every argument on the host, including row
     totals that the kernel-argument table (32-bit offsets) cannot hold."""

@@ -94,15 +94,50 @@ class FakeLib:
         self.calls.append(("bwd", N, T, D, xdt, gstride, gx is not None, gw is not None, gwdt))
         return 0
 
+    def fmoe_combine_small_max_rows(self):
+        return self.real.fmoe_combine_small_max_rows()
 
-@pytest.fixture
-def fake(monkeypatch):
+    def fmoe_combine_fwd_small(self, host_ptrs, host_rows, E, idx, idt, w, wdt, T, D, xdt, out,
+                               odt, ostride, acc, status, stream):
+        assert isinstance(E, int) and len(host_ptrs) == E and len(host_rows) == E
+        assert idt in (_abi.I64, _abi.I32) and wdt in (_abi.F32, _abi.BF16, _abi.F16)
+        assert all(isinstance(p, int) for p in (idx, w, out, status))
+        self.calls.append(("fwd_small", E, list(host_rows), T, D, idt, wdt, xdt, odt, ostride,
+                           acc))
+        return 0
+
+    def fmoe_combine_bwd_small(self, host_ptrs, host_rows, E, idx, idt, w, wdt, T, D, xdt, gout,
+                               gdt, gstride, gx, gw, gwdt, stream):
+        assert isinstance(E, int) and len(host_ptrs) == E and len(host_rows) == E
+        assert all(isinstance(p, int) for p in (idx, w, gout)) and gdt == xdt
+        self.calls.append(("bwd_small", E, list(host_rows), T, D, xdt, gstride, gx is not None,
+                           gw is not None, gwdt))
+        return 0
+
+
+def _fake_lib(monkeypatch):
     f = FakeLib()
     monkeypatch.setattr(_abi, "lib", lambda: f)
     monkeypatch.setattr(ops, "_require_cuda", lambda t, what: None)
     monkeypatch.setattr(ops, "_stream_handle", lambda dev: 0)
     monkeypatch.setattr(torch.cuda, "device", lambda dev: contextlib.nullcontext())
     return f
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    """The planned path (metadata + plan, forward, backward passes): the small path is off."""
+    f = _fake_lib(monkeypatch)
+    with _abi.options(small=1):
+        yield f
+
+
+@pytest.fixture
+def fake_small(monkeypatch):
+    """The default choice, which takes the one-launch small path for these sizes."""
+    f = _fake_lib(monkeypatch)
+    with _abi.options(small=0):
+        yield f
 
 
 def _experts(dtype=torch.bfloat16, sizes=(3, 0, 5), D=16):
@@ -256,3 +291,70 @@ def test_weighted_scatter_add_single_tensor(fake):
     out = fastmoe_amd.weighted_scatter_add(src, torch.randint(0, 5, (10,)), torch.rand(10), (5, 4))
     assert out.shape == (5, 4)
     assert fake.calls[0] == ("metadata_plan", 1, [10], 5, 16, _abi.I64, _abi.F32)
+
+
+def test_small_path_is_one_launch_per_direction(fake_small):
+    xs = [x.requires_grad_(True) for x in _experts()]
+    w = torch.rand(8, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, 4, (8,)), w, (4, 16))
+    grads = torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
+    assert [c[0] for c in fake_small.calls] == ["fwd_small", "bwd_small"]
+    assert fake_small.calls[0] == ("fwd_small", 3, [3, 0, 5], 4, 16, _abi.I64, _abi.F32,
+                                   _abi.BF16, _abi.BF16, 16, 0)
+    assert fake_small.calls[1] == ("bwd_small", 3, [3, 0, 5], 4, 16, _abi.BF16, 16, True, True,
+                                   _abi.F32)
+    assert grads[0].shape == (8,) and [g.shape[0] for g in grads[1:]] == [3, 0, 5]
+
+
+def test_small_path_backward_of_one_gradient(fake_small):
+    xs = _experts()
+    w = torch.rand(8, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, 4, (8,)), w, (4, 16))
+    torch.autograd.grad(out, [w], torch.ones(4, 16, dtype=torch.bfloat16))
+    assert fake_small.calls[1][7:9] == (False, True)
+
+
+def test_small_path_in_place_accumulates(fake_small):
+    """An in-place call has no backward: the plan path by default, the small path when forced."""
+    args = (_experts(torch.float32), torch.randint(0, 4, (8,), dtype=torch.int32), torch.rand(8),
+            (4, 16))
+    fastmoe_amd.grouped_weighted_scatter_add(*args, out=torch.zeros(4, 16))
+    assert "fwd_small" not in [c[0] for c in fake_small.calls]
+    fake_small.calls.clear()
+    with _abi.options(small=2):
+        fastmoe_amd.grouped_weighted_scatter_add(*args, out=torch.zeros(4, 16))
+    assert fake_small.calls == [("fwd_small", 3, [3, 0, 5], 4, 16, _abi.I32, _abi.F32, _abi.F32,
+                                 _abi.F32, 16, 1)]
+
+
+def test_small_path_only_when_a_backward_may_follow(fake_small):
+    fastmoe_amd.grouped_weighted_scatter_add(_experts(), torch.randint(0, 4, (8,)), torch.rand(8),
+                                             (4, 16))
+    assert [c[0] for c in fake_small.calls] == ["metadata_plan", "fwd"]
+
+
+@pytest.mark.parametrize("case", ["off", "plan_forced", "atomic", "experts", "rows", "scan"])
+def test_small_path_not_taken(fake_small, case):
+    """The small path stays out of forced plans, atomic modes, more than 256 experts or 4096 rows,
+    and (by default) calls whose forward scan T * N exceeds 2^17 -- here with gradients wanted."""
+    sizes, T, opts, mode = (3, 0, 5), 4, {}, None
+    if case == "off":
+        opts = {"small": 1}
+    elif case == "plan_forced":
+        opts = {"plan": 3}
+    elif case == "atomic":
+        mode = "atomic"
+    elif case == "experts":
+        sizes = (1,) * 257
+    elif case == "rows":
+        sizes = (4097,)
+    else:
+        T = 1 << 15  # T * N = 2^18
+    xs = [x.requires_grad_(True) for x in _experts(sizes=sizes, D=4)]
+    N = sum(sizes)
+    with _abi.options(**opts):
+        fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, T, (N,)),
+                                                 torch.rand(N, requires_grad=True), (T, 4),
+                                                 mode=mode)
+    kinds = [c[0] for c in fake_small.calls]
+    assert "fwd_small" not in kinds and ("fwd" in kinds)
