@@ -79,9 +79,12 @@ def test_campaign_autograd(kernel_options):
         # radix / bucketed / one launch / ranged / automatic (a forced path whose limits do not
         # hold falls back to the automatic choice)
         plan = 1 if r < 0.2 else (2 if r < 0.3 else (3 if r < 0.45 else (4 if r < 0.65 else 0)))
-        kernel_options(plan=plan, bwd_fused=1 if fused else 0)
+        # with the automatic plan, half the cases force the one-launch small path where its
+        # limits (4096 rows, 256 experts) allow it; the others take the default choice
+        small = 2 if plan == 0 and rng.random() < 0.5 else 0
+        kernel_options(plan=plan, bwd_fused=1 if fused else 0, small=small)
         label = (f"autograd case {case}: T={T} N={N} E={E} D={D} {routing} {xdt} {wdt} {idt} "
-                 f"plan={plan} fused={fused}")
+                 f"plan={plan} fused={fused} small={small}")
         gen = torch.Generator().manual_seed(1101 * 1000 + case)
         idx_t = torch.from_numpy(np.asarray(idx, dtype=np.int64)).to(idt)
         w = torch.rand(N, generator=gen).to(wdt)
