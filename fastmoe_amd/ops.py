@@ -501,20 +501,19 @@ def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
 
 
 # The one-launch small path (fmoe_combine_fwd_small / fmoe_combine_bwd_small): deterministic calls
-# of at most fmoe_combine_small_max_rows() rows over at most 256 experts, with no plan.  What it
-# saves is a training step's launches: its backward is one launch (both gradients, no plan) where
-# the planned step has metadata + plan, the grad_X pass and the grad_w pass.  A forward alone
-# gains nothing (a graph of one small kernel costs what one of two does), and each forward wave
-# scans the token id of every row, so the cost grows with T * N.  By default it is taken for calls
-# that a backward may follow, while T * N <= _SMALL_SCAN_LIMIT (graph-replayed fwd+bwd steps on
-# one MI355X: 17.6 -> 15.3 us at T=256, D=512, top-2, fp32; 24.3 -> 18.9 us at T=64, D=7168,
-# top-8, bf16; 31.9 -> 33.7 us at T=256, D=7168, top-8, past the limit).
+# of at most fmoe_combine_small_max_rows() rows over at most 256 experts, with no plan.  A training
+# step is two launches instead of four (metadata + plan, forward, grad_X pass, grad_w pass), and a
+# forward saves the plan's dependent launch.  Each forward wave scans the token id of every row, so
+# the cost grows with T * N: it is taken while T * N <= _SMALL_SCAN_LIMIT (graph-replayed steps on
+# one MI355X, planned -> small: fwd+bwd 17.6 -> 15.3 us at T=256, D=512, top-2, fp32 and 24.3 ->
+# 18.9 us at T=64, D=7168, top-8, bf16; forward 19.0 -> 14.8 us at T=128, D=16384, top-8; past
+# the limit, fwd+bwd 31.9 -> 33.7 us at T=256, D=7168, top-8).
 _SMALL_MAX_EXPERTS = 256
 _SMALL_SCAN_LIMIT = 1 << 17
 _SMALL_MAX_ROWS: list = []
 
 
-def _use_small(rows: int, num_tokens: int, num_experts: int, backward: bool) -> bool:
+def _use_small(rows: int, num_tokens: int, num_experts: int) -> bool:
     choice = _abi.option("small")
     if choice == 1 or _abi.option("plan") != 0 or num_experts > _SMALL_MAX_EXPERTS or rows < 1:
         return False
@@ -522,7 +521,7 @@ def _use_small(rows: int, num_tokens: int, num_experts: int, backward: bool) -> 
         _SMALL_MAX_ROWS.append(int(_abi.lib().fmoe_combine_small_max_rows()))
     if rows > _SMALL_MAX_ROWS[0]:
         return False
-    return choice == 2 or (backward and rows * num_tokens <= _SMALL_SCAN_LIMIT)
+    return choice == 2 or rows * num_tokens <= _SMALL_SCAN_LIMIT
 
 
 def _small_tables(checked) -> tuple:
@@ -564,7 +563,7 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
         checked = _check_experts(expert_tensors)
         rows = sum(checked[3])
         idx, w = _routing_args(indices, weights, rows, checked[1])
-        if code == _abi.MODE_DET and _use_small(rows, T, len(checked[3]), backward=False):
+        if code == _abi.MODE_DET and _use_small(rows, T, len(checked[3])):
             _check_out(out, None, checked[2], checked[1])
             status = _launch_fwd_small(_small_tables(checked), len(checked[3]), idx, w,
                                        checked[0], out, accumulate=True)
@@ -608,8 +607,7 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
     if rows == 0:
         meta = _metadata(expert_tensors, checked)
         out = torch.zeros(shape, dtype=dtype, device=dev)
-    elif code == _abi.MODE_DET and _use_small(
-            rows, T, len(sizes), w_grad or any(getattr(ctx, "needs_input_grad", ()))):
+    elif code == _abi.MODE_DET and _use_small(rows, T, len(sizes)):
         # one launch, no plan; the backward is one launch too
         small = _small_tables(checked)
         out = torch.empty(shape, dtype=dtype, device=dev)

@@ -315,28 +315,23 @@ def test_small_path_backward_of_one_gradient(fake_small):
 
 
 def test_small_path_in_place_accumulates(fake_small):
-    """An in-place call has no backward: the plan path by default, the small path when forced."""
-    args = (_experts(torch.float32), torch.randint(0, 4, (8,), dtype=torch.int32), torch.rand(8),
-            (4, 16))
-    fastmoe_amd.grouped_weighted_scatter_add(*args, out=torch.zeros(4, 16))
-    assert "fwd_small" not in [c[0] for c in fake_small.calls]
-    fake_small.calls.clear()
-    with _abi.options(small=2):
-        fastmoe_amd.grouped_weighted_scatter_add(*args, out=torch.zeros(4, 16))
+    fastmoe_amd.grouped_weighted_scatter_add(_experts(torch.float32),
+                                             torch.randint(0, 4, (8,), dtype=torch.int32),
+                                             torch.rand(8), (4, 16), out=torch.zeros(4, 16))
     assert fake_small.calls == [("fwd_small", 3, [3, 0, 5], 4, 16, _abi.I32, _abi.F32, _abi.F32,
                                  _abi.F32, 16, 1)]
 
 
-def test_small_path_only_when_a_backward_may_follow(fake_small):
+def test_small_path_forward_only(fake_small):
     fastmoe_amd.grouped_weighted_scatter_add(_experts(), torch.randint(0, 4, (8,)), torch.rand(8),
                                              (4, 16))
-    assert [c[0] for c in fake_small.calls] == ["metadata_plan", "fwd"]
+    assert [c[0] for c in fake_small.calls] == ["fwd_small"]
 
 
 @pytest.mark.parametrize("case", ["off", "plan_forced", "atomic", "experts", "rows", "scan"])
 def test_small_path_not_taken(fake_small, case):
     """The small path stays out of forced plans, atomic modes, more than 256 experts or 4096 rows,
-    and (by default) calls whose forward scan T * N exceeds 2^17 -- here with gradients wanted."""
+    and (by default) calls whose forward scan T * N exceeds 2^17."""
     sizes, T, opts, mode = (3, 0, 5), 4, {}, None
     if case == "off":
         opts = {"small": 1}

@@ -86,10 +86,10 @@ def test_small_path_equals_planned_path_and_oracle(case, kernel_options):
     idd, wd, god = idx.to(DEV), w.to(DEV), go.to(DEV)
     print(f"small-path case {case}: T={T} D={D} N={N} E={E}", flush=True)
     kernel_options(small=2)
-    assert ops._use_small(N, T, E, True)
+    assert ops._use_small(N, T, E)
     got = _fwd_bwd(xd, idd, wd, god, T, D)
     kernel_options(small=1)
-    assert not ops._use_small(N, T, E, True)
+    assert not ops._use_small(N, T, E)
     ref = _fwd_bwd(xd, idd, wd, god, T, D)
     for a, b in zip(got, ref):  # out, grad_w, grad_X
         np.testing.assert_array_equal(bits(a), bits(b))
