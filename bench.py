@@ -324,8 +324,10 @@ def _event_kernels(step, steps):
     return timer.summary(), backlog
 
 
-def _graph_ms(capture_step, steps, warmup):
-    """Replay time of one step captured as a HIP graph: (ms per replay, wall ms, error or None)."""
+def _graph_ms(capture_step, steps, warmup, after=None):
+    """Replay time of one step captured as a HIP graph: (ms per replay, wall ms, error or None,
+    ``after(captured outputs)`` or None).  ``after`` runs once the timed replays are done, while
+    the graph (and so its outputs) is alive."""
     import torch
 
     try:
@@ -338,15 +340,37 @@ def _graph_ms(capture_step, steps, warmup):
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            capture_step()
+            static = capture_step()
         for _ in range(warmup):
             graph.replay()
         torch.cuda.synchronize()
     except Exception as exc:  # capture unsupported: the caller reports eager numbers only
-        return None, None, f"{type(exc).__name__}: {exc}"
+        return None, None, f"{type(exc).__name__}: {exc}", None
     ms, wall_ms = _timed(graph.replay, steps)
-    del graph
-    return ms, wall_ms, None
+    checked = after(static) if after is not None else None
+    del graph, static
+    return ms, wall_ms, None, checked
+
+
+def _replay_matches_eager(static, eager_step, exact_out):
+    """Compares the captured step's outputs after its last replay with one eager step through the
+    public autograd API: (all compared bits equal, what was compared).  ``exact_out`` False (the
+    atomic modes, whose fp32 summation order varies run to run) leaves the output out."""
+    import torch
+
+    torch.cuda.synchronize()
+    eager = eager_step()
+    torch.cuda.synchronize()
+    first = 0 if exact_out else 1
+    pairs = list(zip(static, eager))[first:]
+    same = len(static) == len(eager) and all(
+        a.shape == b.shape and a.dtype == b.dtype
+        and torch.equal(a.reshape(-1).view(torch.uint8), b.reshape(-1).view(torch.uint8))
+        for a, b in pairs)
+    what = ["out"] if exact_out else []
+    if len(static) > 1:
+        what += ["grad_w", "every expert's grad_X"]
+    return same, "bits of " + ", ".join(what)
 
 
 def _autograd_floor_ms(wl, xs, idx, w, grad_out, steps):
@@ -426,16 +450,17 @@ def _combine_steps(wl, xs, idx, w, grad_out, mode, backward, inplace, dev):
     def step():
         out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (wl.T, wl.D), mode=mode)
         if backward:
-            torch.autograd.grad(out, inputs, grad_out)
-        return out
+            return (out, *torch.autograd.grad(out, inputs, grad_out))
+        return (out,)
 
     def direct_step():
         with torch.no_grad():
             ctx = _StepCtx()
             out = ops._combine_forward(ctx, mode, None, idx, w, (wl.T, wl.D), xs, backward)
             if backward:
-                ops._combine_backward(ctx, grad_out, True, [True] * len(xs))
-        return out
+                gw, gx = ops._combine_backward(ctx, grad_out, True, [True] * len(xs))
+                return (out, gw, *gx)
+        return (out,)
     return step, direct_step
 
 
@@ -469,7 +494,7 @@ def _config_line(name, mode, steps, warmup, dev):
     torch.cuda.synchronize()
     kernels, _ = _event_kernels(step, steps)
     dom = _summarize_kernels(kernels, kernel_bytes(wl.T, wl.D, wl.N, xb, xb))
-    ms, _, err = _graph_ms(direct_step, steps, warmup)
+    ms, _, err, _ = _graph_ms(direct_step, steps, warmup)
     if ms is None:
         ms, _ = _timed(step, steps)
     plan_us = sum(v["avg_us"] for k, v in kernels.items() if k in ("metadata_plan", "plan", "metadata"))
@@ -479,10 +504,10 @@ def _config_line(name, mode, steps, warmup, dev):
         # BASELINE's det-vs-atomic configuration: 10 runs on the same inputs; det must repeat bit
         # for bit, atomic is reported with its largest run-to-run difference
         with torch.no_grad():
-            ref = step().clone()
+            ref = step()[0].clone()
             same, worst = True, 0.0
             for _ in range(9):
-                o = step()
+                o = step()[0]
                 same = same and torch.equal(o.view(torch.int16), ref.view(torch.int16))
                 worst = max(worst, (o.float() - ref.float()).abs().max().item())
         repeat = {"runs": 10, "bit_identical": same, "max_abs_diff": worst}
@@ -674,6 +699,7 @@ def main() -> int:
     kernels, backlog = _event_kernels(step, args.steps)
 
     graph_error = None
+    replay_check = None
     ms = None
     if not args.eager:
         # The step captured once as a HIP graph and replayed: the timed region is pure device
@@ -681,7 +707,12 @@ def main() -> int:
         # The combine's step is captured from the launches the autograd path makes, issued by its
         # own forward and backward functions on this thread (_StepCtx), without the autograd
         # engine.
-        ms, wall_ms, graph_error = _graph_ms(direct_step or step, args.steps, args.warmup)
+        after = None
+        if direct_step is not None and not args.inplace:
+            after = lambda static: _replay_matches_eager(static, step,  # noqa: E731
+                                                         args.mode == "det")
+        ms, wall_ms, graph_error, replay_check = _graph_ms(direct_step or step, args.steps,
+                                                           args.warmup, after)
     if ms is not None:
         timing = "hip-graph replay of one captured step"
     else:
@@ -737,6 +768,8 @@ def main() -> int:
         "eager_wall_ms_per_step": round(eager_wall_ms, 4),
         "eager_autograd_floor_ms": round(floor_ms, 4) if floor_ms is not None else None,
         "graph_error": graph_error,
+        "graph_replay_matches_eager": replay_check[0] if replay_check else None,
+        "graph_replay_compared": replay_check[1] if replay_check else None,
         "kernel_timing": "HIP events around each launch in eager steps queued behind a sleep kernel"
                          if backlog else "HIP events around each launch in eager steps",
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}

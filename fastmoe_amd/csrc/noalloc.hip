@@ -40,7 +40,9 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device (null: not looked up)
 
 // Device address of the current device's `scratch`, looked up on the first call on that device.
-int scratch_address(void** out) {
+// That first call must not be recorded into a HIP graph: the lookup is a runtime query, not a
+// stream operation, so a stream under capture is refused until the address is known.
+int scratch_address(hipStream_t stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
@@ -54,6 +56,14 @@ int scratch_address(void** out) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cap);
+    if (e != hipSuccess || cap != hipStreamCaptureStatusNone) {
+      fmoe_host::set_error("fmoe_combine_fwd_noalloc: the first call on device %d must come before "
+                           "any graph capture on its stream (it looks up the static buffer's "
+                           "address); call it once outside the capture", dev);
+      return FMOE_EINVAL;
+    }
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr) {
@@ -107,7 +117,7 @@ extern "C" int fmoe_combine_fwd_noalloc(const int64_t* host_ptrs, const int64_t*
     return FMOE_ERANGE;
   }
   void* base = nullptr;
-  if (int rc = scratch_address(&base)) return rc;
+  if (int rc = scratch_address(static_cast<hipStream_t>(stream), &base)) return rc;
   char* s = static_cast<char*>(base);
   int64_t* ptr_table = reinterpret_cast<int64_t*>(s + kPtrTableOff);
   int32_t* chunk_sizes = reinterpret_cast<int32_t*>(s + kChunkSizesOff);

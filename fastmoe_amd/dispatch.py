@@ -30,8 +30,8 @@ import torch
 
 from . import _abi
 from .ops import (_FLOAT_CODES, _INDEX_CODES, _check_experts, _launch_fwd,
-                  _metadata_and_plan_from_slots, _require_cuda, _span, _stream_handle,
-                  _validate_default, prepare_metadata_and_plan)
+                  _metadata_and_plan_from_slots, _refuse_autograd_capture, _require_cuda, _span,
+                  _stream_handle, _validate_default, prepare_metadata_and_plan)
 
 __all__ = ["PermutedTokens", "permute_tokens"]
 
@@ -47,19 +47,24 @@ class PermutedTokens(NamedTuple):
     slot_pos: torch.Tensor             # int32 [T*k], packed row of slot t*k + j
 
 
-# Unit gates of the backward combine, kept per (device, rows): built once, outside any graph a
-# caller captures after its warm-up steps, instead of a fill kernel in every backward.
+# Unit gates of the backward combine: one grow-only buffer of ones per device, handed out as
+# prefixes, built outside any graph a caller captures after its warm-up steps instead of a fill
+# kernel in every backward.  A captured graph keeps the raw address of the prefix it was given
+# (a pointer passed through the C ABI holds no reference), so no buffer is ever released: when a
+# larger one replaces it, the old one moves to _RETIRED for the life of the process.  Sizes at
+# least double, so the retired buffers together hold fewer elements than the live one.
 _ONES: dict = {}
+_RETIRED: list = []
 
 
 def _unit_gates(n: int, dev: torch.device) -> torch.Tensor:
-    key = (dev, n)
-    ones = _ONES.get(key)
-    if ones is None:
-        if len(_ONES) >= 8:
-            _ONES.clear()
-        ones = _ONES[key] = torch.ones(n, dtype=torch.float32, device=dev)
-    return ones
+    ones = _ONES.get(dev)
+    if ones is None or ones.numel() < n:
+        if ones is not None:
+            _RETIRED.append(ones)
+        size = max(n, 2 * ones.numel() if ones is not None else 0, 1024)
+        ones = _ONES[dev] = torch.ones(size, dtype=torch.float32, device=dev)
+    return ones[:n]
 
 
 def _unit_gate_combine(rows: torch.Tensor, rev: torch.Tensor, slot_pos: torch.Tensor,
@@ -131,6 +136,7 @@ class _TokenPermute(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_out, g_sorted_w, _g_counts, _g_rev, _g_off, _g_pos):
         rev, slot_pos = ctx.saved_tensors
+        _refuse_autograd_capture("the permutation's backward", rev)
         T, k = ctx.num_tokens, ctx.top_k
         grad_x = grad_w = None
         if ctx.needs_input_grad[0] and g_out is not None:
@@ -177,6 +183,9 @@ def permute_tokens(x_flat: torch.Tensor, topk_indices: torch.Tensor, topk_weight
         raise ValueError(f"fastmoe_amd: num_experts must be in [1, 4096], got {num_experts}")
     if len({x_flat.device, topk_indices.device, topk_weights.device}) != 1:
         raise ValueError("fastmoe_amd: x_flat, topk_indices and topk_weights must share a device")
+    if torch.is_grad_enabled():
+        _refuse_autograd_capture("the autograd permutation", x_flat,
+                                 x_flat.requires_grad or topk_weights.requires_grad)
     out, sorted_w, counts, rev, offsets, slot_pos = _TokenPermute.apply(
         x_flat, topk_weights, topk_indices, int(num_experts), _validate_default(validate))
     return PermutedTokens(out, counts, rev, sorted_w, offsets, slot_pos)

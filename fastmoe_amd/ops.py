@@ -563,12 +563,14 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
         checked = _check_experts(expert_tensors)
         rows = sum(checked[3])
         idx, w = _routing_args(indices, weights, rows, checked[1])
-        if code == _abi.MODE_DET and _use_small(rows, T, len(checked[3])):
+        # The small path counts out-of-range indices in the same launch that accumulates into
+        # ``out``; a validating call takes the planned path, which raises before any forward
+        # launch, so ``out`` is left untouched when it raises.
+        if (code == _abi.MODE_DET and not _validate_default(validate)
+                and _use_small(rows, T, len(checked[3]))):
             _check_out(out, None, checked[2], checked[1])
-            status = _launch_fwd_small(_small_tables(checked), len(checked[3]), idx, w,
-                                       checked[0], out, accumulate=True)
-            if _validate_default(validate):
-                _check_small_status(status, T)
+            _launch_fwd_small(_small_tables(checked), len(checked[3]), idx, w, checked[0], out,
+                              accumulate=True)
             return out
         if code == _abi.MODE_DET and rows > 0:
             metadata, plan = _metadata_and_plan(expert_tensors, checked, idx, w, T, validate)
@@ -722,8 +724,39 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
 
 
 def _apply(fn, *args):
-    """``fn.apply(*args)`` (one place for every autograd entry of the combine)."""
+    """``fn.apply(*args)`` (one place for every autograd entry of the combine), refused under HIP
+    graph capture when it would record a backward (see _refuse_autograd_capture)."""
+    probe = next(a for a in args if isinstance(a, torch.Tensor))
+    if _capturing(probe) and torch.is_grad_enabled():
+        _refuse_autograd_capture("the autograd combine", probe, _records_backward(args))
     return fn.apply(*args)
+
+
+def _records_backward(args) -> bool:
+    return any(isinstance(a, torch.Tensor) and a.requires_grad for a in args)
+
+
+def _capturing(t: torch.Tensor) -> bool:
+    """Whether ``t`` is a GPU tensor and the current stream is capturing a HIP graph."""
+    return t.is_cuda and torch.cuda.is_current_stream_capturing()
+
+
+def _refuse_autograd_capture(what: str, t: torch.Tensor, recording: bool = True) -> None:
+    """Raise instead of recording an autograd step into a HIP graph.
+
+    One capture of a whole autograd step (this forward and ``torch.autograd.grad``, whose backward
+    runs on the autograd engine's device thread) inside ``torch.cuda.graph`` ended in a host
+    segmentation fault in ``CUDAGraph.capture_end``, with no GPU fault, and no cause has been shown
+    in this package's code.  Until one is, that capture is refused with this error rather than
+    risked.  Captures that do not go through the engine stay supported and tested: the in-place
+    call (``out=``, run_on_cloud.py:66-92) and the autograd forward under ``torch.no_grad()``.
+    """
+    if recording and _capturing(t):
+        raise RuntimeError(
+            f"fastmoe_amd: {what} under HIP graph capture is not supported (a captured autograd "
+            "step once crashed the host in CUDAGraph.capture_end).  Capture the in-place call "
+            "(grouped_weighted_scatter_add(..., out=..., metadata=...)) or run the autograd step "
+            "eagerly.")
 
 
 class GroupedWeightedScatterAdd(torch.autograd.Function):
@@ -744,6 +777,7 @@ class GroupedWeightedScatterAdd(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
+        _refuse_autograd_capture("the combine's backward", grad_output)
         gw, gx = _combine_backward(ctx, grad_output, ctx.needs_input_grad[1],
                                    ctx.needs_input_grad[3:])
         return (None, gw, None, *gx)
@@ -760,6 +794,7 @@ class _GroupedCombineWithOptions(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
+        _refuse_autograd_capture("the combine's backward", grad_output)
         gw, gx = _combine_backward(ctx, grad_output, ctx.needs_input_grad[2],
                                    ctx.needs_input_grad[4:])
         return (None, None, gw, None, *gx)
@@ -776,6 +811,7 @@ class _GroupedCombinePermuted(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
+        _refuse_autograd_capture("the combine's backward", grad_output)
         gw, gx = _combine_backward(ctx, grad_output, ctx.needs_input_grad[2],
                                    ctx.needs_input_grad[4:])
         return (None, None, gw, None, *gx)

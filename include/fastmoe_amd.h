@@ -265,6 +265,9 @@ FMOE_API int fmoe_combine_fwd(int mode, const void* d_plan, const void* d_indice
  * Calls on one GPU share its buffer: calls that overlap on one GPU (two streams, two threads)
  * race; calls on one stream are ordered.  Arguments as in fmoe_build_metadata_and_plan and
  * fmoe_combine_fwd.
+ * Graph capture: the first call on a device looks up the buffer's address and must run outside
+ * any capture (under one it returns FMOE_EINVAL); later calls can be captured and replayed, each
+ * replay rebuilding the metadata and plan in the buffer.
  */
 #define FMOE_NOALLOC_SCRATCH_BYTES (16 << 20)
 FMOE_API int fmoe_combine_fwd_noalloc(const int64_t* host_ptrs, const int64_t* host_rows,

@@ -353,3 +353,85 @@ def test_small_path_not_taken(fake_small, case):
                                                  mode=mode)
     kinds = [c[0] for c in fake_small.calls]
     assert "fwd_small" not in kinds and ("fwd" in kinds)
+
+
+def test_validating_in_place_call_checks_indices_before_accumulating(fake_small, monkeypatch):
+    """With validate=True an in-place call of small-path size takes the planned path, whose index
+    check runs before the forward launch (so ``out`` is untouched when it raises); without it,
+    the one-launch small path."""
+    order = []
+    monkeypatch.setattr(ops, "_check_plan_status", lambda plan, T: order.append("check"))
+    xs, idx, w = _experts(torch.float32), torch.randint(0, 4, (8,)), torch.rand(8)
+    fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16), out=torch.zeros(4, 16),
+                                             validate=True)
+    kinds = [c[0] for c in fake_small.calls]
+    assert kinds == ["metadata_plan", "fwd"] and order == ["check"]
+    fake_small.calls.clear()
+    fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16), out=torch.zeros(4, 16))
+    assert [c[0] for c in fake_small.calls] == ["fwd_small"]
+
+
+def _capture_on(monkeypatch):
+    monkeypatch.setattr(ops, "_capturing", lambda t: True)
+
+
+@pytest.mark.parametrize("path", ["planned", "small"])
+def test_autograd_combine_refused_under_capture(path, monkeypatch):
+    """Under HIP graph capture the autograd forward that records a backward, and the backward,
+    raise a clear error before any launch; the forward without gradients and the in-place call
+    stay capturable."""
+    f = _fake_lib(monkeypatch)
+    with _abi.options(small=1 if path == "planned" else 0):
+        xs = [x.requires_grad_(True) for x in _experts()]
+        idx = torch.randint(0, 4, (8,))
+        w = torch.rand(8, requires_grad=True)
+        _capture_on(monkeypatch)
+        with pytest.raises(RuntimeError, match="graph capture is not supported"):
+            fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16))
+        with pytest.raises(RuntimeError, match="graph capture is not supported"):
+            fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16), mode="det")
+        assert f.calls == []
+        with torch.no_grad():
+            fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16))
+        fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16), out=torch.zeros(4, 16))
+        assert len(f.calls) >= 2
+        # forward outside the capture, backward inside it
+        monkeypatch.setattr(ops, "_capturing", lambda t: False)
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx, w, (4, 16))
+        _capture_on(monkeypatch)
+        n = len(f.calls)
+        with pytest.raises(RuntimeError, match="backward under HIP graph capture"):
+            torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
+        assert len(f.calls) == n
+
+
+def test_autograd_permutation_refused_under_capture(monkeypatch):
+    from fastmoe_amd import dispatch
+
+    _capture_on(monkeypatch)
+    monkeypatch.setattr(dispatch, "_require_cuda", lambda t, what: None)
+    x = torch.randn(4, 8, requires_grad=True)
+    with pytest.raises(RuntimeError, match="graph capture is not supported"):
+        dispatch.permute_tokens(x, torch.randint(0, 3, (4, 2)), torch.rand(4, 2), 3)
+
+
+def test_unit_gates_never_release_a_buffer_handed_out(monkeypatch):
+    """A captured permutation backward keeps the raw address of its unit gates: every prefix handed
+    out stays inside a buffer the module still holds, however many row counts follow."""
+    from fastmoe_amd import dispatch
+
+    monkeypatch.setattr(dispatch, "_ONES", {})
+    monkeypatch.setattr(dispatch, "_RETIRED", [])
+    dev = torch.device("cpu")
+    handed = []
+    for n in [5, 3000, 7, 100_000, 1, 2047, 250_000, 64, 9000, 1_000_003]:
+        g = dispatch._unit_gates(n, dev)
+        assert g.shape == (n,) and bool((g == 1).all())
+        handed.append((g.data_ptr(), n))
+        del g
+    held = [dispatch._ONES[dev], *dispatch._RETIRED]
+    spans = [(b.data_ptr(), b.data_ptr() + 4 * b.numel()) for b in held]
+    for ptr, n in handed:
+        assert any(lo <= ptr and ptr + 4 * n <= hi for lo, hi in spans)
+    # growth at least doubles: the retired buffers hold fewer elements than the live one
+    assert sum(b.numel() for b in dispatch._RETIRED) < dispatch._ONES[dev].numel()

@@ -1170,10 +1170,11 @@ def test_graph_capture_replays(mode):
         _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum().item()
 
 
-@pytest.mark.skip(reason="its one run with this build's rewritten host path (det mode) ended in a "
+@pytest.mark.skip(reason="its one run (det mode, on the host path of commit b95310e) ended in a "
                          "host segmentation fault inside torch.cuda.CUDAGraph.capture_end, with no "
                          "GPU fault; no cause has been shown in this library's code, so the case "
-                         "stays off the GPU (the same capture passed before that rewrite)")
+                         "stays off the GPU and the library refuses such a capture with an error "
+                         "(test_autograd_step_under_capture_raises)")
 @pytest.mark.parametrize("mode", ["det", "atomic"])
 def test_graph_capture_autograd_step_replays(mode):
     """The bench's timed step -- metadata, plan, forward and both backward passes through the
@@ -1240,14 +1241,43 @@ class _DirectCtx:
         self.saved_tensors = tensors
 
 
-@pytest.mark.parametrize("mode", ["det", "atomic"])
-def test_graph_capture_direct_step_replays(mode):
-    """bench.py's timed step: the launches of one autograd step (metadata + plan, forward, grad_X
-    and grad_w passes), issued by the autograd path's own forward and backward functions on this
-    thread, captured once as a graph.  Every replay (with eager work in between) equals the oracle
-    -- forward and grad_X bit for bit in det mode, the one-ulp bar in atomic mode, grad_w within
-    1e-6 of sum|terms| -- and, in det mode, the eager step bit for bit."""
+def test_autograd_step_under_capture_raises():
+    """The autograd forward that records a backward raises a clear RuntimeError under HIP graph
+    capture, before any launch of this library; the graph captured so far (one torch kernel)
+    still replays."""
+    wl, T, idx, w, experts = _inputs("gigachat", T=16)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    xs = [x.requires_grad_(True) for x in xd]
+    bump = torch.zeros(4, device=DEV)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="graph capture is not supported"):
+        with torch.cuda.graph(g):
+            bump.add_(1)
+            fastmoe_amd.grouped_weighted_scatter_add(xs, idd, wd, (T, wl.D))
+    g.replay()
+    torch.cuda.synchronize()
+    assert bump.tolist() == [1.0] * 4
+
+
+# (mode, kernel option "small"): the planned step (metadata + plan, forward, grad_X pass, grad_w
+# pass -- what bench.py times at the headline shape) and the one-launch small path.
+_DIRECT_STEPS = [("det", 1), ("det", 2), ("atomic", 1)]
+
+
+@pytest.mark.parametrize("mode,small", _DIRECT_STEPS,
+                         ids=[f"{m}-{'planned' if s == 1 else 'small'}" for m, s in _DIRECT_STEPS])
+def test_graph_capture_direct_step_replays(mode, small, kernel_options):
+    """bench.py's timed step: the launches of one autograd step, issued by the autograd path's own
+    forward and backward functions on this thread, captured once as a graph -- the planned step
+    (metadata + plan, forward, grad_X and grad_w passes) and, in det mode, the small path's two
+    launches.  Every replay (with eager work in between) equals the oracle -- forward and grad_X
+    bit for bit in det mode, the one-ulp bar in atomic mode, grad_w within 1e-6 of sum|terms| --
+    and, in det mode, the eager step bit for bit."""
     wl, T, idx, w, experts = _inputs("gigachat", T=128)
+    kernel_options(small=small)
+    if mode == "det":  # the atomic modes never take the small path
+        assert ops._use_small(idx.numel(), T, len(experts)) == (small == 2)
     xd, idd, wd = _to_dev(experts, idx, w)
     go_cpu = torch.randn(T, wl.D, generator=torch.Generator().manual_seed(5)).to(wl.dtype)
     go = go_cpu.to(DEV)

@@ -7,7 +7,8 @@ small path (2) and turning it off (1).  The cases cover what the small kernels d
 from the planned ones: tokens of more than 64 rows (the compaction window refills), indices out
 of range (staged as -1), rows that are not 16-byte aligned (element loads), D that no 16-byte
 vector divides (the scalar kernels), empty experts, the row and expert limits, int32 indices,
-16-bit gates and a single token.
+16-bit gates, a single token and rows of 32 KiB (where the planned grad_w pass stages grad_out
+in LDS).
 """
 from __future__ import annotations
 
@@ -50,6 +51,10 @@ CASES = {
     "int32_bf16_gates": (97, [60, 80, 0, 45], 1536, torch.bfloat16, None,
                          {"idx_dtype": torch.int32, "w_dtype": torch.bfloat16}),
     "one_token": (1, [13, 27], 4096, torch.bfloat16, None, {}),
+    # rows of 32 KiB: the planned grad_w pass takes its LDS-staged form and the small backward
+    # its 4-vector column step
+    "wide_rows_bf16": (16, [16] * 8, 16384, torch.bfloat16, None, {}),
+    "wide_rows_f32": (16, [8] * 16, 8192, torch.float32, None, {}),
 }
 
 
@@ -135,3 +140,18 @@ def test_small_path_validate_raises_on_out_of_range_indices(kernel_options):
                                                  validate=True)
     torch.cuda.synchronize()
 
+
+
+@pytest.mark.parametrize("force", [0, 2])
+def test_validating_in_place_call_leaves_out_untouched(force, kernel_options):
+    """A validating in-place call of small-path size raises IndexError before any forward launch,
+    so ``out`` keeps its bits (a caller that catches the error and retries adds nothing twice)."""
+    T, D, idx, w, xd, _ = _make("invalid_indices")
+    kernel_options(small=force)
+    out0 = torch.randn(T, D, generator=torch.Generator().manual_seed(11))
+    out = out0.to(DEV)
+    with pytest.raises(IndexError, match="outside"):
+        fastmoe_amd.grouped_weighted_scatter_add(xd, idx.to(DEV), w.to(DEV), (T, D), out=out,
+                                                 validate=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(out), bits(out0))

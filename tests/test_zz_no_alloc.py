@@ -155,6 +155,40 @@ def test_noalloc_accumulates_into_padded_out_with_int32_indices():
         assert np.array_equal(bits(b), _as_bits(exp))
 
 
+@pytest.mark.gpu
+def test_noalloc_captured_in_a_graph_replays_like_the_oracle():
+    """After one eager call on the device (which looks up the static buffer's address), the
+    entry point is captured in a HIP graph.  Every replay overwrites ``out`` with the oracle's
+    bits, also after an eager call of another size has reused the static buffer in between."""
+    print("noalloc: captured once, replayed with eager calls between", flush=True)
+    c = _case(512, 1024, 32, 6, torch.bfloat16, 15)
+    other = _case(96, 520, 8, 2, torch.bfloat16, 16)
+    dev = c["xs"][0].device
+    exp, _, _ = oracle_fwd(c["xs_cpu"], c["idx_cpu"], c["w_cpu"], c["T"], torch.bfloat16)
+    exp_other, _, _ = oracle_fwd(other["xs_cpu"], other["idx_cpu"], other["w_cpu"], other["T"],
+                                 torch.bfloat16)
+    out = torch.zeros((c["T"], c["D"]), dtype=torch.bfloat16, device=dev)
+    _noalloc(c, out, 0)  # first call on the device, outside any capture
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), _as_bits(exp))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            _noalloc(c, out, 0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.fill_(-1.0)
+        o2 = torch.full((other["T"], other["D"]), 2.0, dtype=torch.bfloat16, device=dev)
+        _noalloc(other, o2, 0)  # reuses the static buffer between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), _as_bits(exp)), f"replay {i}"
+        assert np.array_equal(bits(o2), _as_bits(exp_other))
+
+
 def test_noalloc_rejects_sizes_beyond_the_static_buffer():
     """Host-side checks only: they return before any HIP call (no GPU needed)."""
     lib = _abi.lib()
