@@ -20,6 +20,10 @@ BUILD_DIR = PKG / "_build"
 LIB_NAME = "libfastmoe_amd.so"
 LIB_PATH = PKG / LIB_NAME
 
+# The operator layer's host helper module (fastmoe_amd._host, a CPython extension built against
+# the installed torch): it reads tensor properties in C++, and is not part of the C ABI.
+HOST_EXT_SOURCE = "host_ext.cpp"
+
 HIP_SOURCES = ["metadata.hip", "plan.hip", "plan_bucket.hip", "plan_radix.hip", "combine_fwd.hip",
                "combine_bwd.hip", "permute.hip", "noalloc.hip"]
 HOST_SOURCES = ["abi.cpp"]
@@ -46,12 +50,13 @@ CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall"]
 
 def source_hash() -> str:
     """sha256 (hex, 16 digits) of every source the library is built from: the HIP and host
-    translation units, their headers and the C ABI header.  Measurements kept in profiles/ record
+    translation units, their headers and the C ABI header (not the Python helper module).  Measurements kept in profiles/ record
     it, so a reader (bench.py) can tell whether they describe the current kernels."""
     import hashlib
 
     h = hashlib.sha256()
-    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.cpp"))
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h"))
+    files += [CSRC / s for s in HOST_SOURCES]
     files.append(PKG.parent / "include" / "fastmoe_amd.h")
     for f in files:
         h.update(f.name.encode())
@@ -81,9 +86,28 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
+def _host_ext_command(cxx: str):
+    """g++ command of the host helper module: (command, temporary output, final path)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    path = PKG / ("_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = path.with_name(path.name + ".tmp")
+    incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"]]
+    libdirs = cpp_extension.library_paths()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [cxx, *CXX_FLAGS, "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", str(CSRC / HOST_EXT_SOURCE),
+           "-o", str(tmp), *[f"-I{i}" for i in incs], *[f"-L{d}" for d in libdirs],
+           *[f"-Wl,-rpath,{d}" for d in libdirs], "-lc10", "-ltorch", "-ltorch_python"]
+    return cmd, tmp, path
+
+
 def build(verbose: bool = True, jobs: int | None = None, defines: list[str] | None = None,
           out: Path | None = None, build_dir: Path | None = None) -> Path:
-    """Compile every translation unit and link ``libfastmoe_amd.so``; returns its path.
+    """Compile every translation unit and link ``libfastmoe_amd.so``; returns its path.  The
+    in-tree build also compiles the host helper module ``fastmoe_amd._host``.
 
     ``defines`` (e.g. ``["FMOE_BWD_WAVES=8"]``) set the kernels' compile-time knobs; ``out`` and
     ``build_dir`` redirect the result (tuning builds), by default the in-tree library.
@@ -104,9 +128,14 @@ def build(verbose: bool = True, jobs: int | None = None, defines: list[str] | No
         obj = bdir / (src + ".o")
         cmds.append([cxx, *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
+    ext_cmd, ext_tmp, ext_path = (None, None, None) if out else _host_ext_command(cxx)
+    if ext_cmd:
+        cmds.append(ext_cmd)
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
+    if ext_cmd:
+        os.replace(ext_tmp, ext_path)
     tmp = lib_path.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
     os.replace(tmp, lib_path)

@@ -30,8 +30,9 @@ import torch
 
 from . import _abi
 from .ops import (_FLOAT_CODES, _INDEX_CODES, _check_experts, _launch_fwd,
-                  _metadata_and_plan_from_slots, _refuse_autograd_capture, _require_cuda, _span,
-                  _stream_handle, _validate_default, prepare_metadata_and_plan)
+                  _metadata_and_plan_from_slots, _on_device, _refuse_autograd_capture,
+                  _require_cuda, _span, _stream_handle, _validate_default,
+                  prepare_metadata_and_plan)
 
 __all__ = ["PermutedTokens", "permute_tokens"]
 
@@ -79,7 +80,7 @@ def _unit_gate_combine(rows: torch.Tensor, rev: torch.Tensor, slot_pos: torch.Te
         return out.zero_()
     ones = _unit_gates(rows.shape[0], rows.device)
     if top_k <= 64 and rows.shape[0] == num_tokens * top_k:
-        meta, plan = _metadata_and_plan_from_slots([rows], _check_experts([rows]), slot_pos, ones,
+        meta, plan = _metadata_and_plan_from_slots(_check_experts([rows]), slot_pos, ones,
                                                    num_tokens, top_k)
     else:
         meta, plan = prepare_metadata_and_plan([rows], rev, ones, num_tokens, validate=False)
@@ -108,7 +109,7 @@ class _TokenPermute(torch.autograd.Function):
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         out = torch.empty((N, D), dtype=x_flat.dtype, device=dev)
         es = x_flat.element_size()
-        with torch.cuda.device(dev):
+        with _on_device(dev):
             with _span("permute_build"):
                 rc = lib.fmoe_permute_build(
                     ids.data_ptr(), _INDEX_CODES[ids.dtype], gates.data_ptr(),
@@ -144,7 +145,7 @@ class _TokenPermute(torch.autograd.Function):
         if ctx.needs_input_grad[1] and g_sorted_w is not None:
             gs = g_sorted_w.contiguous()
             grad_w = torch.empty(T * k, dtype=gs.dtype, device=gs.device)
-            with torch.cuda.device(gs.device), _span("permute_gate_grad"):
+            with _on_device(gs.device), _span("permute_gate_grad"):
                 rc = _abi.lib().fmoe_permute_gate_grad(
                     slot_pos.data_ptr(), T * k, gs.data_ptr(), _FLOAT_CODES[gs.dtype],
                     grad_w.data_ptr(), _stream_handle(gs.device))

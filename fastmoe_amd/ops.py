@@ -34,10 +34,8 @@ Differences from the reference, each deliberate:
 """
 from __future__ import annotations
 
-import array
 import contextlib
 import ctypes
-import operator
 import os
 from typing import Optional, Sequence
 
@@ -60,6 +58,22 @@ __all__ = [
 # Optional per-launch timer (bench.py installs one): an object with span(name) returning a
 # context manager that brackets the C-ABI launch on the current stream.
 _TIMER = None
+
+
+_HOST = []
+
+
+def _host():
+    """The host helper module ``fastmoe_amd._host`` (built with the library); raises if missing."""
+    if not _HOST:
+        try:
+            from . import _host as mod
+        except ImportError as exc:
+            raise _abi.FastMoEError(
+                "fastmoe_amd: the host helper module fastmoe_amd._host is not built "
+                "(run python -m fastmoe_amd.build)") from exc
+        _HOST.append(mod)
+    return _HOST[0]
 
 
 def _span(name: str):
@@ -90,7 +104,15 @@ def _validate_default(validate: Optional[bool]) -> bool:
 
 
 def _stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of ``device``'s current stream (every launch goes on it)."""
+    return torch._C._cuda_getCurrentRawStream(device.index)
+
+
+def _on_device(device: torch.device):
+    """``torch.cuda.device(device)``, or nothing when it is already the current device."""
+    if torch._C._cuda_getDevice() == device.index:
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 class _DeviceProbe:
@@ -123,15 +145,17 @@ class GroupedMetadata(tuple):
         self = super().__new__(
             cls, (ptr_table, chunk_sizes, offsets_full[:num_experts], max_rows, num_experts)
         )
+        ex = extra["experts"]
         self.offsets_full = offsets_full  # int64[E + 1], offsets_full[E] == N
         self.max_rows_device = extra["max_rows_device"]
-        self.tensors = tuple(extra["tensors"])
-        self.sizes = tuple(extra["sizes"])
-        self.ptrs = tuple(extra["ptrs"])
-        self.hidden = extra["hidden"]
-        self.dtype = extra["dtype"]
-        self.device = extra["device"]
-        self.num_rows = sum(self.sizes)
+        self.tensors = tuple(ex.tensors)
+        self.sizes = tuple(ex.sizes)
+        self.ptrs = tuple(ex.ptrs)
+        self.table = bytes(ex.table)  # the packed (addresses, rows) this metadata describes
+        self.hidden = ex.hidden
+        self.dtype = ex.dtype
+        self.device = ex.device
+        self.num_rows = ex.rows
         return self
 
     # the reference tuple's fields by name
@@ -148,29 +172,48 @@ class GroupedMetadata(tuple):
         if len(expert_tensors) != len(self.ptrs):
             return False
         try:
-            checked = _check_experts(expert_tensors)
+            ex = _check_experts(expert_tensors)
         except (ValueError, TypeError, RuntimeError):
             return False
-        return (checked[0] == self.dtype and checked[1] == self.device
-                and checked[2] == self.hidden and tuple(checked[3]) == self.sizes
-                and tuple(checked[4]) == self.ptrs)
+        return (ex.dtype == self.dtype and ex.device == self.device and ex.hidden == self.hidden
+                and ex.table == self.table)
 
 
-# Per-tensor property readers for map(): unbound C accessors, without a Python-level loop body.
-_DTYPE_OF = torch.Tensor.dtype.__get__
-_SHAPE_OF = torch.Tensor.shape.__get__
-_ROWS_OF, _COLS_OF = operator.itemgetter(0), operator.itemgetter(1)
+class _Experts:
+    """Validated expert buffers (``_check_experts``): dtype, device, hidden size, total and largest
+    row count, and ``table``, a bytearray of the E data addresses then the E row counts (int64),
+    which the C ABI takes as its two host tables."""
+
+    __slots__ = ("tensors", "dtype", "device", "hidden", "rows", "max_rows", "table", "num")
+
+    def __init__(self, tensors, dtype, device, hidden, rows, max_rows, table):
+        self.tensors, self.dtype, self.device, self.hidden = tensors, dtype, device, hidden
+        self.rows, self.max_rows, self.table = rows, max_rows, table
+        self.num = len(table) // 16
+
+    @property
+    def ptrs(self) -> list:
+        return memoryview(self.table).cast("q")[: self.num].tolist()
+
+    @property
+    def sizes(self) -> list:
+        return memoryview(self.table).cast("q")[self.num:].tolist()
+
+    def host_tables(self) -> tuple:
+        """(addresses, rows) as ctypes int64 arrays over ``table`` (they keep it alive)."""
+        E = self.num
+        return ((ctypes.c_int64 * E).from_buffer(self.table),
+                (ctypes.c_int64 * E).from_buffer(self.table, 8 * E))
 
 
-def _check_experts(expert_tensors: Sequence[torch.Tensor]):
-    """Validate the expert buffers; returns (dtype, device, hidden, sizes, ptrs).
+def _check_experts(expert_tensors: Sequence[torch.Tensor]) -> _Experts:
+    """Validate the expert buffers.
 
     Every buffer must be a 2-D [rows, D] tensor of one float dtype on one GPU, row-contiguous
     (``is_contiguous()`` on a 2-D tensor is exactly the layout the kernels address: strides (D, 1)
     for several rows, a unit column stride for one row, anything for no rows).  With hundreds of
-    experts this runs on every call, so each property is read once per tensor through ``map``
-    over the tensor type's own accessors; only a failing list is walked again, to name the first
-    offending buffer.
+    experts this runs on every call, so the per-tensor checks and the packing of the (address,
+    rows) pairs run in C++ (``_host.experts``), which names the first offending buffer.
     """
     if len(expert_tensors) == 0:
         raise ValueError("fastmoe_amd: expert_tensors is empty")
@@ -178,48 +221,100 @@ def _check_experts(expert_tensors: Sequence[torch.Tensor]):
     _require_cuda(ref, "expert_tensors[0]")
     if ref.dtype not in _FLOAT_CODES:
         raise TypeError(f"fastmoe_amd: unsupported expert dtype {ref.dtype}")
-    if ref.dim() != 2:
-        raise ValueError(f"fastmoe_amd: expert tensors must be 2-D [rows, D], got {tuple(ref.shape)}")
-    dtype, device, hidden = ref.dtype, ref.device, ref.shape[1]
-    shapes = list(map(_SHAPE_OF, expert_tensors))
-    if (set(map(_DTYPE_OF, expert_tensors)) != {dtype}
-            or set(map(torch.Tensor.get_device, expert_tensors)) != {ref.get_device()}
-            or set(map(len, shapes)) != {2} or set(map(_COLS_OF, shapes)) != {hidden}
-            or not all(map(torch.Tensor.is_contiguous, expert_tensors))):
-        _explain_bad_expert(expert_tensors, dtype, device, hidden)
-    return (dtype, device, hidden, list(map(_ROWS_OF, shapes)),
-            list(map(torch.Tensor.data_ptr, expert_tensors)))
+    hidden, rows, max_rows, table = _host().experts(expert_tensors)
+    return _Experts(expert_tensors, ref.dtype, ref.device, hidden, rows, max_rows, table)
 
 
-def _explain_bad_expert(expert_tensors, dtype, device, hidden) -> None:
-    for i, t in enumerate(expert_tensors):
-        if t.dtype != dtype or t.device != device:
-            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] differs in device/dtype from [0]")
-        if t.dim() != 2 or t.shape[1] != hidden:
-            raise ValueError(f"fastmoe_amd: expert_tensors[{i}] has shape {tuple(t.shape)}, "
-                             f"expected [*, {hidden}]")
-        if not t.is_contiguous():
-            raise ValueError(
-                f"fastmoe_amd: expert_tensors[{i}] must be row-contiguous (strides {t.stride()})")
-    raise AssertionError("unreachable")
+_ELEM_BYTES = {torch.float32: 4, torch.bfloat16: 2, torch.float16: 2}
 
 
-def _host_table(values) -> ctypes.Array:
-    """int64 host array for the C ABI: a ctypes view of an ``array.array``, which converts a list
-    of ints about three times faster than the ctypes array constructor (the view keeps the
-    buffer alive)."""
-    buf = array.array("q", values)
-    return (ctypes.c_int64 * len(buf)).from_buffer(buf)
+def _meta_layout(E: int, plan_bytes: int = 0):
+    """One device workspace for the metadata arrays -- ptr_table int64[E], offsets int64[E + 1],
+    chunk_sizes int32[E], max_rows int32[1] -- and, at the next 256-byte boundary, the plan of
+    ``plan_bytes``: (byte offsets of offsets, chunk_sizes, max_rows, plan; total bytes).  torch's
+    caching allocator returns 512-byte aligned blocks, so the plan is 256-byte aligned."""
+    o_off = 8 * E
+    o_chunk = o_off + 8 * (E + 1)
+    o_max = o_chunk + 4 * E
+    o_plan = (o_max + 4 + 255) & ~255
+    return (o_off, o_chunk, o_max, o_plan), o_plan + plan_bytes
 
 
-def _meta_arrays(E: int, dev, plan_bytes: int = 0):
-    """Device arrays of the metadata (ptr_table int64[E], chunk_sizes int32[E], offsets
-    int64[E + 1], max_rows int32[1]) and, if asked for, the plan workspace."""
-    return (torch.empty(E, dtype=torch.int64, device=dev),
-            torch.empty(E, dtype=torch.int32, device=dev),
-            torch.empty(E + 1, dtype=torch.int64, device=dev),
-            torch.empty(1, dtype=torch.int32, device=dev),
-            torch.empty(plan_bytes, dtype=torch.uint8, device=dev) if plan_bytes else None)
+class _RawMeta:
+    """Metadata (and optionally a plan) in one device workspace, as raw addresses for the C ABI;
+    ``ws`` keeps the memory alive."""
+
+    __slots__ = ("ws", "E", "offs", "ptr_table", "offsets", "chunk_sizes", "max_rows", "plan")
+
+    def __init__(self, ex: _Experts, plan_bytes: int = 0):
+        self.E = ex.num
+        self.offs, total = _meta_layout(ex.num, plan_bytes)
+        self.ws = torch.empty(total, dtype=torch.uint8, device=ex.device)
+        base = self.ws.data_ptr()
+        self.ptr_table = base
+        self.offsets = base + self.offs[0]
+        self.chunk_sizes = base + self.offs[1]
+        self.max_rows = base + self.offs[2]
+        self.plan = base + self.offs[3] if plan_bytes else None
+
+    def plan_tensor(self) -> torch.Tensor:
+        return self.ws[self.offs[3]:]
+
+    def tensors(self):
+        """(ptr_table, chunk_sizes, offsets, max_rows) as views of the workspace."""
+        E, (o_off, o_chunk, o_max, _) = self.E, self.offs
+        ws = self.ws
+        return (ws[: 8 * E].view(torch.int64), ws[o_chunk: o_chunk + 4 * E].view(torch.int32),
+                ws[o_off: o_off + 8 * (E + 1)].view(torch.int64),
+                ws[o_max: o_max + 4].view(torch.int32))
+
+
+def _new_metadata(ex: _Experts, m: _RawMeta) -> GroupedMetadata:
+    ptr_table, chunk_sizes, offsets, max_rows_dev = m.tensors()
+    return GroupedMetadata(ptr_table, chunk_sizes, offsets, ex.max_rows, ex.num,
+                           max_rows_device=max_rows_dev, experts=ex)
+
+
+def _plan_bytes(N: int, num_tokens: int) -> int:
+    nbytes = _abi.lib().fmoe_plan_workspace_bytes(N, num_tokens)
+    if nbytes <= 0:
+        raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
+    return nbytes
+
+
+def _run_metadata(ex: _Experts, m: _RawMeta) -> None:
+    """fmoe_build_metadata into ``m``."""
+    ptrs, rows = ex.host_tables()
+    dev = ex.device
+    with _on_device(dev), _span("metadata"):
+        rc = _abi.lib().fmoe_build_metadata(ptrs, rows, ex.num, m.ptr_table, m.chunk_sizes,
+                                            m.offsets, m.max_rows, _stream_handle(dev))
+    _abi.check(rc, "fmoe_build_metadata")
+
+
+def _run_metadata_and_plan(ex: _Experts, m: _RawMeta, idx, w, num_tokens: int) -> None:
+    """fmoe_build_metadata_and_plan into ``m``; idx and w already flat and checked."""
+    ptrs, rows = ex.host_tables()
+    dev = ex.device
+    with _on_device(dev), _span("metadata_plan"):
+        rc = _abi.lib().fmoe_build_metadata_and_plan(
+            ptrs, rows, ex.num, m.ptr_table, m.chunk_sizes, m.offsets, m.max_rows,
+            idx.data_ptr(), _INDEX_CODES[idx.dtype], w.data_ptr(), _FLOAT_CODES[w.dtype],
+            num_tokens, ex.hidden * _ELEM_BYTES[ex.dtype], m.plan, _stream_handle(dev))
+    _abi.check(rc, "fmoe_build_metadata_and_plan")
+
+
+def _run_metadata_and_plan_from_slots(ex: _Experts, m: _RawMeta, slot_pos, w, num_tokens: int,
+                                      top_k: int) -> None:
+    """fmoe_build_metadata_and_plan_from_slots into ``m``; arguments already checked."""
+    ptrs, rows = ex.host_tables()
+    dev = ex.device
+    with _on_device(dev), _span("metadata_plan"):
+        rc = _abi.lib().fmoe_build_metadata_and_plan_from_slots(
+            ptrs, rows, ex.num, m.ptr_table, m.chunk_sizes, m.offsets, m.max_rows,
+            slot_pos.data_ptr(), num_tokens, top_k, w.data_ptr(), _FLOAT_CODES[w.dtype],
+            ex.hidden * _ELEM_BYTES[ex.dtype], m.plan, _stream_handle(dev))
+    _abi.check(rc, "fmoe_build_metadata_and_plan_from_slots")
 
 
 def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None) -> GroupedMetadata:
@@ -229,34 +324,16 @@ def prepare_grouped_metadata(expert_tensors: Sequence[torch.Tensor], device=None
     the device by one kernel launch whose arguments carry the (address, rows) pairs
     (``fmoe_build_metadata``): no host staging buffer and no synchronous copy.
     """
-    checked = _check_experts(expert_tensors)
+    ex = _check_experts(expert_tensors)
     if device is not None:
         _require_cuda(_DeviceProbe(device), "device")
-    return _metadata(expert_tensors, checked)
+    return _metadata(ex)
 
 
-def _new_metadata(expert_tensors, checked, arrays) -> GroupedMetadata:
-    dtype, dev, hidden, sizes, ptrs = checked
-    ptr_table, chunk_sizes, offsets, max_rows_dev, _ = arrays
-    return GroupedMetadata(
-        ptr_table, chunk_sizes, offsets, max(sizes), len(sizes),
-        max_rows_device=max_rows_dev, tensors=expert_tensors, sizes=sizes, ptrs=ptrs,
-        hidden=hidden, dtype=dtype, device=dev,
-    )
-
-
-def _metadata(expert_tensors, checked) -> GroupedMetadata:
-    dtype, dev, hidden, sizes, ptrs = checked
-    lib = _abi.lib()
-    E = len(sizes)
-    arrays = _meta_arrays(E, dev)
-    with torch.cuda.device(dev), _span("metadata"):
-        rc = lib.fmoe_build_metadata(
-            _host_table(ptrs), _host_table(sizes), E, arrays[0].data_ptr(), arrays[1].data_ptr(),
-            arrays[2].data_ptr(), arrays[3].data_ptr(), _stream_handle(dev),
-        )
-    _abi.check(rc, "fmoe_build_metadata")
-    return _new_metadata(expert_tensors, checked, arrays)
+def _metadata(ex: _Experts) -> GroupedMetadata:
+    m = _RawMeta(ex)
+    _run_metadata(ex, m)
+    return _new_metadata(ex, m)
 
 
 def _routing_args(indices: torch.Tensor, weights: torch.Tensor, num_rows: int, dev):
@@ -282,19 +359,15 @@ def _check_plan_status(plan: torch.Tensor, num_tokens: int) -> None:
         raise IndexError(f"fastmoe_amd: {bad} scatter indices lie outside [0, {num_tokens})")
 
 
-def _build_plan_raw(ptr_table, offsets_full, E: int, N: int, row_bytes: int, idx, w,
+def _build_plan_raw(ptr_table: int, offsets_full: int, E: int, N: int, row_bytes: int, idx, w,
                     num_tokens: int, dev) -> torch.Tensor:
-    """fmoe_build_plan into a new workspace; idx and w already flat and checked."""
-    lib = _abi.lib()
-    nbytes = lib.fmoe_plan_workspace_bytes(N, num_tokens)
-    if nbytes <= 0:
-        raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev), _span("plan"):
-        rc = lib.fmoe_build_plan(
+    """fmoe_build_plan into a new workspace (returned); the metadata arrays given by address, idx
+    and w already flat and checked."""
+    ws = torch.empty(_plan_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
+    with _on_device(dev), _span("plan"):
+        rc = _abi.lib().fmoe_build_plan(
             idx.data_ptr(), _INDEX_CODES[idx.dtype], w.data_ptr(), _FLOAT_CODES[w.dtype], N,
-            num_tokens, ptr_table.data_ptr(), offsets_full.data_ptr(), E, row_bytes,
-            ws.data_ptr(), _stream_handle(dev),
+            num_tokens, ptr_table, offsets_full, E, row_bytes, ws.data_ptr(), _stream_handle(dev),
         )
     _abi.check(rc, "fmoe_build_plan")
     return ws
@@ -309,9 +382,8 @@ def build_plan(meta: GroupedMetadata, indices: torch.Tensor, weights: torch.Tens
     """
     N = meta.num_rows
     idx, w = _routing_args(indices, weights, N, meta.device)
-    ws = _build_plan_raw(meta.ptr_table, meta.offsets_full, len(meta.sizes), N,
-                         meta.hidden * meta.tensors[0].element_size(), idx, w, num_tokens,
-                         meta.device)
+    ws = _build_plan_raw(meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(), len(meta.sizes),
+                         N, meta.hidden * _ELEM_BYTES[meta.dtype], idx, w, num_tokens, meta.device)
     if _validate_default(validate):
         _check_plan_status(ws, num_tokens)
     return ws
@@ -323,33 +395,19 @@ def prepare_metadata_and_plan(expert_tensors: Sequence[torch.Tensor], indices: t
     """``prepare_grouped_metadata`` followed by ``build_plan`` in one C-ABI call
     (``fmoe_build_metadata_and_plan``: the plan's own launches write the metadata for up to 256
     experts); returns ``(metadata, plan)``, each exactly what the two calls return."""
-    checked = _check_experts(expert_tensors)
-    idx, w = _routing_args(indices, weights, sum(checked[3]), checked[1])
-    return _metadata_and_plan(expert_tensors, checked, idx, w, num_tokens, validate)
+    ex = _check_experts(expert_tensors)
+    idx, w = _routing_args(indices, weights, ex.rows, ex.device)
+    return _metadata_and_plan(ex, idx, w, num_tokens, validate)
 
 
-def _metadata_and_plan(expert_tensors, checked, idx, w, num_tokens, validate):
+def _metadata_and_plan(ex: _Experts, idx, w, num_tokens, validate):
     """idx and w already flat and checked (_routing_args)."""
-    dtype, dev, hidden, sizes, ptrs = checked
-    lib = _abi.lib()
-    E, N = len(sizes), sum(sizes)
-    nbytes = lib.fmoe_plan_workspace_bytes(N, num_tokens)
-    if nbytes <= 0:
-        raise ValueError(f"fastmoe_amd: bad plan size N={N} T={num_tokens}")
-    arrays = _meta_arrays(E, dev, nbytes)
-    ws = arrays[4]
-    with torch.cuda.device(dev), _span("metadata_plan"):
-        rc = lib.fmoe_build_metadata_and_plan(
-            _host_table(ptrs), _host_table(sizes), E, arrays[0].data_ptr(), arrays[1].data_ptr(),
-            arrays[2].data_ptr(), arrays[3].data_ptr(), idx.data_ptr(), _INDEX_CODES[idx.dtype],
-            w.data_ptr(), _FLOAT_CODES[w.dtype], num_tokens,
-            hidden * expert_tensors[0].element_size(), ws.data_ptr(), _stream_handle(dev),
-        )
-    _abi.check(rc, "fmoe_build_metadata_and_plan")
-    meta = _new_metadata(expert_tensors, checked, arrays)
+    m = _RawMeta(ex, _plan_bytes(ex.rows, num_tokens))
+    _run_metadata_and_plan(ex, m, idx, w, num_tokens)
+    plan = m.plan_tensor()
     if _validate_default(validate):
-        _check_plan_status(ws, num_tokens)
-    return meta, ws
+        _check_plan_status(plan, num_tokens)
+    return _new_metadata(ex, m), plan
 
 
 def _check_slots(slot_pos, weights, N: int, num_tokens: int, top_k: int, dev):
@@ -364,15 +422,13 @@ def _check_slots(slot_pos, weights, N: int, num_tokens: int, top_k: int, dev):
     return slot_pos.contiguous(), w
 
 
-def _build_plan_from_slots_raw(ptr_table, offsets_full, E: int, N: int, row_bytes: int,
+def _build_plan_from_slots_raw(ptr_table: int, offsets_full: int, E: int, N: int, row_bytes: int,
                                slot_pos, w, num_tokens: int, top_k: int, dev) -> torch.Tensor:
-    lib = _abi.lib()
-    ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev), _span("plan"):
-        rc = lib.fmoe_build_plan_from_slots(
+    ws = torch.empty(_plan_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
+    with _on_device(dev), _span("plan"):
+        rc = _abi.lib().fmoe_build_plan_from_slots(
             slot_pos.data_ptr(), num_tokens, top_k, w.data_ptr(), _FLOAT_CODES[w.dtype],
-            ptr_table.data_ptr(), offsets_full.data_ptr(), E, N, row_bytes, ws.data_ptr(),
-            _stream_handle(dev),
+            ptr_table, offsets_full, E, N, row_bytes, ws.data_ptr(), _stream_handle(dev),
         )
     _abi.check(rc, "fmoe_build_plan_from_slots")
     return ws
@@ -388,9 +444,9 @@ def build_plan_from_slots(meta: GroupedMetadata, slot_pos: torch.Tensor, weights
     """
     N = meta.num_rows
     sp, w = _check_slots(slot_pos, weights, N, num_tokens, top_k, meta.device)
-    return _build_plan_from_slots_raw(meta.ptr_table, meta.offsets_full, len(meta.sizes), N,
-                                      meta.hidden * meta.tensors[0].element_size(), sp, w,
-                                      num_tokens, top_k, meta.device)
+    return _build_plan_from_slots_raw(meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(),
+                                      len(meta.sizes), N, meta.hidden * _ELEM_BYTES[meta.dtype],
+                                      sp, w, num_tokens, top_k, meta.device)
 
 
 def prepare_metadata_and_plan_from_slots(expert_tensors: Sequence[torch.Tensor],
@@ -399,26 +455,15 @@ def prepare_metadata_and_plan_from_slots(expert_tensors: Sequence[torch.Tensor],
     """``prepare_grouped_metadata`` followed by ``build_plan_from_slots`` in one C-ABI call
     (``fmoe_build_metadata_and_plan_from_slots``: one kernel launch for up to 256 experts);
     returns ``(metadata, plan)``."""
-    return _metadata_and_plan_from_slots(expert_tensors, _check_experts(expert_tensors), slot_pos,
-                                         weights, num_tokens, top_k)
+    return _metadata_and_plan_from_slots(_check_experts(expert_tensors), slot_pos, weights,
+                                         num_tokens, top_k)
 
 
-def _metadata_and_plan_from_slots(expert_tensors, checked, slot_pos, weights, num_tokens, top_k):
-    dtype, dev, hidden, sizes, ptrs = checked
-    lib = _abi.lib()
-    E, N = len(sizes), sum(sizes)
-    sp, w = _check_slots(slot_pos, weights, N, num_tokens, top_k, dev)
-    arrays = _meta_arrays(E, dev, lib.fmoe_plan_workspace_bytes(N, num_tokens))
-    ws = arrays[4]
-    with torch.cuda.device(dev), _span("metadata_plan"):
-        rc = lib.fmoe_build_metadata_and_plan_from_slots(
-            _host_table(ptrs), _host_table(sizes), E, arrays[0].data_ptr(), arrays[1].data_ptr(),
-            arrays[2].data_ptr(), arrays[3].data_ptr(), sp.data_ptr(), num_tokens, top_k,
-            w.data_ptr(), _FLOAT_CODES[w.dtype], hidden * expert_tensors[0].element_size(),
-            ws.data_ptr(), _stream_handle(dev),
-        )
-    _abi.check(rc, "fmoe_build_metadata_and_plan_from_slots")
-    return _new_metadata(expert_tensors, checked, arrays), ws
+def _metadata_and_plan_from_slots(ex: _Experts, slot_pos, weights, num_tokens, top_k):
+    sp, w = _check_slots(slot_pos, weights, ex.rows, num_tokens, top_k, ex.device)
+    m = _RawMeta(ex, _plan_bytes(ex.rows, num_tokens))
+    _run_metadata_and_plan_from_slots(ex, m, sp, w, num_tokens, top_k)
+    return _new_metadata(ex, m), m.plan_tensor()
 
 
 def invert_scatter_index(indices: torch.Tensor, num_tokens: int):
@@ -440,7 +485,7 @@ def invert_scatter_index(indices: torch.Tensor, num_tokens: int):
     row_ptr = torch.empty(num_tokens + 2, dtype=torch.int32, device=dev)
     rows = torch.empty(N, dtype=torch.int32, device=dev)
     ws = torch.empty(lib.fmoe_plan_workspace_bytes(N, num_tokens), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev), _span("invert_scatter_index"):
+    with _on_device(dev), _span("invert_scatter_index"):
         rc = lib.fmoe_invert_scatter_index(
             idx.data_ptr(), _INDEX_CODES[idx.dtype], N, num_tokens, row_ptr.data_ptr(),
             rows.data_ptr(), ws.data_ptr(), _stream_handle(dev),
@@ -472,32 +517,41 @@ def _check_out(out: torch.Tensor, num_tokens_hint, hidden: int, dev) -> None:
         raise ValueError("fastmoe_amd: out rows overlap")
 
 
-def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
-                idx: Optional[torch.Tensor], w: Optional[torch.Tensor], out: torch.Tensor,
-                accumulate: bool) -> None:
+def _launch_fwd_raw(mode: int, plan: Optional[int], idx: Optional[torch.Tensor],
+                    w: Optional[torch.Tensor], ptr_table: int, offsets_full: int, E: int, N: int,
+                    x_dtype: torch.dtype, out: torch.Tensor, accumulate: bool) -> None:
+    """fmoe_combine_fwd; the plan and the metadata arrays given by address."""
     lib = _abi.lib()
     T, D = out.shape
+    dev = out.device
     out_code = _FLOAT_CODES[out.dtype]
     ws, ws_bytes = None, 0
     if mode == _abi.MODE_ATOMIC and out_code != _abi.F32:
         # the fp32 accumulator of a 16-bit output (fmoe_combine_fwd_workspace_bytes)
         ws_bytes = lib.fmoe_combine_fwd_workspace_bytes(mode, T, D, out_code)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=meta.device)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     name = "fwd_det" if mode == _abi.MODE_DET else "fwd_atomic"
-    with torch.cuda.device(meta.device), _span(name):
+    with _on_device(dev), _span(name):
         rc = lib.fmoe_combine_fwd(
-            mode,
-            plan.data_ptr() if plan is not None else None,
+            mode, plan,
             idx.data_ptr() if idx is not None else None,
             _INDEX_CODES[idx.dtype] if idx is not None else _abi.I64,
             w.data_ptr() if w is not None else None,
             _FLOAT_CODES[w.dtype] if w is not None else _abi.F32,
-            meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(), len(meta.sizes),
-            meta.num_rows, T, D, _FLOAT_CODES[meta.dtype], out.data_ptr(), out_code,
+            ptr_table, offsets_full, E, N, T, D, _FLOAT_CODES[x_dtype], out.data_ptr(), out_code,
             out.stride(0) if T > 1 else D, 1 if accumulate else 0,
-            ws.data_ptr() if ws is not None else None, ws_bytes, _stream_handle(meta.device),
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream_handle(dev),
         )
     _abi.check(rc, "fmoe_combine_fwd")
+
+
+def _launch_fwd(meta: GroupedMetadata, mode: int, plan: Optional[torch.Tensor],
+                idx: Optional[torch.Tensor], w: Optional[torch.Tensor], out: torch.Tensor,
+                accumulate: bool) -> None:
+    """fmoe_combine_fwd from a GroupedMetadata and a plan tensor."""
+    _launch_fwd_raw(mode, plan.data_ptr() if plan is not None else None, idx, w,
+                    meta.ptr_table.data_ptr(), meta.offsets_full.data_ptr(), len(meta.sizes),
+                    meta.num_rows, meta.dtype, out, accumulate)
 
 
 # The one-launch small path (fmoe_combine_fwd_small / fmoe_combine_bwd_small): deterministic calls
@@ -524,18 +578,13 @@ def _use_small(rows: int, num_tokens: int, num_experts: int) -> bool:
     return choice == 2 or rows * num_tokens <= _SMALL_SCAN_LIMIT
 
 
-def _small_tables(checked) -> tuple:
-    """The (address, rows) host tables of the small path, from _check_experts' result."""
-    return _host_table(checked[4]), _host_table(checked[3])
-
-
 def _launch_fwd_small(tables, num_experts: int, idx: torch.Tensor, w: torch.Tensor,
                       x_dtype: torch.dtype, out: torch.Tensor, accumulate: bool) -> torch.Tensor:
     """fmoe_combine_fwd_small into ``out``; returns its status word (rows with an index outside
     [0, T)) on the device."""
     T, D = out.shape
     status = torch.empty(1, dtype=torch.int32, device=out.device)
-    with torch.cuda.device(out.device), _span("fwd_small"):
+    with _on_device(out.device), _span("fwd_small"):
         rc = _abi.lib().fmoe_combine_fwd_small(
             tables[0], tables[1], num_experts, idx.data_ptr(), _INDEX_CODES[idx.dtype],
             w.data_ptr(), _FLOAT_CODES[w.dtype], T, D, _FLOAT_CODES[x_dtype], out.data_ptr(),
@@ -560,22 +609,20 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
     if isinstance(metadata, GroupedMetadata) and metadata.matches(expert_tensors):
         idx, w = _routing_args(indices, weights, metadata.num_rows, metadata.device)
     else:
-        checked = _check_experts(expert_tensors)
-        rows = sum(checked[3])
-        idx, w = _routing_args(indices, weights, rows, checked[1])
+        ex = _check_experts(expert_tensors)
+        idx, w = _routing_args(indices, weights, ex.rows, ex.device)
         # The small path counts out-of-range indices in the same launch that accumulates into
         # ``out``; a validating call takes the planned path, which raises before any forward
         # launch, so ``out`` is left untouched when it raises.
         if (code == _abi.MODE_DET and not _validate_default(validate)
-                and _use_small(rows, T, len(checked[3]))):
-            _check_out(out, None, checked[2], checked[1])
-            _launch_fwd_small(_small_tables(checked), len(checked[3]), idx, w, checked[0], out,
-                              accumulate=True)
+                and _use_small(ex.rows, T, ex.num)):
+            _check_out(out, None, ex.hidden, ex.device)
+            _launch_fwd_small(ex.host_tables(), ex.num, idx, w, ex.dtype, out, accumulate=True)
             return out
-        if code == _abi.MODE_DET and rows > 0:
-            metadata, plan = _metadata_and_plan(expert_tensors, checked, idx, w, T, validate)
+        if code == _abi.MODE_DET and ex.rows > 0:
+            metadata, plan = _metadata_and_plan(ex, idx, w, T, validate)
         else:
-            metadata = _metadata(expert_tensors, checked)
+            metadata = _metadata(ex)
     _check_out(out, None, metadata.hidden, metadata.device)
     if metadata.max_rows == 0:  # ops.py:286: nothing to add
         return out
@@ -592,61 +639,67 @@ def _launch_grouped_kernel(expert_tensors, indices, weights, out, metadata=None,
 
 def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices, weights,
                      out_shape, expert_tensors, w_grad: bool, slots=None):
-    """Autograd forward.  ``w_grad``: the gate gradient will be asked for (the expert tensors are
-    then saved for the backward, which reads them for it; otherwise only the index and gates are,
-    as in the reference, ops.py:326)."""
-    checked = _check_experts(expert_tensors)
-    dtype, dev, hidden, sizes, ptrs = checked
+    """Autograd forward.  ``w_grad``: the gate gradient will be asked for.  The backward then
+    reads the expert buffers through the addresses in the plan (or the small path's tables), so
+    the forward keeps the tensors on ``ctx`` with the sum of their version counters, and the
+    backward refuses buffers modified in place since (torch's check of saved tensors).  They are
+    not passed through ``save_for_backward``: unpacking hundreds of saved tensors in every
+    backward costs more host time than the rest of the call (the reference saves only the index
+    and gates, ops.py:326, and needs no expert data in its backward)."""
+    ex = _check_experts(expert_tensors)
+    dtype, dev, hidden = ex.dtype, ex.device, ex.hidden
     shape = tuple(int(s) for s in out_shape)
     if len(shape) != 2 or shape[1] != hidden:
         raise ValueError(f"fastmoe_amd: out_shape {shape} must be [T, {hidden}]")
     T = shape[0]
     code = _mode_code(mode)
-    rows = sum(sizes)
+    rows = ex.rows
     idx, w = _routing_args(indices, weights, rows, dev)
     use_slots = slots is not None and rows == T * slots[1] and slots[1] <= 64
-    plan = meta = small = None
+    meta = small = None
     if rows == 0:
-        meta = _metadata(expert_tensors, checked)
+        meta = _RawMeta(ex)
+        _run_metadata(ex, meta)
         out = torch.zeros(shape, dtype=dtype, device=dev)
-    elif code == _abi.MODE_DET and _use_small(rows, T, len(sizes)):
+    elif code == _abi.MODE_DET and _use_small(rows, T, ex.num):
         # one launch, no plan; the backward is one launch too
-        small = _small_tables(checked)
+        small = ex.host_tables()
         out = torch.empty(shape, dtype=dtype, device=dev)
-        status = _launch_fwd_small(small, len(sizes), idx, w, dtype, out, accumulate=False)
+        status = _launch_fwd_small(small, ex.num, idx, w, dtype, out, accumulate=False)
         if _validate_default(validate):
             _check_small_status(status, T)
     elif code == _abi.MODE_DET:
-        # metadata and plan in one call; every output row is written exactly once (tokens
-        # without rows get zeros), so out needs no zero-fill
+        # metadata and plan in one workspace and one call; every output row is written exactly
+        # once (tokens without rows get zeros), so out needs no zero-fill
+        meta = _RawMeta(ex, _plan_bytes(rows, T))
         if use_slots:
-            meta, plan = _metadata_and_plan_from_slots(expert_tensors, checked, slots[0], w, T,
-                                                       slots[1])
+            sp, w = _check_slots(slots[0], w, rows, T, slots[1], dev)
+            _run_metadata_and_plan_from_slots(ex, meta, sp, w, T, slots[1])
         else:
-            meta, plan = _metadata_and_plan(expert_tensors, checked, idx, w, T, validate)
+            _run_metadata_and_plan(ex, meta, idx, w, T)
+            if _validate_default(validate):
+                _check_plan_status(meta.plan_tensor(), T)
         out = torch.empty(shape, dtype=dtype, device=dev)
-        _launch_fwd(meta, code, plan, None, None, out, accumulate=False)
+        _launch_fwd_raw(code, meta.plan, None, None, meta.ptr_table, meta.offsets, ex.num, rows,
+                        dtype, out, accumulate=False)
     else:
         # the atomic forward reads no plan: the backward builds it if a gradient is asked for
-        meta = _metadata(expert_tensors, checked)
+        meta = _RawMeta(ex)
+        _run_metadata(ex, meta)
         if _validate_default(validate):
-            _check_plan_status(_build_plan_raw(meta.ptr_table, meta.offsets_full, len(sizes), rows,
-                                               hidden * expert_tensors[0].element_size(), idx, w,
-                                               T, dev), T)
+            _check_plan_status(_build_plan_raw(meta.ptr_table, meta.offsets, ex.num, rows,
+                                               hidden * _ELEM_BYTES[dtype], idx, w, T, dev), T)
         out = torch.empty(shape, dtype=dtype, device=dev)  # overwritten: the library clears it
-        _launch_fwd(meta, code, None, idx, w, out, accumulate=False)
-    if w_grad:
-        ctx.save_for_backward(idx, w, *expert_tensors)
-    else:
-        ctx.save_for_backward(idx, w)
-    ctx.plan = plan
-    ctx.small = small
-    # what a deferred plan needs (device arrays only: no reference to the expert tensors)
-    ctx.meta_arrays = (meta.ptr_table, meta.offsets_full) if plan is None and meta else None
-    ctx.slots = (slots[0], slots[1]) if (use_slots and plan is None) else None
-    ctx.sizes = sizes
+        _launch_fwd_raw(code, None, idx, w, meta.ptr_table, meta.offsets, ex.num, rows, dtype,
+                        out, accumulate=False)
+    ctx.save_for_backward(idx, w)
+    ctx.experts = tuple(expert_tensors) if w_grad else None
+    ctx.x_version = _host().versions(expert_tensors) if w_grad else 0
+    ctx.meta = meta    # metadata and plan workspace (None on the small path)
+    ctx.small = small  # the small path's host tables
+    ctx.slots = (slots[0], slots[1]) if use_slots else None
+    ctx.sizes = ex.sizes
     ctx.hidden = hidden
-    ctx.row_bytes = hidden * expert_tensors[0].element_size()
     ctx.num_tokens = T
     ctx.x_dtype = dtype
     ctx.w_shape = weights.shape
@@ -654,30 +707,39 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
 
 
 def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
-    saved = ctx.saved_tensors
-    idx, w = saved[0], saved[1]
+    idx, w = ctx.saved_tensors
     sizes = ctx.sizes
     need_x = any(needs_x)
-    N, T, D = sum(sizes), ctx.num_tokens, ctx.hidden
+    N, T, D = idx.numel(), ctx.num_tokens, ctx.hidden
     dev = idx.device
     if not (needs_w or need_x):
         return None, [None] * len(sizes)
+    if needs_w and ctx.experts is not None and _host().versions(ctx.experts) != ctx.x_version:
+        raise RuntimeError(
+            "fastmoe_amd: an expert tensor needed for the gate gradient has been modified by an "
+            "inplace operation since the forward")
     if N == 0:
         gw = torch.zeros(ctx.w_shape, dtype=w.dtype, device=dev) if needs_w else None
         gx = [torch.zeros((n, D), dtype=ctx.x_dtype, device=dev) if need else None
               for n, need in zip(sizes, needs_x)]
         return gw, gx
-    plan = ctx.plan
-    small = getattr(ctx, "small", None)
-    if plan is None and small is None:  # atomic forward: the plan now
-        ptr_table, offsets_full = ctx.meta_arrays
+    small = ctx.small
+    meta = ctx.meta
+    plan_ws = None
+    if small is not None:
+        plan = None
+    elif meta.plan is not None:
+        plan = meta.plan
+    else:  # atomic forward: the plan now
+        row_bytes = D * _ELEM_BYTES[ctx.x_dtype]
         if ctx.slots is not None:
-            plan = _build_plan_from_slots_raw(ptr_table, offsets_full, len(sizes), N,
-                                              ctx.row_bytes, ctx.slots[0], w, T, ctx.slots[1],
-                                              dev)
+            sp, ws_w = _check_slots(ctx.slots[0], w, N, T, ctx.slots[1], dev)
+            plan_ws = _build_plan_from_slots_raw(meta.ptr_table, meta.offsets, meta.E, N,
+                                                 row_bytes, sp, ws_w, T, ctx.slots[1], dev)
         else:
-            plan = _build_plan_raw(ptr_table, offsets_full, len(sizes), N, ctx.row_bytes, idx, w,
-                                   T, dev)
+            plan_ws = _build_plan_raw(meta.ptr_table, meta.offsets, meta.E, N, row_bytes, idx, w,
+                                      T, dev)
+        plan = plan_ws.data_ptr()
     go = grad_output
     if go.dtype != ctx.x_dtype:
         go = go.to(ctx.x_dtype)
@@ -687,36 +749,36 @@ def _combine_backward(ctx, grad_output, needs_w: bool, needs_x: Sequence[bool]):
     gw = torch.empty(N, dtype=w.dtype, device=dev) if needs_w else None
     lib = _abi.lib()
     stream = _stream_handle(dev)
-
-    def launch(name, gx_ptr, gw_ptr):
-        with torch.cuda.device(dev), _span(name):
-            rc = lib.fmoe_combine_bwd(
-                plan.data_ptr(), N, T, D, _FLOAT_CODES[ctx.x_dtype], go.data_ptr(),
-                _FLOAT_CODES[go.dtype], go.stride(0) if T > 1 else D, gx_ptr, gw_ptr,
-                _FLOAT_CODES[w.dtype], stream,
-            )
-        _abi.check(rc, "fmoe_combine_bwd")
-
+    x_code, g_code, w_code = _FLOAT_CODES[ctx.x_dtype], _FLOAT_CODES[go.dtype], _FLOAT_CODES[w.dtype]
+    g_stride = go.stride(0) if T > 1 else D
     gx_ptr = gx.data_ptr() if gx is not None else None
     gw_ptr = gw.data_ptr() if gw is not None else None
-    if small is not None:
-        # both gradients (or either) in one launch, no plan
-        with torch.cuda.device(dev), _span("bwd_small"):
-            rc = lib.fmoe_combine_bwd_small(
-                small[0], small[1], len(sizes), idx.data_ptr(), _INDEX_CODES[idx.dtype],
-                w.data_ptr(), _FLOAT_CODES[w.dtype], T, D, _FLOAT_CODES[ctx.x_dtype],
-                go.data_ptr(), _FLOAT_CODES[go.dtype], go.stride(0) if T > 1 else D, gx_ptr,
-                gw_ptr, _FLOAT_CODES[w.dtype], stream)
-        _abi.check(rc, "fmoe_combine_bwd_small")
-    elif gx_ptr and gw_ptr and not _abi.option("bwd_fused"):
-        # The grad_X (write) and grad_w (read) passes, one call each -- the same two launches
-        # fmoe_combine_bwd makes when given both outputs, issued separately so each is timed.
-        launch("bwd_gx", gx_ptr, None)
-        launch("bwd_gw", None, gw_ptr)
-    else:
-        launch("bwd" if gx_ptr and gw_ptr else ("bwd_gx" if gx_ptr else "bwd_gw"), gx_ptr, gw_ptr)
+    with _on_device(dev):
+        if small is not None:
+            # both gradients (or either) in one launch, no plan
+            with _span("bwd_small"):
+                rc = lib.fmoe_combine_bwd_small(
+                    small[0], small[1], len(sizes), idx.data_ptr(), _INDEX_CODES[idx.dtype],
+                    w.data_ptr(), w_code, T, D, x_code, go.data_ptr(), g_code, g_stride, gx_ptr,
+                    gw_ptr, w_code, stream)
+            _abi.check(rc, "fmoe_combine_bwd_small")
+        elif gx_ptr and gw_ptr and _TIMER is not None and not _abi.option("bwd_fused"):
+            # Timed: the grad_X (write) and grad_w (read) passes, one call each -- the same two
+            # launches fmoe_combine_bwd makes when given both outputs, issued separately so that
+            # each gets its own span.
+            for name, a, b in (("bwd_gx", gx_ptr, None), ("bwd_gw", None, gw_ptr)):
+                with _span(name):
+                    rc = lib.fmoe_combine_bwd(plan, N, T, D, x_code, go.data_ptr(), g_code,
+                                              g_stride, a, b, w_code, stream)
+                _abi.check(rc, "fmoe_combine_bwd")
+        else:
+            name = "bwd" if gx_ptr and gw_ptr else ("bwd_gx" if gx_ptr else "bwd_gw")
+            with _span(name):
+                rc = lib.fmoe_combine_bwd(plan, N, T, D, x_code, go.data_ptr(), g_code, g_stride,
+                                          gx_ptr, gw_ptr, w_code, stream)
+            _abi.check(rc, "fmoe_combine_bwd")
     if need_x:
-        parts = torch.split(gx, list(sizes))
+        parts = torch.split(gx, sizes)
         grads_x = parts if all(needs_x) else [p if n else None for p, n in zip(parts, needs_x)]
     else:
         grads_x = [None] * len(sizes)

@@ -120,7 +120,7 @@ def _fake_lib(monkeypatch):
     monkeypatch.setattr(_abi, "lib", lambda: f)
     monkeypatch.setattr(ops, "_require_cuda", lambda t, what: None)
     monkeypatch.setattr(ops, "_stream_handle", lambda dev: 0)
-    monkeypatch.setattr(torch.cuda, "device", lambda dev: contextlib.nullcontext())
+    monkeypatch.setattr(ops, "_on_device", lambda dev: contextlib.nullcontext())
     return f
 
 
@@ -153,14 +153,35 @@ def test_autograd_forward_and_backward_calls(fake):
     assert out.shape == (4, 16) and out.dtype == torch.bfloat16
     grads = torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
     kinds = [c[0] for c in fake.calls]
-    assert kinds == ["metadata_plan", "fwd", "bwd", "bwd"]
+    assert kinds == ["metadata_plan", "fwd", "bwd"]
     assert fake.calls[0] == ("metadata_plan", 3, [3, 0, 5], 4, 32, _abi.I64, _abi.F32)
     assert fake.calls[1] == ("fwd", _abi.MODE_DET, 8, 4, 16, _abi.BF16, _abi.BF16, 16, 0)
+    # one call with both outputs (the library runs the grad_X pass, then the grad_w pass)
+    assert fake.calls[2] == ("bwd", 8, 4, 16, _abi.BF16, 16, True, True, _abi.F32)
+    assert grads[0].shape == (N,) and grads[0].dtype == torch.float32
+    assert [g.shape[0] for g in grads[1:]] == [3, 0, 5]
+
+
+class _Timer:
+    def __init__(self):
+        self.names = []
+
+    def span(self, name):
+        self.names.append(name)
+        return contextlib.nullcontext()
+
+
+def test_timed_backward_issues_each_pass_in_its_own_span(fake, monkeypatch):
+    timer = _Timer()
+    monkeypatch.setattr(ops, "_TIMER", timer)
+    xs = [x.requires_grad_(True) for x in _experts()]
+    w = torch.rand(8, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.randint(0, 4, (8,)), w, (4, 16))
+    torch.autograd.grad(out, [w, *xs], torch.ones(4, 16, dtype=torch.bfloat16))
+    assert timer.names == ["metadata_plan", "fwd_det", "bwd_gx", "bwd_gw"]
     # grad_X pass, then grad_w pass
     assert fake.calls[2] == ("bwd", 8, 4, 16, _abi.BF16, 16, True, False, _abi.F32)
     assert fake.calls[3] == ("bwd", 8, 4, 16, _abi.BF16, 16, False, True, _abi.F32)
-    assert grads[0].shape == (N,) and grads[0].dtype == torch.float32
-    assert [g.shape[0] for g in grads[1:]] == [3, 0, 5]
 
 
 def test_fused_backward_is_one_call(fake):
@@ -216,19 +237,34 @@ def test_atomic_mode_overwrites_and_defers_the_plan(fake):
                                                    (4, 16), mode="atomic")
     assert [c[0] for c in fake.calls] == ["metadata", "fwd"]
     torch.autograd.grad(out, [wg, *xg], torch.ones(4, 16))
-    assert [c[0] for c in fake.calls] == ["metadata", "fwd", "plan", "bwd", "bwd"]
+    assert [c[0] for c in fake.calls] == ["metadata", "fwd", "plan", "bwd"]
 
 
-def test_gate_gradient_keeps_the_weights_shape_and_experts_saved_only_for_it(fake):
+def test_gate_gradient_keeps_the_weights_shape_and_experts_kept_only_for_it(fake):
     xs = [x.requires_grad_(True) for x in _experts(torch.float32)]
     w = torch.rand(4, 2, requires_grad=True)  # [T, k]-shaped gates
     out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long), w, (2, 16))
-    assert len(out.grad_fn.saved_tensors) == 2 + len(xs)
+    assert len(out.grad_fn.saved_tensors) == 2  # index and gates, as the reference saves
+    assert all(a is b for a, b in zip(out.grad_fn.experts, xs))  # read by the grad_w pass
     (gw,) = torch.autograd.grad(out, [w], torch.ones(2, 16))
     assert gw.shape == w.shape
     out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long),
                                                    w.detach(), (2, 16))
-    assert len(out.grad_fn.saved_tensors) == 2  # index and gates only, as the reference saves
+    assert len(out.grad_fn.saved_tensors) == 2 and out.grad_fn.experts is None
+
+
+@pytest.mark.parametrize("fixture", ["fake", "fake_small"])
+def test_gate_gradient_refuses_experts_modified_in_place(fixture, request):
+    """The grad_w pass reads the expert buffers: one modified in place after the forward makes
+    the backward raise, as torch does for a modified saved tensor."""
+    request.getfixturevalue(fixture)
+    xs = [x.requires_grad_(True) for x in _experts(torch.float32)]
+    w = torch.rand(8, requires_grad=True)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, torch.zeros(8, dtype=torch.long), w, (4, 16))
+    with torch.no_grad():
+        xs[2].mul_(2)
+    with pytest.raises(RuntimeError, match="modified by an inplace operation"):
+        torch.autograd.grad(out, [w], torch.ones(4, 16))
 
 
 def test_stale_metadata_is_rebuilt(fake):
