@@ -37,6 +37,7 @@ static const OptDef kOpts[] = {
     {"fwd_atomic_tile", "FMOE_FWD_ATOMIC_TILE", 0},
     {"fwd_det_u", "FMOE_FWD_DET_U", 0}, {"fwd_grid", "FMOE_FWD_GRID", 0},
     {"plan_groups", "FMOE_PLAN_GROUPS", 0}, {"small", "FMOE_SMALL", 0},
+    {"fwd_atomic_order", "FMOE_FWD_ATOMIC_ORDER", 0},
 };
 constexpr int kNumOpts = (int)(sizeof(kOpts) / sizeof(kOpts[0]));
 static_assert(kNumOpts == kOptCount, "one table entry per enum Opt value");

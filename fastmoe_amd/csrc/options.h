@@ -22,6 +22,8 @@ enum Opt {
   kOptPlanGroups,    // "plan_groups": workgroups of the one-launch plan (0 = by N and T)
   kOptSmall,         // "small": the host's choice of the one-launch small path (0 = by size,
                      // 1 = never, 2 = whenever its limits allow)
+  kOptAtomicOrder,   // "fwd_atomic_order": atomic forward's grid order (0 = by size, 1 = row
+                     // chunks together, 2 = column-chunk-major)
   kOptCount
 };
 int64_t opt(int o);

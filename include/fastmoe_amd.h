@@ -111,6 +111,9 @@ FMOE_API const char* fmoe_last_error(void);
  *   "small"           [FMOE_SMALL]     the Python host's use of fmoe_combine_fwd_small /
  *                                      fmoe_combine_bwd_small: 0 = by size, 1 = never, 2 = whenever
  *                                      their limits allow (the library itself does not read it)
+ *   "fwd_atomic_order" [FMOE_FWD_ATOMIC_ORDER] grid order of the atomic forward: 0 = by size,
+ *                                      1 = a row's column chunks side by side, 2 = column-chunk
+ *                                      major (all rows' chunk 0, then chunk 1, ...)
  * fmoe_set_option returns FMOE_EINVAL for an unknown name; *previous (if not NULL) gets the old
  * value.  Not synchronised with launches in flight on other threads.
  */
