@@ -227,3 +227,24 @@ def test_library_missing_a_symbol_fails_loudly(monkeypatch, tmp_path):
     with pytest.raises(_abi.FastMoEError, match="does not export fmoe_last_error"):
         _abi.lib()
     monkeypatch.setattr(_abi, "_LIB", None)
+
+
+def _documented_options():
+    """Option names listed in the header's comment on fmoe_set_option (``"name" [FMOE_ENV]``
+    entries, or the names of a shared line)."""
+    text = HEADER.read_text()
+    block = text[text.index("Kernel-variant options"): text.index("FMOE_API int fmoe_set_option")]
+    return set(re.findall(r'"(\w+)"', block))
+
+
+def test_every_documented_option_reads_and_sets():
+    names = _documented_options()
+    assert {"plan", "small", "fwd_atomic_order", "fwd_atomic_tile"} <= names
+    for name in sorted(names):
+        v = ctypes.c_int64(-99)
+        assert _abi.lib().fmoe_get_option(name.encode(), ctypes.byref(v)) == _abi.OK, name
+        prev = _abi.set_option(name, v.value + 1)
+        assert prev == v.value and _abi.option(name) == v.value + 1
+        _abi.set_option(name, prev)
+    v = ctypes.c_int64(0)
+    assert _abi.lib().fmoe_get_option(b"no_such_option", ctypes.byref(v)) == _abi.EINVAL

@@ -62,13 +62,16 @@ def test_fwd_det_bitexact(name):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32) if want.dtype == np.float32 else want)
 
 
+@pytest.mark.parametrize("order", [1, 2], ids=["row_chunks", "chunk_major"])
 @pytest.mark.parametrize("mode", ["atomic", "atomic_packed"])
 @pytest.mark.parametrize("name", list(SCALED))
-def test_fwd_atomic_within_reordering(name, mode):
-    """Atomic forwards against the oracle.  fp32 outputs (both modes): within the gap of two fp32
+def test_fwd_atomic_within_reordering(name, mode, order, kernel_options):
+    """Atomic forwards against the oracle, in both grid orders (a row's column chunks side by
+    side, and column-chunk-major).  fp32 outputs (both modes): within the gap of two fp32
     summation orders.  16-bit outputs: "atomic" accumulates in fp32 and rounds once, so within one
     ulp of the oracle's result (the sequential fp32 sum rounded once) plus that gap;
     "atomic_packed" rounds at every add, within the (n + 2) u sum|terms| rounding model."""
+    kernel_options(fwd_atomic_order=order)
     wl, T, idx, w, experts = _inputs(name)
     xd, idd, wd = _to_dev(experts, idx, w)
     out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, wl.D), mode=mode)
