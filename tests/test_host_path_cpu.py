@@ -471,3 +471,44 @@ def test_unit_gates_never_release_a_buffer_handed_out(monkeypatch):
         assert any(lo <= ptr and ptr + 4 * n <= hi for lo, hi in spans)
     # growth at least doubles: the retired buffers hold fewer elements than the live one
     assert sum(b.numel() for b in dispatch._RETIRED) < dispatch._ONES[dev].numel()
+
+
+def test_host_helper_validates_and_packs_expert_tables():
+    """fastmoe_amd._host.experts: the (address, rows) table of a list of buffers, and the first
+    offending buffer named for every kind of bad input."""
+    from fastmoe_amd import _host
+
+    base = torch.randn(40, 8)
+    xs = [base[0:3], torch.empty(0, 8), base[10:15], torch.randn(1, 8)]
+    hidden, rows, max_rows, table = _host.experts(xs)
+    t = memoryview(table).cast("q").tolist()
+    assert (hidden, rows, max_rows) == (8, 9, 5)
+    assert t[:4] == [xs[0].data_ptr(), 0, xs[2].data_ptr(), xs[3].data_ptr()]
+    assert t[4:] == [3, 0, 5, 1]
+    cases = [
+        ([base[:3], "x"], TypeError, r"expert_tensors\[1\] is not a tensor"),
+        ([base[:3], base[:3].double()], ValueError, r"\[1\] differs in device/dtype"),
+        ([base[:3], torch.randn(2, 9)], ValueError, r"\[1\] has shape \(2, 9\), expected \[\*, 8\]"),
+        ([base[:3], torch.randn(8)], ValueError, r"\[1\] has shape \(8,\)"),
+        ([torch.randn(8)], ValueError, r"\[0\] must be 2-D"),
+        ([base[:3], base[:, :16].t()[:, :8]], ValueError, r"\[1\] must be row-contiguous"),
+        ([base[:3], torch.randn(1, 8).expand(4, 8)], ValueError, r"row-contiguous \(strides \(0, 1\)\)"),
+        ([base[:3], torch.randn(4, 8).to_sparse()], ValueError, r"\[1\] must be a dense"),
+        ([], ValueError, "empty"),
+    ]
+    for bad, exc, msg in cases:
+        with pytest.raises(exc, match=msg):
+            _host.experts(bad)
+    # one row with any row stride is row-contiguous (torch's is_contiguous)
+    assert _host.experts([base[5:6], base[::5][:1]])[1] == 2
+
+
+def test_host_helper_version_sum_grows_on_in_place_writes():
+    from fastmoe_amd import _host
+
+    xs = [torch.randn(3, 4) for _ in range(5)]
+    v0 = _host.versions(xs)
+    xs[3].add_(1)
+    assert _host.versions(xs) > v0
+    with pytest.raises(TypeError):
+        _host.versions([xs[0], 3])
