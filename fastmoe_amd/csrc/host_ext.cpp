@@ -7,10 +7,11 @@
 // the same properties from the tensors' C++ objects in one pass.  It only inspects tensors and
 // writes host memory: no device memory is touched and no HIP call is made.
 //
-//   experts(seq) -> (hidden, n_rows, max_rows, table)
+//   experts(seq, versions=False) -> (hidden, n_rows, max_rows, table, version_sum)
 //       Every element must be a tensor with the dtype and device of seq[0], 2-D with seq[0]'s
 //       column count, and row-contiguous (is_contiguous()).  table is a bytearray of 16 * E bytes:
 //       the E data addresses (int64; 0 for an expert without rows), then the E row counts.
+//       version_sum is versions(seq) when asked for, else 0.
 //   versions(seq) -> int
 //       Sum of the tensors' autograd version counters.  Counters never decrease, so the sum
 //       grows whenever any tensor is modified in place.
@@ -39,7 +40,10 @@ std::string dims(c10::IntArrayRef v) {
   return s + (v.size() == 1 ? ",)" : ")");
 }
 
-PyObject* experts(PyObject*, PyObject* seq) {
+PyObject* experts(PyObject*, PyObject* args) {
+  PyObject* seq = nullptr;
+  int with_versions = 0;
+  if (!PyArg_ParseTuple(args, "O|p", &seq, &with_versions)) return nullptr;
   PyObject* fast = PySequence_Fast(seq, "fastmoe_amd: expert_tensors must be a sequence");
   if (!fast) return nullptr;
   const Py_ssize_t E = PySequence_Fast_GET_SIZE(fast);
@@ -58,6 +62,7 @@ PyObject* experts(PyObject*, PyObject* seq) {
   PyObject** items = PySequence_Fast_ITEMS(fast);
   PyObject* err = nullptr;
   int64_t hidden = 0, total = 0, max_rows = 0;
+  long long version_sum = 0;
   at::ScalarType dtype = at::ScalarType::Undefined;
   c10::Device device(c10::DeviceType::CPU);
   try {
@@ -96,6 +101,7 @@ PyObject* experts(PyObject*, PyObject* seq) {
       rows[i] = n;
       total += n;
       if (n > max_rows) max_rows = n;
+      if (with_versions) version_sum += (long long)t._version();
     }
   }
   } catch (const std::exception& e) {  // a tensor type whose accessors throw
@@ -106,8 +112,8 @@ PyObject* experts(PyObject*, PyObject* seq) {
     Py_DECREF(table);
     return nullptr;
   }
-  PyObject* res = Py_BuildValue("(LLLN)", (long long)hidden, (long long)total,
-                                (long long)max_rows, table);
+  PyObject* res = Py_BuildValue("(LLLNL)", (long long)hidden, (long long)total,
+                                (long long)max_rows, table, version_sum);
   if (!res) Py_DECREF(table);
   return res;
 }
@@ -131,9 +137,9 @@ PyObject* versions(PyObject*, PyObject* seq) {
 }
 
 PyMethodDef kMethods[] = {
-    {"experts", experts, METH_O,
-     "experts(seq) -> (hidden, n_rows, max_rows, table): validate the expert "
-     "buffers and pack their (address, rows) pairs"},
+    {"experts", experts, METH_VARARGS,
+     "experts(seq, versions=False) -> (hidden, n_rows, max_rows, table, version_sum): validate "
+     "the expert buffers and pack their (address, rows) pairs"},
     {"versions", versions, METH_O, "versions(seq) -> sum of the tensors' version counters"},
     {nullptr, nullptr, 0, nullptr}};
 

@@ -184,12 +184,14 @@ class _Experts:
     row count, and ``table``, a bytearray of the E data addresses then the E row counts (int64),
     which the C ABI takes as its two host tables."""
 
-    __slots__ = ("tensors", "dtype", "device", "hidden", "rows", "max_rows", "table", "num")
+    __slots__ = ("tensors", "dtype", "device", "hidden", "rows", "max_rows", "table", "num",
+                 "versions")
 
-    def __init__(self, tensors, dtype, device, hidden, rows, max_rows, table):
+    def __init__(self, tensors, dtype, device, hidden, rows, max_rows, table, versions):
         self.tensors, self.dtype, self.device, self.hidden = tensors, dtype, device, hidden
         self.rows, self.max_rows, self.table = rows, max_rows, table
         self.num = len(table) // 16
+        self.versions = versions  # sum of the autograd version counters, if asked for
 
     @property
     def ptrs(self) -> list:
@@ -206,7 +208,7 @@ class _Experts:
                 (ctypes.c_int64 * E).from_buffer(self.table, 8 * E))
 
 
-def _check_experts(expert_tensors: Sequence[torch.Tensor]) -> _Experts:
+def _check_experts(expert_tensors: Sequence[torch.Tensor], versions: bool = False) -> _Experts:
     """Validate the expert buffers.
 
     Every buffer must be a 2-D [rows, D] tensor of one float dtype on one GPU, row-contiguous
@@ -221,8 +223,8 @@ def _check_experts(expert_tensors: Sequence[torch.Tensor]) -> _Experts:
     _require_cuda(ref, "expert_tensors[0]")
     if ref.dtype not in _FLOAT_CODES:
         raise TypeError(f"fastmoe_amd: unsupported expert dtype {ref.dtype}")
-    hidden, rows, max_rows, table = _host().experts(expert_tensors)
-    return _Experts(expert_tensors, ref.dtype, ref.device, hidden, rows, max_rows, table)
+    hidden, rows, max_rows, table, vsum = _host().experts(expert_tensors, versions)
+    return _Experts(expert_tensors, ref.dtype, ref.device, hidden, rows, max_rows, table, vsum)
 
 
 _ELEM_BYTES = {torch.float32: 4, torch.bfloat16: 2, torch.float16: 2}
@@ -646,7 +648,7 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
     not passed through ``save_for_backward``: unpacking hundreds of saved tensors in every
     backward costs more host time than the rest of the call (the reference saves only the index
     and gates, ops.py:326, and needs no expert data in its backward)."""
-    ex = _check_experts(expert_tensors)
+    ex = _check_experts(expert_tensors, w_grad)
     dtype, dev, hidden = ex.dtype, ex.device, ex.hidden
     shape = tuple(int(s) for s in out_shape)
     if len(shape) != 2 or shape[1] != hidden:
@@ -694,7 +696,7 @@ def _combine_forward(ctx, mode: Optional[str], validate: Optional[bool], indices
                         out, accumulate=False)
     ctx.save_for_backward(idx, w)
     ctx.experts = tuple(expert_tensors) if w_grad else None
-    ctx.x_version = _host().versions(expert_tensors) if w_grad else 0
+    ctx.x_version = ex.versions
     ctx.meta = meta    # metadata and plan workspace (None on the small path)
     ctx.small = small  # the small path's host tables
     ctx.slots = (slots[0], slots[1]) if use_slots else None

@@ -480,7 +480,8 @@ def test_host_helper_validates_and_packs_expert_tables():
 
     base = torch.randn(40, 8)
     xs = [base[0:3], torch.empty(0, 8), base[10:15], torch.randn(1, 8)]
-    hidden, rows, max_rows, table = _host.experts(xs)
+    hidden, rows, max_rows, table, vsum = _host.experts(xs)
+    assert vsum == 0 and _host.experts(xs, True)[4] == _host.versions(xs)
     t = memoryview(table).cast("q").tolist()
     assert (hidden, rows, max_rows) == (8, 9, 5)
     assert t[:4] == [xs[0].data_ptr(), 0, xs[2].data_ptr(), xs[3].data_ptr()]
