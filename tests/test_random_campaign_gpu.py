@@ -15,6 +15,8 @@ Every assertion message names the case and its configuration.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -28,6 +30,10 @@ from tests.helpers import (abs_dot, abs_sum, bits, oracle_bwd, oracle_fwd, packe
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 DTS = [torch.float32, torch.bfloat16, torch.float16]
+# Wider runs of the same campaigns (off the suite, on a GPU box): FMOE_CAMPAIGN_SEED shifts every
+# campaign's seed, FMOE_CAMPAIGN_SCALE multiplies its case count.
+SEED_SHIFT = int(os.environ.get("FMOE_CAMPAIGN_SEED", "0"))
+SCALE = max(1, int(os.environ.get("FMOE_CAMPAIGN_SCALE", "1")))
 
 
 def _logu(rng, hi: int) -> int:
@@ -46,8 +52,8 @@ def _expect_bits(got: torch.Tensor, want: np.ndarray, label: str) -> None:
 
 
 def test_campaign_autograd(kernel_options):
-    rng = np.random.default_rng(1101)
-    for case in range(120):
+    rng = np.random.default_rng(1101 + SEED_SHIFT)
+    for case in range(120 * SCALE):
         T = _logu(rng, 20000)
         D = int(rng.choice([1, 3, 8, 16, 64, 100, 512, 1024, 2048, 4104]))
         cap = max(1, min(65536, (1 << 21) // D, max(64 * T, 5000)))
@@ -82,20 +88,43 @@ def test_campaign_autograd(kernel_options):
         # with the automatic plan, half the cases force the one-launch small path where its
         # limits (4096 rows, 256 experts) allow it; the others take the default choice
         small = 2 if plan == 0 and rng.random() < 0.5 else 0
-        kernel_options(plan=plan, bwd_fused=1 if fused else 0, small=small)
+        # forward mode: det mostly; the atomic modes in some cases (atomic_packed needs whole
+        # 16-byte vectors of a 16-bit output)
+        m = rng.random()
+        mode = "atomic" if m < 0.15 else ("atomic_packed" if m < 0.25 else "det")
+        if mode == "atomic_packed" and xdt != torch.float32 and D % 8:
+            mode = "atomic"
+        order = int(rng.integers(1, 3))  # the atomic grid's order
+        kernel_options(plan=plan, bwd_fused=1 if fused else 0, small=small,
+                       fwd_atomic_order=order)
         label = (f"autograd case {case}: T={T} N={N} E={E} D={D} {routing} {xdt} {wdt} {idt} "
-                 f"plan={plan} fused={fused} small={small}")
-        gen = torch.Generator().manual_seed(1101 * 1000 + case)
+                 f"plan={plan} fused={fused} small={small} mode={mode} order={order}")
+        gen = torch.Generator().manual_seed((1101 + SEED_SHIFT) * 1000 + case)
         idx_t = torch.from_numpy(np.asarray(idx, dtype=np.int64)).to(idt)
         w = torch.rand(N, generator=gen).to(wdt)
         experts = [torch.randn(n, D, generator=gen).to(xdt) for n in sizes]
         xs = [x.to(DEV).requires_grad_(True) for x in experts]
         wd = w.to(DEV).requires_grad_(True)
-        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx_t.to(DEV), wd, (T, D))
+        out = fastmoe_amd.grouped_weighted_scatter_add(xs, idx_t.to(DEV), wd, (T, D), mode=mode)
         go = torch.randn(T, D, generator=gen).to(xdt)
         grads = torch.autograd.grad(out, [wd, *xs], go.to(DEV))
-        want, _, _ = oracle_fwd(experts, idx_t, w, T, xdt)
-        _expect_bits(out, want, label)
+        want, acc, _ = oracle_fwd(experts, idx_t, w, T, xdt)
+        if mode == "det":
+            _expect_bits(out, want, label)
+        else:
+            i64 = idx_t.to(torch.int64).numpy()
+            valid = (i64 >= 0) & (i64 < T)
+            k = max(2, int(np.bincount(i64[valid], minlength=T).max()) if valid.any() else 2)
+            fscale = abs_sum(experts, idx_t, w, T)
+            got = out.detach().float().cpu().numpy()
+            if xdt == torch.float32:
+                assert np.all(np.abs(got - acc) <= reorder_tol(k, fscale)), label
+            else:
+                want16 = torch.from_numpy(want.view(np.int16)).view(xdt).float().numpy()
+                if mode == "atomic":
+                    assert np.all(within_one_ulp16(got, want16, xdt, k, fscale)), label
+                else:
+                    assert np.all(np.abs(got - want16) <= packed_tol(k, fscale, xdt)), label
         want_gx, want_gw = oracle_bwd(experts, idx_t, w, T, go)
         got_gx = np.concatenate([to_np(g).reshape(-1, D) for g in grads[1:]])
         np.testing.assert_array_equal(got_gx.view(want_gx.dtype), want_gx, err_msg=label)
@@ -106,9 +135,9 @@ def test_campaign_autograd(kernel_options):
 
 
 def test_campaign_permutation_and_inplace(kernel_options):
-    rng = np.random.default_rng(2202)
-    for case in range(160):
-        gen = torch.Generator().manual_seed(2202 * 1000 + case)
+    rng = np.random.default_rng(2202 + SEED_SHIFT)
+    for case in range(160 * SCALE):
+        gen = torch.Generator().manual_seed((2202 + SEED_SHIFT) * 1000 + case)
         if case % 2:
             T, k = _logu(rng, 10000), int(rng.integers(1, 9))
             E = int(rng.choice([1, 2, 7, 64, 256, 1000, 1025, 3000, 4096]))
@@ -190,9 +219,9 @@ def test_campaign_permutation_and_inplace(kernel_options):
 
 
 def test_campaign_inverse_slot_plan_and_graphs(kernel_options):
-    rng = np.random.default_rng(3303)
-    for case in range(150):
-        gen = torch.Generator().manual_seed(3303 * 1000 + case)
+    rng = np.random.default_rng(3303 + SEED_SHIFT)
+    for case in range(150 * SCALE):
+        gen = torch.Generator().manual_seed((3303 + SEED_SHIFT) * 1000 + case)
         kind = case % 3
         if kind == 0:
             T = _logu(rng, 60000)
