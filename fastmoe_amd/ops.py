@@ -103,14 +103,18 @@ def _validate_default(validate: Optional[bool]) -> bool:
     return _DEFAULT_VALIDATE if validate is None else bool(validate)
 
 
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch._C._cuda_getDevice()
+
+
 def _stream_handle(device: torch.device) -> int:
     """The raw handle of ``device``'s current stream (every launch goes on it)."""
-    return torch._C._cuda_getCurrentRawStream(device.index)
+    return torch._C._cuda_getCurrentRawStream(_device_index(device))
 
 
 def _on_device(device: torch.device):
     """``torch.cuda.device(device)``, or nothing when it is already the current device."""
-    if torch._C._cuda_getDevice() == device.index:
+    if torch._C._cuda_getDevice() == _device_index(device):
         return contextlib.nullcontext()
     return torch.cuda.device(device)
 
