@@ -569,6 +569,165 @@ CONFIG_LINES = [("mid", "det"), ("mid", "atomic"), ("skewed", "det"), ("skewed",
                 ("detatomic", "det"), ("detatomic", "atomic"), ("plumbing", "det")]
 
 
+# --plan-sweep shapes: (tokens, rows, rows sent to one hot token).  Uniform random scatter
+# indices over 256 experts of random sizes; the slot-map plan is timed where the rows are a top-k
+# routing (rows = k * tokens, no hot token).
+PLAN_SWEEP_CASES = [(4096, 32768, 0), (8192, 49152, 0), (32768, 65536, 0), (16384, 131072, 0),
+                    (1, 131072, 0), (100, 131072, 65536), (32768, 262144, 0),
+                    (32768, 262144, 65536), (65536, 1048576, 0), (1048576, 2097152, 0),
+                    (131071, 4194304, 0)]
+PLAN_PATHS = {"one_launch": 3, "ranged": 4, "bucketed": 2, "radix": 1, "automatic": 0}
+
+
+def _plan_sweep(dev, reps=15):
+    """Median HIP-event span (µs) of the metadata + plan call for every plan path forced in turn
+    (a forced path whose limits do not hold falls back to the automatic choice, and is reported
+    as null), plus the slot-map plan of a top-k routing.  The launches are queued behind a sleep
+    kernel so that the events bracket the kernels."""
+    import statistics
+
+    import torch
+
+    from fastmoe_amd import _abi, ops
+
+    lib = _abi.lib()
+
+    def span(fn):
+        ts = []
+        for r in range(reps + 3):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(2_000_000)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            if r >= 3:
+                ts.append(a.elapsed_time(b) * 1e3)
+        return round(statistics.median(ts), 1)
+
+    rows = []
+    for T, N, hot in PLAN_SWEEP_CASES:
+        gen = torch.Generator().manual_seed(T + N)
+        idx = torch.randint(0, T, (N,), generator=gen)
+        if hot:
+            idx[torch.randperm(N, generator=gen)[:hot]] = 7
+        E = 256
+        cuts = torch.sort(torch.randint(0, N + 1, (E - 1,), generator=gen)).values.tolist()
+        sizes = [b - a for a, b in zip([0] + cuts, cuts + [N])]
+        xd = [torch.empty(n, 8, device=dev) for n in sizes]
+        idd, wd = idx.to(dev), torch.rand(N, generator=gen).to(dev)
+        row = {"tokens": T, "rows": N, "hot_token_rows": hot, "us": {}}
+        for name, code in PLAN_PATHS.items():
+            with _abi.options(plan=code):
+                if code and lib.fmoe_plan_path(N, T, E) != code:  # limits do not hold
+                    row["us"][name] = None
+                    continue
+                row["us"][name] = span(lambda: ops.prepare_metadata_and_plan(xd, idd, wd, T))
+        with _abi.options(plan=0):
+            row["automatic_path"] = {v: k for k, v in PLAN_PATHS.items()}[lib.fmoe_plan_path(N, T, E)]
+        k = N // T
+        if not hot and k * T == N and k <= 64:
+            # a top-k routing of the same size: token t's rows are the slots t*k .. t*k+k-1,
+            # placed at random packed rows
+            slot_pos = torch.randperm(N, generator=gen).to(torch.int32).to(dev)
+            row["us"]["slot_map"] = span(
+                lambda: ops.prepare_metadata_and_plan_from_slots(xd, slot_pos, wd, T, k))
+        rows.append(row)
+    return {"what": "metadata + plan span per plan path (median of %d, HIP events, µs)" % reps,
+            "experts": 256, "cases": rows}
+
+
+def _plan_floor(wl, dev, reps=50, rounds=3):
+    """Graph-replayed forward of ``wl`` (µs per replay, min over rounds): the forward alone with
+    its plan prebuilt, an empty kernel then the forward, each metadata + plan builder then the
+    forward, and the plan launches alone.  The experts come from the dispatch permutation of the
+    workload's top-k routing, so the slot-map plan applies; the forward's output is checked
+    equal from both plans first."""
+    import torch
+
+    import fastmoe_amd
+    from fastmoe_amd import _abi, ops
+    from fastmoe_amd.workloads import make_topk
+
+    T, D, E, k = wl.T, wl.D, wl.E, wl.k
+    ids, gates = make_topk(wl)
+    x = torch.randn(T, D, device=dev).to(wl.dtype)
+    with torch.no_grad():
+        p = fastmoe_amd.permute_tokens(x, ids.to(dev), gates.to(dev), E)
+    counts = p.expert_counts.tolist()
+    xs = [t.contiguous() for t in p.permuted_data.split(counts)]
+    idd, wd, sp = p.reverse_map_indices, p.sorted_weights.float(), p.slot_pos
+    meta, plan = ops.prepare_metadata_and_plan(xs, idd, wd, T)
+    meta2, plan2 = ops.prepare_metadata_and_plan_from_slots(xs, sp, wd, T, k)
+    out = torch.empty(T, D, dtype=wl.dtype, device=dev)
+    out2 = torch.empty_like(out)
+    ops._launch_fwd(meta, _abi.MODE_DET, plan, None, None, out, accumulate=False)
+    ops._launch_fwd(meta2, _abi.MODE_DET, plan2, None, None, out2, accumulate=False)
+    torch.cuda.synchronize()
+    same = torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    tiny = torch.zeros(1, device=dev)
+
+    def fwd():
+        ops._launch_fwd(meta, _abi.MODE_DET, plan, None, None, out, accumulate=False)
+
+    def idx_plan():
+        return ops.prepare_metadata_and_plan(xs, idd, wd, T)
+
+    def slot_plan():
+        return ops.prepare_metadata_and_plan_from_slots(xs, sp, wd, T, k)
+
+    def then_fwd(build):
+        def step():
+            m, pl = build()
+            ops._launch_fwd(m, _abi.MODE_DET, pl, None, None, out, accumulate=False)
+        return step
+
+    steps = {
+        "forward alone (plan prebuilt)": fwd,
+        "empty kernel, then the forward": lambda: (tiny.add_(1.0), fwd()),
+        "slot-map metadata + plan, then the forward": then_fwd(slot_plan),
+        "scatter-index metadata + plan, then the forward": then_fwd(idx_plan),
+        "slot-map metadata + plan alone": slot_plan,
+        "scatter-index metadata + plan alone": idx_plan,
+        "empty kernel alone": lambda: tiny.add_(1.0),
+    }
+    graphs = {}
+    for name, fn in steps.items():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        graphs[name] = g
+    res = {name: [] for name in graphs}
+    for _ in range(rounds):  # the graphs alternate within each round
+        for name, g in graphs.items():
+            for _ in range(5):
+                g.replay()
+            torch.cuda._sleep(5_000_000)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            res[name].append(a.elapsed_time(b) * 1e3 / reps)
+    from fastmoe_amd.workloads import algorithmic_bytes
+
+    fwd_b, _ = algorithmic_bytes(T, D, wl.N, x.element_size(), x.element_size())
+    return {"workload": wl.name, "outputs_equal_from_both_plans": same,
+            "bar_us_at_70pct": round(fwd_b / (0.7 * HBM_PEAK_GBS * 1e3), 1),
+            "us_per_replay_min": {n: round(min(v), 1) for n, v in res.items()},
+            "us_per_replay_all": {n: [round(x, 1) for x in v] for n, v in res.items()}}
+
+
 def _cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -613,6 +772,12 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE configurations (the 'configs' object)")
     ap.add_argument("--config-steps", type=int, default=10)
+    ap.add_argument("--plan-sweep", action="store_true",
+                    help="instead of a step: time every builder of the plan (the token-major "
+                         "inverse of the scatter index) on a set of shapes, HIP events")
+    ap.add_argument("--plan-floor", action="store_true",
+                    help="instead of a step: graph-replayed forward of --workload alone, behind "
+                         "an empty kernel, behind each plan builder, and each of those alone")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -633,6 +798,12 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.plan_sweep:
+        print(json.dumps(_plan_sweep(dev)), flush=True)
+        return 0
+    if args.plan_floor:
+        print(json.dumps(_plan_floor(WORKLOADS[args.workload], dev)), flush=True)
+        return 0
     wl = WORKLOADS[args.workload]
     backward = wl.backward and not args.fwd_only and not args.inplace
     gen_dev = torch.Generator(device=dev)

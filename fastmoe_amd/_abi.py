@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp],
     ),
+    "fmoe_plan_path": (_c_int, [_c_i64, _c_i64, _c_i64]),
     "fmoe_plan_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "fmoe_plan_status_offset": (_c_i64, []),
     "fmoe_plan_row_ptr_offset": (_c_i64, [_c_i64, _c_i64]),

@@ -779,6 +779,20 @@ PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bi
 
 }  // namespace
 
+extern "C" int fmoe_plan_path(int64_t num_rows, int64_t num_tokens, int64_t num_experts) {
+  if (num_rows < 0 || num_tokens < 1 || num_tokens >= (int64_t(1) << 30) ||
+      num_rows >= (int64_t(1) << 31) || num_experts < 1)
+    return -1;
+  int64_t groups = 0, bins = 0;
+  switch (pick_plan(num_rows, num_tokens, num_experts, &groups, &bins)) {
+    case kPathRadix: return 1;
+    case kPathBucketed: return 2;
+    case kPathTok: return 3;
+    case kPathRanged: return 4;
+  }
+  return -1;
+}
+
 extern "C" int64_t fmoe_plan_workspace_bytes(int64_t num_rows, int64_t num_tokens) {
   if (num_rows < 0 || num_tokens < 1) return -1;
   return fmoe::plan_layout(num_rows, num_tokens).total;

@@ -169,6 +169,15 @@ FMOE_API int fmoe_build_plan(const void* d_indices, int idx_dtype, const void* d
                     void* d_workspace, void* stream);
 
 /*
+ * The plan builder fmoe_build_plan / fmoe_build_metadata_and_plan take for N rows, T tokens and E
+ * experts under the current "plan" option: 1 radix, 2 bucketed, 3 one launch, 4 ranged (the
+ * option's own numbering), or -1 for sizes no builder takes.  No counterpart in the reference
+ * (its Triton kernel has no plan); for callers and benchmarks that force a path and need to know
+ * whether its limits hold.  Host only: no GPU call.
+ */
+FMOE_API int fmoe_plan_path(int64_t num_rows, int64_t num_tokens, int64_t num_experts);
+
+/*
  * fmoe_build_metadata followed by fmoe_build_plan on the same experts, in one call (no counterpart
  * in the reference, which builds metadata per call in prepare_grouped_metadata, ops.py:200-271,
  * and needs no inverse).  Outputs and workspace exactly as those two calls; num_rows is the sum
