@@ -515,6 +515,9 @@ def test_plan_matches_oracle(case, path, kernel_options):
     plan = fastmoe_amd.build_plan(meta, idd, wd, T)
     lib = fastmoe_amd._abi.lib()
     N = idx.numel()
+    # the forced builder's limits hold here, so it is the one that ran (the status word's
+    # longest-segment field below tells the builders apart)
+    assert lib.fmoe_plan_path(N, T, len(experts)) == _PLAN_PATHS[path]
     rp_off = lib.fmoe_plan_row_ptr_offset(N, T)
     rec_off = lib.fmoe_plan_records_offset(N, T)
     row_ptr = plan[rp_off: rp_off + 4 * (T + 2)].view(torch.int32).cpu().numpy()
