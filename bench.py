@@ -45,7 +45,8 @@ def _atomic_rate(wl, mode, us, passes_us=None):
     (mode atomic, or any fp32 target) make N*D*4/64 line requests, packed 16-bit pairs N*D*2/64.
     ``passes_us``: the same call's span with every index out of range, i.e. what it spends besides
     the adds (mode atomic with a 16-bit output: the fp32 accumulator's init and store passes over
-    T*D, plus a grid of waves that exit at once); the rate is then taken over the rest."""
+    T*D; otherwise the zero-fill of the overwritten output; plus a grid of waves that exit at
+    once); the rate is then taken over the rest."""
     import torch
 
     out_bytes = 4 if (mode == "atomic" or wl.dtype == torch.float32) else 2
@@ -56,21 +57,23 @@ def _atomic_rate(wl, mode, us, passes_us=None):
            "atomic_ceiling_frac": round(rate / ATOMIC_CEILING_LINES_PER_S, 3),
            "note": "G 64-byte line requests/s; ceiling 20.7 G/s measured with a synthetic kernel"}
     if passes_us:
-        res.update(call_us=round(us, 2), accumulator_passes_us=round(passes_us, 2),
+        acc = mode == "atomic" and wl.dtype != torch.float32
+        res.update(call_us=round(us, 2), passes_us=round(passes_us, 2),
                    call_requests_per_s=round(lines / (us * 1e-6) / 1e9, 2),
-                   passes="fp32 accumulator init + store, timed as the call with every index out "
-                          "of range; the rate above is over the call less this")
+                   passes=("fp32 accumulator init + store" if acc else "zero-fill of the output")
+                   + ", timed as the call with every index out of range; the rate above is over "
+                     "the call less this")
     return res
 
 
-def _accumulator_passes_us(wl, xs, mode, steps, dev):
-    """HIP-event span of the atomic forward call with every scatter index out of range (see
-    _atomic_rate), or None when the call has no accumulator (fp32 output, or atomic_packed)."""
+def _non_add_passes_us(wl, xs, mode, steps, dev):
+    """HIP-event span of the atomic forward call (the autograd path's, which overwrites its
+    output) with every scatter index out of range (see _atomic_rate)."""
     import torch
 
     import fastmoe_amd
 
-    if mode != "atomic" or wl.dtype == torch.float32:
+    if mode not in ("atomic", "atomic_packed"):
         return None
     bad = torch.full((wl.N,), wl.T, dtype=torch.int64, device=dev)
     w = torch.ones(wl.N, device=dev)
@@ -558,7 +561,7 @@ def _config_line(name, mode, steps, warmup, dev):
         res["repeatability"] = repeat
     if mode != "det" and "fwd_atomic" in kernels:
         res["atomic"] = _atomic_rate(wl, mode, kernels["fwd_atomic"]["avg_us"],
-                                     _accumulator_passes_us(wl, xs, mode, steps, dev))
+                                     _non_add_passes_us(wl, xs, mode, steps, dev))
     del idx, w, xs, grad_out, step, direct_step
     torch.cuda.empty_cache()
     return res
@@ -997,7 +1000,7 @@ def main() -> int:
     if args.path == "combine" and args.mode != "det" and "fwd_atomic" in kernels:
         res["atomic"] = _atomic_rate(wl, args.mode, kernels["fwd_atomic"]["avg_us"],
                                      None if args.inplace else
-                                     _accumulator_passes_us(wl, xs, args.mode, args.steps, dev))
+                                     _non_add_passes_us(wl, xs, args.mode, args.steps, dev))
     if not args.no_standard:
         res["verify"] = verify()
         std_step, what = std()
