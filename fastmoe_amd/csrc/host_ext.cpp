@@ -112,9 +112,11 @@ PyObject* experts(PyObject*, PyObject* args) {
     Py_DECREF(table);
     return nullptr;
   }
-  PyObject* res = Py_BuildValue("(LLLNL)", (long long)hidden, (long long)total,
+  // "O" takes a new reference to table on success and none on failure, so ours is dropped
+  // either way.
+  PyObject* res = Py_BuildValue("(LLLOL)", (long long)hidden, (long long)total,
                                 (long long)max_rows, table, version_sum);
-  if (!res) Py_DECREF(table);
+  Py_DECREF(table);
   return res;
 }
 
