@@ -313,6 +313,32 @@ __device__ __forceinline__ void small_table_to_lds(const HostTable& t, int* off_
   if (e == 0) off_lds[t.count] = t.off[t.count];
 }
 
+// For the first kn of K keys (kn wave-uniform), the largest a in [0, n) with arr[a] <= key[k]
+// (arr non-decreasing over [0, n), n >= 1, arr[0] <= every key; out[k] = 0 for k >= kn): binary
+// lifting, whose trip count depends on n alone, so the searches run side by side and their
+// dependent LDS reads overlap (a loop per key would wait for each read in turn).  Only
+// arr[0 .. n) is read.
+template <int K>
+__device__ __forceinline__ void last_le(const int* __restrict__ arr, int n, const int (&key)[K],
+                                        int (&out)[K], int kn = K) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) out[k] = 0;
+  if (n <= 1) return;
+  for (int step = 1 << (31 - __builtin_clz((unsigned)(n - 1))); step > 0; step >>= 1) {
+    int val[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)  // all the reads first
+      if (k < kn) val[k] = arr[min(out[k] + step, n - 1)];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (k < kn) {
+        const int c = out[k] + step;
+        out[k] = c < n && val[k] <= key[k] ? c : out[k];
+      }
+    }
+  }
+}
+
 // Largest e in [0, E) with off[e] <= g (int32 offsets, off[0] == 0 <= g < off[E]).
 __device__ __forceinline__ int expert_of_row32(const int* __restrict__ off, int E, int g) {
   int lo = 0, hi = E;  // invariant: off[lo] <= g < off[hi]
@@ -338,6 +364,23 @@ __device__ __forceinline__ uint64_t match_key(bool active, int key, int bits) {
     m &= bit ? b : ~b;
   }
   return m;
+}
+
+// cnt[j] += 1 in LDS for every active lane (called by the whole wave).  The lanes whose bin is
+// the first active lane's add their number with one atomic: LDS atomics to one address execute
+// one lane at a time, so a token holding most rows of a wave (a hot token) would otherwise cost
+// 64 serialised atomics per row batch.
+__device__ __forceinline__ void count_bins(int* cnt, bool active, uint32_t j) {
+  const uint64_t am = __ballot(active);
+  if (am == 0) return;  // wave-uniform
+  const uint32_t j0 = (uint32_t)__builtin_amdgcn_readlane((int)j, __builtin_ctzll(am));
+  const bool same = active && j == j0;
+  const uint64_t sm = __ballot(same);
+  if (same) {
+    if (lanes_below(sm) == 0) atomicAdd(&cnt[j0], __popcll(sm));
+  } else if (active) {
+    atomicAdd(&cnt[j], 1);
+  }
 }
 
 }  // namespace fmoe

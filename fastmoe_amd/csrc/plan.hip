@@ -53,7 +53,7 @@ constexpr int kTokRows = 256;                          // rows per workgroup aim
 constexpr int kTokGroups = 256;
 constexpr int kTokExperts = 4096;                      // expert tables staged in LDS
 constexpr int64_t kTokMaxRows = int64_t(1) << 17;
-constexpr int kTokLoads = 8;                           // 16-byte index loads per lane per batch
+constexpr int kTokLoads = 8;  // 16-byte int64 index loads per lane per batch (half for int32)
 static_assert(kTokBins == kRangeMaxBins, "a range of the ranged plan is a token-sliced workgroup");
 static_assert(kRangeMaxSlices <= kScanThreads * kRangeSlicesPerThread,
               "k_plan_range reads kRangeSlicesPerThread slices per thread");
@@ -145,12 +145,16 @@ struct TokLds {
 
 // The end of a token-sliced plan workgroup, after each wave has stashed its rows of the range
 // [lo, lo + nloc) in ascending g (wcount of them; past kTokWaveStash the stash holds only the
-// first): count them per bin, scan the bins into row_ptr (rows_part: this thread's share of the
-// rows before the range, summed over the workgroup) and the per-wave cursors, and write each row's
-// record at its wave's cursor for the bin plus its rank among the lower lanes of the same bin.
-// rows(fn) replays this wave's rows in ascending g, calling fn(act, g, j) once per 64 rows with
-// every lane: used when the stash overflowed.
-template <typename TW, typename Meta, typename Rows>
+// first): count them per bin (with kPassCounts the caller's pass has counted the rows past the
+// stash into L.cnt, and only the stash's are counted here), scan the bins into row_ptr (rows_part:
+// this thread's share of the rows before the range, summed over the workgroup) and the per-wave
+// cursors, and write each row's record at its wave's cursor for the bin plus its rank among the
+// lower lanes of the same bin.
+// rows(fn, gates) replays this wave's rows in ascending g, calling fn(act, g, j, gate, e) once per
+// 64 rows with every lane, several batches of loads in flight; with `gates` std::true_type it
+// also loads each row's gate and finds its expert e (else both are 0): used when the stash
+// overflowed.
+template <bool kPassCounts, typename TW, typename Meta, typename Rows>
 __device__ __forceinline__ void tok_finish(TokLds& L, const TokMetaRegs<Meta>& mreg,
                                            const Meta& meta, int ne, int64_t row_bytes,
                                            const TW* __restrict__ w, int lo, int nloc, int nb,
@@ -162,25 +166,25 @@ __device__ __forceinline__ void tok_finish(TokLds& L, const TokMetaRegs<Meta>& m
   int* mycnt = L.cnt + wave * nloc;
   const int2* mystash = L.stash + wave * (kTokWaveStash + 1);
   mreg.store(meta, ne, L.off32, L.ptr_lds);
-  // This wave's rows per bin, counted from the stash (or, when it overflowed, from its rows
-  // again), and the gates of the stashed rows, loaded before the scan so that their latency
-  // overlaps it.
+  // This wave's rows per bin, counted from the stash (when it overflowed: the stash's rows here and
+  // the rest by the caller's pass, or all of them from its rows again), and the gates of the
+  // stashed rows, loaded before the scan so that their latency overlaps it.
   constexpr int kStashChunks = kTokWaveStash / kWave;
   int2 se[kStashChunks];
   float sw[kStashChunks];
-  if (wcount <= kTokWaveStash) {  // wave-uniform
+  const bool stashed = wcount <= kTokWaveStash;  // wave-uniform
+  if (stashed || kPassCounts) {
 #pragma unroll
     for (int q = 0; q < kStashChunks; ++q) {
       const int at = q * kWave + lane;
-      const bool act = at < wcount;
+      const bool act = at < wcount && at < kTokWaveStash;
       se[q] = act ? mystash[at] : make_int2(0, 0);
-      sw[q] = act ? ld1(w + se[q].x) : 0.f;
+      sw[q] = act && stashed ? ld1(w + se[q].x) : 0.f;
       if (act) atomicAdd(&mycnt[se[q].y], 1);
     }
   } else {
-    rows([&](bool act, int, uint32_t j) {
-      if (act) atomicAdd(&mycnt[j], 1);
-    });
+    rows([&](bool act, int, uint32_t j, float, int) { count_bins(mycnt, act, j); },
+         std::false_type{});
   }
   __syncthreads();  // the expert table and every wave's counts
 
@@ -223,13 +227,14 @@ __device__ __forceinline__ void tok_finish(TokLds& L, const TokMetaRegs<Meta>& m
 
   // fill: each wave its rows in ascending g -- from the stash, or replayed if it overflowed
   const int jbits = nloc > 1 ? 32 - __builtin_clz((unsigned)(nloc - 1)) : 0;
-  auto place = [&](bool act, int g, int j, float wg) {
+  // e: the row's expert, or -1 to look it up here
+  auto place = [&](bool act, int g, int j, float wg, int e) {
     const uint64_t m = match_key(act, j, jbits);
     if (act) {
       const int rank = lanes_below(m);
       const int pos = mycnt[j] + rank;
       if (rank == 0) mycnt[j] = pos + __popcll(m);
-      const int e = expert_of_row32(L.off32, ne, g);
+      if (e < 0) e = expert_of_row32(L.off32, ne, g);
       Rec r;
       r.src = L.ptr_lds[e] + (uint64_t)((int64_t)(g - L.off32[e]) * row_bytes);
       r.w = wg;
@@ -237,12 +242,13 @@ __device__ __forceinline__ void tok_finish(TokLds& L, const TokMetaRegs<Meta>& m
       rec[pos] = r;
     }
   };
-  if (wcount <= kTokWaveStash) {  // wave-uniform
+  if (stashed) {
 #pragma unroll
     for (int q = 0; q < kStashChunks; ++q)
-      if (q * kWave < wcount) place(q * kWave + lane < wcount, se[q].x, se[q].y, sw[q]);
+      if (q * kWave < wcount) place(q * kWave + lane < wcount, se[q].x, se[q].y, sw[q], -1);
   } else {
-    rows([&](bool act, int g, uint32_t j) { place(act, g, (int)j, act ? ld1(w + g) : 0.f); });
+    rows([&](bool act, int g, uint32_t j, float wg, int e) { place(act, g, (int)j, wg, e); },
+         std::true_type{});
   }
 }
 
@@ -269,6 +275,9 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   //    then the next lane's, so the wave still sees its rows in ascending g).  The rows past the
   //    last whole vector (fewer than RPL) are read one per lane after the pass.
   constexpr int RPL = 16 / (int)sizeof(TI);
+  // 16-byte loads per lane per batch: the same rows per batch for either index width (an int32
+  // batch with as many loads as an int64 one needs more registers than the kernel may use)
+  constexpr int kLoads = kTokLoads * 2 / RPL;
   const int n32 = (int)N;
   const int n_al = n32 - n32 % RPL;  // rows in whole 16-byte vectors
   const int per = ((n32 + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;  // 64 | per
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   const rsrc_t rv = make_rsrc(idx, (uint32_t)((int64_t)n_al * (int64_t)sizeof(TI)));  // vectors
   auto load_batch = [&](int base, u32x4* v) {  // past n_al: zeros from the range check, no traffic
 #pragma unroll
-    for (int i = 0; i < kTokLoads; ++i) {
+    for (int i = 0; i < kLoads; ++i) {
       const int g0 = base + (i * kWave + lane) * RPL;
       v[i] = Raw<16>::template ld<kCPolCached>(rv, (uint32_t)g0 * (uint32_t)sizeof(TI));
     }
@@ -287,7 +296,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
   // Two batch buffers used in turn (no register copies, which would make each iteration wait for
   // the next batch's loads), so one batch is always in flight while the other is counted.  The
   // first batch is issued before the LDS set-up and its barrier.
-  u32x4 va[kTokLoads], vb[kTokLoads];
+  u32x4 va[kLoads], vb[kLoads];
   if (r0 < lim) load_batch(r0, va);  // wave-uniform
 
   TokMetaRegs<Meta> mreg;
@@ -347,14 +356,14 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
     else
       return (TI)v[r];
   };
-  constexpr int kBatchRows = kTokLoads * kWave * RPL;
+  constexpr int kBatchRows = kLoads * kWave * RPL;
   // A whole batch below lim whose rows are all below 2^32 as unsigned 64-bit values (int64: every
   // high word zero; int32 always) takes the low word as the bin as it is: a value of T or more,
   // or a negative int32, is then neither in a range that ends at or below T nor below it, so only
   // the workgroup of bin T clamps it to T.  Anything else takes the exact per-row path.
   auto count_fast = [&](int base, const u32x4* v, auto owns_invalid) {
 #pragma unroll
-    for (int i = 0; i < kTokLoads; ++i) {
+    for (int i = 0; i < kLoads; ++i) {
       const int g0 = base + (i * kWave + lane) * RPL;
       uint32_t b[RPL];
 #pragma unroll
@@ -371,7 +380,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       if (!exact) {
         uint32_t high = 0;
 #pragma unroll
-        for (int i = 0; i < kTokLoads; ++i) high |= v[i][1] | v[i][3];
+        for (int i = 0; i < kLoads; ++i) high |= v[i][1] | v[i][3];
         exact = __ballot(high != 0) != 0;
       }
     }
@@ -380,7 +389,7 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       else count_fast(base, v, std::false_type{});
     } else {
 #pragma unroll
-      for (int i = 0; i < kTokLoads; ++i) {
+      for (int i = 0; i < kLoads; ++i) {
         const int g0 = base + (i * kWave + lane) * RPL;
         uint32_t b[RPL];
 #pragma unroll
@@ -414,18 +423,42 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_tok(
       wcount += __popcll(m);
     }
   }
-  // this wave's rows again, for a stash that overflowed
-  auto rows = [&](auto fn) {
-    for (int base = r0; base < r1; base += kWave) {
-      const int g = base + lane;
-      const uint32_t j = bin_at(g, r1, __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
-                                                                  ri, (uint32_t)g * (uint32_t)sizeof(TI)))) -
-                         (uint32_t)lo;
-      fn(j < (uint32_t)nloc, g, j);
+  // this wave's rows again, for a stash that overflowed: kReplay batches of 64 rows in flight
+  // (the index loads past r1 read rows of other waves or, past N, zeros from the range check, and
+  // bin_at discards them); a row's gate is loaded only when it is in the range
+  constexpr int kReplay = 8;
+  auto rows = [&](auto fn, auto gates) {
+    constexpr bool kGates = decltype(gates)::value;
+    for (int base = r0; base < r1; base += kReplay * kWave) {
+      TI raw[kReplay];
+#pragma unroll
+      for (int k = 0; k < kReplay; ++k)
+        raw[k] = __builtin_bit_cast(TI, Raw<sizeof(TI)>::template ld<kCPolCached>(
+                                            ri, (uint32_t)(base + k * kWave + lane) * (uint32_t)sizeof(TI)));
+      uint32_t j[kReplay];
+      float wg[kReplay];
+      int gk[kReplay], ek[kReplay];
+#pragma unroll
+      for (int k = 0; k < kReplay; ++k) {
+        const int g = base + k * kWave + lane;
+        j[k] = bin_at(g, r1, raw[k]) - (uint32_t)lo;
+        wg[k] = kGates && j[k] < (uint32_t)nloc ? ld1(w + g) : 0.f;
+        gk[k] = j[k] < (uint32_t)nloc ? g : 0;
+      }
+      if constexpr (kGates) {
+        last_le(L.off32, ne, gk, ek, min(kReplay, (r1 - base + kWave - 1) / kWave));
+      } else {
+#pragma unroll
+        for (int k = 0; k < kReplay; ++k) ek[k] = 0;
+      }
+#pragma unroll
+      for (int k = 0; k < kReplay; ++k)
+        if (base + k * kWave < r1)  // wave-uniform
+          fn(j[k] < (uint32_t)nloc, base + k * kWave + lane, j[k], wg[k], ek[k]);
     }
   };
-  tok_finish(L, mreg, meta, ne, row_bytes, w, lo, nloc, nb, wcount, lane == 0 ? below : 0,
-             row_ptr, rec, status, rows);
+  tok_finish<false>(L, mreg, meta, ne, row_bytes, w, lo, nloc, nb, wcount,
+                    lane == 0 ? below : 0, row_ptr, rec, status, rows);
 }
 
 // ---- ranged plan: two launches, each CU reading only its share of idx -----------------------
@@ -540,50 +573,68 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_range(
   const int per = ((nrows + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;
   const int p0 = min(nrows, wave * per);
   const int p1 = min(nrows, p0 + per);
-  auto fetch = [&](int i) -> int2 {
-    int a = 0, b = G1;
-    while (b - a > 1) {
-      const int mid = (a + b) >> 1;
-      if (first[mid] <= i) a = mid; else b = mid;
-    }
-    return part[at[a] + (i - first[a])];
-  };
-  int2* mystash = L.stash + wave * (kTokWaveStash + 1);
-  int wcount = 0;  // wave-uniform
   constexpr int kGather = 4;  // chunks of 64 rows in flight
-  for (int base = p0; base < p1; base += kGather * kWave) {
-    int2 v[kGather];
+  // rows base + k * 64 + lane of the range, k < kGather (`none` past p1)
+  auto fetch = [&](int base, int2 (&v)[kGather], int2 none) {
 #pragma unroll
     for (int k = 0; k < kGather; ++k) {
       const int i = base + k * kWave + lane;
-      v[k] = i < p1 ? fetch(i) : make_int2(0, -1);
+      v[k] = none;
+      if (i < p1) {
+        int a = 0, b = G1;
+        while (b - a > 1) {
+          const int mid = (a + b) >> 1;
+          if (first[mid] <= i) a = mid; else b = mid;
+        }
+        v[k] = part[at[a] + (i - first[a])];
+      }
     }
+  };
+  int2* mystash = L.stash + wave * (kTokWaveStash + 1);
+  int* mycnt = L.cnt + wave * nloc;  // zeroed before the scan's barriers above
+  int wcount = 0;  // wave-uniform
+  for (int base = p0; base < p1; base += kGather * kWave) {
+    int2 v[kGather];
+    fetch(base, v, make_int2(0, -1));
 #pragma unroll
     for (int k = 0; k < kGather; ++k) {
       const bool in = v[k].y >= 0;
       const uint64_t m = __ballot(in);
-      if (in) {
-        const uint32_t slot = (uint32_t)wcount + (uint32_t)lanes_below(m);
-        mystash[min(slot, (uint32_t)kTokWaveStash)] = make_int2(v[k].x, v[k].y - lo);
-      }
+      const uint32_t slot = (uint32_t)wcount + (uint32_t)lanes_below(m);
+      if (in) mystash[min(slot, (uint32_t)kTokWaveStash)] = make_int2(v[k].x, v[k].y - lo);
+      // the rows past the stash are counted here, so that tok_finish<true> need not replay them
+      if (wcount + __popcll(m) > kTokWaveStash)  // wave-uniform
+        count_bins(mycnt, in && slot >= (uint32_t)kTokWaveStash, (uint32_t)(v[k].y - lo));
       wcount += __popcll(m);
     }
   }
-  auto rows = [&](auto fn) {  // kGather chunks in flight, as in the gather
+  // kGather chunks in flight, as in the gather; the gates and experts of a batch side by side
+  auto rows = [&](auto fn, auto gates) {
+    constexpr bool kGates = decltype(gates)::value;
     for (int base = p0; base < p1; base += kGather * kWave) {
       int2 v[kGather];
+      fetch(base, v, make_int2(0, lo));
+      float wg[kGather];
+      int gk[kGather], ek[kGather];
 #pragma unroll
       for (int k = 0; k < kGather; ++k) {
-        const int i = base + k * kWave + lane;
-        v[k] = i < p1 ? fetch(i) : make_int2(0, lo);
+        wg[k] = kGates && base + k * kWave + lane < p1 ? ld1(w + v[k].x) : 0.f;
+        gk[k] = v[k].x;  // 0 past p1
+      }
+      if constexpr (kGates) {
+        last_le(L.off32, ne, gk, ek, min(kGather, (p1 - base + kWave - 1) / kWave));
+      } else {
+#pragma unroll
+        for (int k = 0; k < kGather; ++k) ek[k] = 0;
       }
 #pragma unroll
       for (int k = 0; k < kGather; ++k)
-        if (base + k * kWave < p1) fn(base + k * kWave + lane < p1, v[k].x, (uint32_t)(v[k].y - lo));
+        if (base + k * kWave < p1)  // wave-uniform
+          fn(base + k * kWave + lane < p1, v[k].x, (uint32_t)(v[k].y - lo), wg[k], ek[k]);
     }
   };
-  tok_finish(L, mreg, meta, ne, row_bytes, w, lo, nloc, nb, wcount, threadIdx.x == 0 ? before : 0,
-             row_ptr, rec, status, rows);
+  tok_finish<true>(L, mreg, meta, ne, row_bytes, w, lo, nloc, nb, wcount,
+                   threadIdx.x == 0 ? before : 0, row_ptr, rec, status, rows);
 }
 
 // ---- plan of a combine fed by the dispatch permutation -------------------------------------

@@ -635,6 +635,54 @@ def test_plan_ranged_matches_oracle(T, N, hot, idx_dtype, kernel_options):
     np.testing.assert_array_equal(bits(out), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+@pytest.mark.parametrize("path,T,N,hot", [("tok", 500, 20_003, 12_000), ("tok", 1, 9_000, 0),
+                                          ("ranged", 3000, 90_001, 50_000),
+                                          ("ranged", 70_000, 140_000, 30_000)])
+def test_plan_hot_token_matches_oracle(path, T, N, hot, idx_dtype, kernel_options):
+    """A hot token (`hot` rows on token 7, or every row on the single token) makes its range's
+    waves overflow their stashes: the one-launch plan then replays each wave's rows for the
+    counts and the fill, the ranged plan counts the rows past the stash during its pass and
+    replays them for the fill, with the rows' gates and experts looked up a batch at a time.
+    256 experts, a fifth of them empty, so the expert search crosses runs of equal offsets.
+    Row pointers, record order and gate bits equal the oracle's stable inverse and the forward
+    reading the records (their source addresses) is bit-exact."""
+    from oracle import cref
+
+    kernel_options(plan=_PLAN_PATHS[path])
+    gen = torch.Generator().manual_seed(T + N + hot)
+    D = 4
+    idx = torch.randint(0, T, (N,), generator=gen)
+    if hot:
+        idx[torch.randperm(N, generator=gen)[:hot]] = 7
+    bad = torch.rand(N, generator=gen) < 0.01
+    idx = torch.where(bad, torch.full_like(idx, T + 3), idx).to(idx_dtype)
+    w = torch.rand(N, generator=gen)
+    cuts = torch.sort(torch.randint(0, N + 1, (255,), generator=gen)).values
+    sizes = [b - a for a, b in zip([0] + cuts.tolist(), cuts.tolist() + [N])]
+    empty = torch.randperm(256, generator=gen)[:51].tolist()
+    for e in empty:  # hand an expert's rows to its neighbour, leaving it empty
+        n = (e + 1) % 256
+        sizes[n] += sizes[e]
+        sizes[e] = 0
+    experts = [torch.randn(n, D, generator=gen) for n in sizes]
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta, plan = ops.prepare_metadata_and_plan(xd, idd, wd, T)
+    lib = fastmoe_amd._abi.lib()
+    assert lib.fmoe_plan_path(N, T, 256) == _PLAN_PATHS[path]
+    rp = plan[lib.fmoe_plan_row_ptr_offset(N, T):][: 4 * (T + 2)].view(torch.int32).cpu().numpy()
+    rec = plan[lib.fmoe_plan_records_offset(N, T):][: 16 * N].view(torch.int64).view(N, 2).cpu()
+    want_rp, want_g = cref.plan(idx.to(torch.int64).numpy(), T)
+    np.testing.assert_array_equal(rp, want_rp)
+    np.testing.assert_array_equal((rec[:, 1] >> 32).numpy().astype(np.int32), want_g)
+    wbits = (rec[:, 1] & 0xFFFFFFFF).numpy().astype(np.uint32)
+    np.testing.assert_array_equal(wbits, w.numpy()[want_g].view(np.uint32))
+    assert int(ops.plan_status(plan).cpu()[0]) == int(bad.sum())
+    out = fastmoe_amd.grouped_weighted_scatter_add(xd, idd, wd, (T, D))
+    want, _, _ = oracle_fwd(experts, idx.to(torch.int64), w, T, torch.float32)
+    np.testing.assert_array_equal(bits(out), want.view(np.uint32))
+
+
 def test_bwd_f16_grad_x_rounds_twice_like_the_reference():
     """f16 experts, fp32 gates: grad_X is the fp32 product rounded to fp32 and then to f16
     (index_select * w, then autograd's cast; ops.py:344-353).  The inputs include elements where
