@@ -573,32 +573,69 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_range(
   const int per = ((nrows + kTokWaves - 1) / kTokWaves + kWave - 1) / kWave * kWave;
   const int p0 = min(nrows, wave * per);
   const int p1 = min(nrows, p0 + per);
-  constexpr int kGather = 4;  // chunks of 64 rows in flight
-  // rows base + k * 64 + lane of the range, k < kGather (`none` past p1)
-  auto fetch = [&](int base, int2 (&v)[kGather], int2 none) {
+  constexpr int kGather = 4;  // chunks of at most 64 rows in flight
+  // The wave's rows in order, kGather chunks per batch: chunk k holds n[k] rows (0: none), lane
+  // l < n[k] gets v[k] = (g, bin) of its row, the others `none`.  A sparse range (fewer than 64
+  // rows per slice on average) takes chunks of 64 consecutive rows and finds each lane's slice by
+  // binary search over first[].  A dense one (a hot token's range) walks the slices in order, a
+  // chunk ending at the end of its slice, with no search per row: its rows are contiguous in the
+  // slice's part of the partition.
+  const bool dense = nrows >= kWave * G1;  // workgroup-uniform
+  struct Walk {
+    int i;  // next row of the wave's share
+    int s;  // its slice (dense walk)
+  };
+  auto walk_start = [&]() -> Walk {
+    Walk wk{p0, 0};
+    if (dense && p0 < p1) {  // wave-uniform
+      int a = 0, b = G1;  // the last slice a with first[a] <= p0
+      while (b - a > 1) {
+        const int mid = (a + b) >> 1;
+        if (__builtin_amdgcn_readfirstlane(first[mid]) <= p0) a = mid; else b = mid;
+      }
+      wk.s = a;
+    }
+    return wk;
+  };
+  auto next_batch = [&](Walk& wk, int2 (&v)[kGather], int (&n)[kGather], int2 none) {
 #pragma unroll
     for (int k = 0; k < kGather; ++k) {
-      const int i = base + k * kWave + lane;
       v[k] = none;
-      if (i < p1) {
-        int a = 0, b = G1;
-        while (b - a > 1) {
-          const int mid = (a + b) >> 1;
-          if (first[mid] <= i) a = mid; else b = mid;
+      n[k] = 0;
+      if (wk.i < p1) {  // wave-uniform
+        if (dense) {
+          int end = __builtin_amdgcn_readfirstlane(first[wk.s + 1]);
+          while (end <= wk.i) end = __builtin_amdgcn_readfirstlane(first[++wk.s + 1]);
+          const int c = min(kWave, min(end, p1) - wk.i);
+          if (lane < c) v[k] = part[at[wk.s] + (wk.i - first[wk.s]) + lane];
+          n[k] = c;
+        } else {
+          const int i = wk.i + lane;
+          const int c = min(kWave, p1 - wk.i);
+          if (lane < c) {
+            int a = 0, b = G1;
+            while (b - a > 1) {
+              const int mid = (a + b) >> 1;
+              if (first[mid] <= i) a = mid; else b = mid;
+            }
+            v[k] = part[at[a] + (i - first[a])];
+          }
+          n[k] = c;
         }
-        v[k] = part[at[a] + (i - first[a])];
+        wk.i += n[k];
       }
     }
   };
   int2* mystash = L.stash + wave * (kTokWaveStash + 1);
   int* mycnt = L.cnt + wave * nloc;  // zeroed before the scan's barriers above
   int wcount = 0;  // wave-uniform
-  for (int base = p0; base < p1; base += kGather * kWave) {
+  for (Walk wk = walk_start(); wk.i < p1;) {
     int2 v[kGather];
-    fetch(base, v, make_int2(0, -1));
+    int n[kGather];
+    next_batch(wk, v, n, make_int2(0, -1));
 #pragma unroll
     for (int k = 0; k < kGather; ++k) {
-      const bool in = v[k].y >= 0;
+      const bool in = lane < n[k];
       const uint64_t m = __ballot(in);
       const uint32_t slot = (uint32_t)wcount + (uint32_t)lanes_below(m);
       if (in) mystash[min(slot, (uint32_t)kTokWaveStash)] = make_int2(v[k].x, v[k].y - lo);
@@ -608,29 +645,32 @@ __global__ __launch_bounds__(kScanThreads) void k_plan_range(
       wcount += __popcll(m);
     }
   }
-  // kGather chunks in flight, as in the gather; the gates and experts of a batch side by side
+  // the same walk again; the gates and experts of a batch side by side
   auto rows = [&](auto fn, auto gates) {
     constexpr bool kGates = decltype(gates)::value;
-    for (int base = p0; base < p1; base += kGather * kWave) {
+    for (Walk wk = walk_start(); wk.i < p1;) {
       int2 v[kGather];
-      fetch(base, v, make_int2(0, lo));
+      int n[kGather];
+      next_batch(wk, v, n, make_int2(0, lo));
       float wg[kGather];
       int gk[kGather], ek[kGather];
+      int kn = 0;  // chunks with rows: a prefix
 #pragma unroll
       for (int k = 0; k < kGather; ++k) {
-        wg[k] = kGates && base + k * kWave + lane < p1 ? ld1(w + v[k].x) : 0.f;
-        gk[k] = v[k].x;  // 0 past p1
+        wg[k] = kGates && lane < n[k] ? ld1(w + v[k].x) : 0.f;
+        gk[k] = v[k].x;  // 0 past the rows
+        kn += n[k] > 0 ? 1 : 0;
       }
       if constexpr (kGates) {
-        last_le(L.off32, ne, gk, ek, min(kGather, (p1 - base + kWave - 1) / kWave));
+        last_le(L.off32, ne, gk, ek, kn);
       } else {
 #pragma unroll
         for (int k = 0; k < kGather; ++k) ek[k] = 0;
       }
 #pragma unroll
       for (int k = 0; k < kGather; ++k)
-        if (base + k * kWave < p1)  // wave-uniform
-          fn(base + k * kWave + lane < p1, v[k].x, (uint32_t)(v[k].y - lo), wg[k], ek[k]);
+        if (n[k] > 0)  // wave-uniform
+          fn(lane < n[k], v[k].x, (uint32_t)(v[k].y - lo), wg[k], ek[k]);
     }
   };
   tok_finish<true>(L, mreg, meta, ne, row_bytes, w, lo, nloc, nb, wcount,
