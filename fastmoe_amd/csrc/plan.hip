@@ -9,19 +9,21 @@
 //   rec[N]          : 16-byte records {source row address, fp32 gate, g}, ascending g in every
 //                     segment
 //
-// Four builders, each linear in N + T and each writing every segment in ascending g:
+// Four builders, each linear in N + T and each writing every segment in ascending g (pick_plan
+// below chooses):
 //   * one launch (k_plan_tok), below 2^16 rows: token-sliced workgroups that each stream all of
 //     idx and fill their own segments stably (below);
-//   * the ranged plan (k_plan_split + k_plan_range), up to 2^21 rows and 2^19 tokens: partition
+//   * the ranged plan (k_plan_split + k_plan_range), up to 2^22 rows and 2^19 tokens: partition
 //     the rows by token range, then one token-sliced workgroup per range reads only its rows;
-//   * two launches (plan_bucket.hip), beyond that: partition the rows by token bucket, then order
-//     each bucket with one wave;
-//   * the radix plan (plan_radix.hip), beyond 2^22 tokens: count + scan (one 1024-thread
-//     workgroup histograms idx in LDS, or zero / global-atomic count / one-block scan for larger
-//     T) for row_ptr and the status words, then a stable LSD radix sort of the rows by token bin.
+//   * the radix plan (plan_radix.hip), for tokens averaging 64 rows or more and beyond the ranged
+//     plan's limits: a stable LSD radix sort of the rows by token bin, with row_ptr from the
+//     sorted bins, whatever the segment lengths;
+//   * the bucketed plan (plan_bucket.hip), only when asked for (option plan=2): partition the
+//     rows by token bucket, then order each bucket with one wave.  Fastest on uniform indices
+//     beyond the ranged plan's limits, but a hot token's bucket is ordered by one wave.
 //
-// fmoe_invert_scatter_index writes bare row numbers instead of records (the bucketed or the radix
-// plan).
+// fmoe_invert_scatter_index writes bare row numbers instead of records (the radix plan, or the
+// bucketed plan when asked for).
 #include <algorithm>
 
 #include "plan.h"
@@ -44,8 +46,8 @@ constexpr int kLdsExperts = 4096;  // expert offsets staged in LDS for the row -
 // thus comes out in ascending g with no ordering pass, in time linear in N per workgroup.  A wave
 // whose stash overflows (a heavily skewed index) re-streams its own rows to count them and again
 // in the fill.
-// Every workgroup reading all of idx makes the total work N * P: beyond kTokMaxRows rows the
-// bucketed plan (plan_bucket.hip) takes over.
+// Every workgroup reading all of idx makes the total work N * P: from 2^16 rows the ranged plan
+// takes over, and kTokMaxRows bounds this plan where the ranged plan's limits do not hold.
 constexpr int kTokWaves = kScanThreads / kWave;        // 16
 constexpr int kTokBins = 512;                          // bins per workgroup at most
 constexpr int kTokWaveStash = 256;                     // stashed rows per wave
@@ -841,16 +843,16 @@ int launch_plan_ranged(const Meta& meta, const void* d_indices, int idx_dtype,
 // more, the radix plan, whose cost does not depend on how the rows spread over the tokens (the
 // others give a token's rows to one workgroup or wave); else the one-launch plan below
 // kRangedMinRows rows, where reading all of idx in every workgroup costs less than a second
-// launch; then the ranged plan up to kRangedMaxRows rows (beyond, its ranges outnumber the CUs,
-// one workgroup each, and the bucketed plan is faster), the bucketed plan and the radix plan, each
-// where its limits hold.
-// Top-k routing (k <= 64 rows per token) never takes the radix plan.  Option "plan": 0 automatic,
-// 1 radix, 2 bucketed, 3 one launch, 4 ranged (a forced path whose limits do not hold falls back
-// to the automatic choice).
+// launch; then the ranged plan wherever its limits hold (from 2^21 rows its ranges outnumber the
+// CUs and it is some 7 % slower than the bucketed plan on uniform indices, but a hot token costs it
+// one CU's time, against one wave's in the bucketed plan); then the one-launch plan up to
+// kTokMaxRows rows, and else the radix plan.  The bucketed plan is taken only when asked for.
+// Top-k routing (k <= 64 rows per token) takes the radix plan only beyond the ranged plan's
+// limits.  Option "plan": 0 automatic, 1 radix, 2 bucketed, 3 one launch, 4 ranged (a forced path
+// whose limits do not hold falls back to the automatic choice).
 enum PlanPath { kPathTok, kPathRanged, kPathBucketed, kPathRadix };
 constexpr int64_t kRadixRowsPerToken = 64;
 constexpr int64_t kRangedMinRows = int64_t(1) << 16;
-constexpr int64_t kRangedMaxRows = int64_t(1) << 21;
 bool long_segments(int64_t N, int64_t T) { return N >= kRadixRowsPerToken * (T + 1); }
 PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bins) {
   const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
@@ -863,9 +865,9 @@ PlanPath pick_plan(int64_t N, int64_t T, int64_t E, int64_t* groups, int64_t* bi
   if (algo == 4 && ranged) return kPathRanged;
   if (long_segments(N, T)) return kPathRadix;
   if (tok && N < kRangedMinRows) return kPathTok;
-  if (ranged && N <= kRangedMaxRows) return kPathRanged;
+  if (ranged) return kPathRanged;
   if (tok && N <= fmoe::kTokMaxRows) return kPathTok;
-  return bucketed ? kPathBucketed : kPathRadix;
+  return kPathRadix;
 }
 
 }  // namespace
@@ -926,8 +928,8 @@ extern "C" int fmoe_build_plan(const void* d_indices, int idx_dtype, const void*
   int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.row_ptr);
   Rec* rec = reinterpret_cast<Rec*>(ws + L.rec);
 
-  // The stable one-launch plan, the bucketed plan or the radix plan (pick_plan; tests compare the
-  // paths through the "plan" option).
+  // The one-launch, ranged, bucketed or radix plan (pick_plan; tests compare the paths through the
+  // "plan" option).
   const TokMetaGlobal meta{d_ptr_table, d_offsets};
   int64_t groups = 0, bins = 0;
   const PlanPath path = pick_plan(N, T, E, &groups, &bins);
@@ -1146,11 +1148,10 @@ extern "C" int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, i
   FMOE_REQUIRE(((uintptr_t)d_workspace & 255) == 0,
                "fmoe_invert_scatter_index: workspace not 256B-aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // the bucketed plan (option plan=2, or by default unless the tokens average 64 rows or more),
-  // else the radix plan
+  // the radix plan, or the bucketed plan when asked for (option plan=2) and within its limits
   const int64_t algo = fmoe_host::opt(fmoe_host::kOptPlan);
   const bool bucketed = plan_geom(N, T).ok;
-  if (bucketed && (algo == 2 || (algo != 1 && !long_segments(N, T))))
+  if (bucketed && algo == 2)
     return fmoe_plan::launch_bucketed(nullptr, nullptr, d_indices, idx_dtype, nullptr, FMOE_F32, N,
                                       T, 0, 0, d_workspace, true, d_rows, d_row_ptr, s,
                                       "fmoe_invert_scatter_index");

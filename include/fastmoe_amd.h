@@ -98,10 +98,11 @@ FMOE_API const char* fmoe_last_error(void);
  * environment.  Options select among variants that compute the same results (tests compare them):
  *   "plan"            [FMOE_PLAN]      0 = automatic (the radix plan when the tokens average 64
  *                                      rows or more; else one launch below 2^16 rows, the ranged
- *                                      plan up to 2^21 rows and 2^19 tokens, then the bucketed
- *                                      plan up to 2^22 tokens, the radix plan beyond), 1 = radix (a
- *                                      stable radix sort by token), 2 = bucketed (two launches),
- *                                      3 = one launch, 4 = ranged (two launches)
+ *                                      plan up to 2^22 rows and 2^19 tokens, the radix plan
+ *                                      beyond), 1 = radix (a stable radix sort by token),
+ *                                      2 = bucketed (two launches; never chosen automatically: a
+ *                                      hot token's bucket is ordered by one wave), 3 = one launch,
+ *                                      4 = ranged (two launches)
  *   "bwd_fused"       [FMOE_BWD_FUSED] 1 = both backward gradients in one pass
  *   "gw_staged"       [FMOE_GW_STAGED] 0 = grad_w pass reads grad_out per wave, not through LDS
  *   "force_scalar"    [FMOE_FORCE_SCALAR] 1 = element-wise instead of 16-byte accesses
@@ -143,10 +144,10 @@ FMOE_API int fmoe_build_metadata(const int64_t* host_ptrs, const int64_t* host_r
  * idx[g] == t, each as a 16-byte record {source row address, fp32 gate, g}, in ascending g.  Rows
  * with an out-of-range index form one extra segment (number T).  Time is linear in N + T: one
  * launch below 2^16 rows, two (the ranged plan: partition by token range, then a workgroup per
- * range) up to 2^21 rows and 2^19 tokens, two (the bucketed plan) up to 2^22 tokens, and a stable
- * radix sort of the rows by token (3 launches per 8 bits of T, plus 3 to 5) beyond that or when
- * the tokens average 64 rows or more, whose time does not depend on how the rows spread (option
- * "plan" selects a path).
+ * range) up to 2^22 rows and 2^19 tokens, and a stable radix sort of the rows by token (3 launches
+ * per 8 bits of T, plus 3 to 5) beyond that or when the tokens average 64 rows or more, whose
+ * time does not depend on how the rows spread (option "plan" selects a path, and also offers the
+ * bucketed plan: partition by token bucket, then a wave per bucket).
  *
  * Workspace: fmoe_plan_workspace_bytes(N, T) bytes of device memory, 256-byte aligned, owned by the
  * caller; no zero-fill is needed.  Layout (byte offsets from the workspace base):
@@ -227,8 +228,8 @@ FMOE_API int fmoe_build_metadata_and_plan_from_slots(
  *                            holds the rows whose index lies outside [0, T)
  *   d_rows[N]        int32 : row numbers g, ascending within every segment
  * d_indices : [N] scatter index, FMOE_I64 or FMOE_I32.  Workspace: fmoe_plan_workspace_bytes(N, T)
- * bytes, 256-byte aligned, no zero-fill.  The bucketed or the radix plan, chosen as for the
- * records; linear in N + T either way.
+ * bytes, 256-byte aligned, no zero-fill.  The radix plan, or the bucketed plan with option
+ * plan=2; linear in N + T either way.
  */
 FMOE_API int fmoe_invert_scatter_index(const void* d_indices, int idx_dtype, int64_t num_rows,
                               int64_t num_tokens, int32_t* d_row_ptr, int32_t* d_rows,

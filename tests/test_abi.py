@@ -251,12 +251,13 @@ def test_every_documented_option_reads_and_sets():
 
 
 @pytest.mark.parametrize("N,T,auto", [(32768, 4096, 3), (49152, 8192, 3), (131072, 16384, 4),
-                                      (131072, 1, 1), (131072, 100, 1), (4194304, 131071, 2),
-                                      (2097152, 1048576, 2)])
+                                      (131072, 1, 1), (131072, 100, 1), (4194304, 131071, 4),
+                                      (2097152, 1048576, 1), (4194305, 131071, 1)])
 def test_plan_path_reports_the_builder_taken(N, T, auto):
-    """fmoe_plan_path: the automatic choice by N and T (one launch below 2^16 rows, ranged to
-    2^21, bucketed beyond, radix for tokens averaging 64 rows or more), a forced path where its
-    limits hold, and the automatic choice where they do not."""
+    """fmoe_plan_path: the automatic choice by N and T (one launch below 2^16 rows, ranged up to
+    2^22 rows and 2^19 tokens, radix beyond and for tokens averaging 64 rows or more; never the
+    bucketed plan), a forced path where its limits hold, and the automatic choice where they do
+    not."""
     lib = _abi.lib()
     with _abi.options(plan=0):
         assert lib.fmoe_plan_path(N, T, 256) == auto
@@ -265,5 +266,5 @@ def test_plan_path_reports_the_builder_taken(N, T, auto):
             got = lib.fmoe_plan_path(N, T, 256)
         assert got in (forced, auto)
     with _abi.options(plan=3):
-        assert lib.fmoe_plan_path(2097152, 1048576, 256) == 2  # beyond the one-launch limits
+        assert lib.fmoe_plan_path(2097152, 1048576, 256) == 1  # beyond the one-launch limits
     assert lib.fmoe_plan_path(-1, 4, 1) == -1 and lib.fmoe_plan_path(4, 0, 1) == -1

@@ -927,7 +927,7 @@ def test_metadata_and_plan_in_one_call_equals_two_calls(case):
     """fmoe_build_metadata_and_plan writes exactly what fmoe_build_metadata + fmoe_build_plan
     write: the plan's own launches for up to 256 experts, the two calls otherwise (300 experts,
     or the radix plan: N > 2^20 rows over 4096 tokens averages 256 rows per token; over 65536
-    tokens the bucketed plan takes them in the one call)."""
+    tokens the ranged plan takes them in the one call)."""
     gen = torch.Generator().manual_seed(31)
     D, dtype, idt, wdt = 8, torch.float32, torch.int64, torch.float32
     if case in ("big_n", "big_n_long"):
@@ -971,16 +971,16 @@ def test_metadata_and_plan_in_one_call_equals_two_calls(case):
                 assert np.array_equal(graw[rp1[b]:rp1[b + 1]], g[rp1[b]:rp1[b + 1]])
 
 
-@pytest.mark.parametrize("path", ["auto", "radix"])
+@pytest.mark.parametrize("path", ["auto", "bucketed"])
 @pytest.mark.parametrize("case", ["topk", "long", "one_token", "invalid_i32", "empty", "bigT"])
 def test_invert_scatter_index_matches_oracle(case, path, kernel_options):
     """fmoe_invert_scatter_index: row_ptr and the row list equal the oracle's stable inverse
     exactly -- top-k routing, segments longer than 64 rows (one of 3000 rows), out-of-range int32
     indices, no rows, and T above the LDS histogram (the global count path) -- through the
-    automatic (bucketed) path and the radix plan."""
+    automatic path (the radix plan) and the bucketed plan (option plan=2)."""
     from oracle import cref
 
-    kernel_options(plan=0 if path == "auto" else _PLAN_PATHS["radix"])
+    kernel_options(plan=0 if path == "auto" else _PLAN_PATHS["bucketed"])
     gen = torch.Generator().manual_seed(21)
     if case == "topk":
         _, T, idx, _, _ = _inputs("gigachat")
@@ -1093,13 +1093,13 @@ def test_backward_of_an_expanded_grad_output(kind, D):
     assert np.all(np.abs(grads[0].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
-@pytest.mark.parametrize("path", ["auto", "radix"])
+@pytest.mark.parametrize("path", ["auto", "bucketed"])
 def test_many_experts_beyond_the_lds_tables(path, kernel_options):
     """5000 experts (0-2 rows each): more than the plan's LDS expert tables (4096) and the
     metadata's kernel-argument table (256), so the plan looks experts up in global memory and
-    metadata and plan take separate calls -- the automatic (bucketed) plan and the radix plan;
+    metadata and plan take separate calls -- the automatic plan (radix) and the bucketed plan;
     forward bits, grad_X bits and grad_w against the oracle."""
-    kernel_options(plan=0 if path == "auto" else _PLAN_PATHS["radix"])
+    kernel_options(plan=0 if path == "auto" else _PLAN_PATHS["bucketed"])
     gen = torch.Generator().manual_seed(41)
     E, T, D = 5000, 700, 24
     sizes = torch.randint(0, 3, (E,), generator=gen).tolist()
