@@ -126,15 +126,19 @@ PyObject* versions(PyObject*, PyObject* seq) {
   const Py_ssize_t n = PySequence_Fast_GET_SIZE(fast);
   PyObject** items = PySequence_Fast_ITEMS(fast);
   long long sum = 0;
-  for (Py_ssize_t i = 0; i < n; ++i) {
-    if (!THPVariable_Check(items[i])) {
-      Py_DECREF(fast);
-      PyErr_SetString(PyExc_TypeError, "fastmoe_amd: expected a sequence of tensors");
-      return nullptr;
+  try {
+    for (Py_ssize_t i = 0; i < n; ++i) {
+      if (!THPVariable_Check(items[i])) {
+        PyErr_SetString(PyExc_TypeError, "fastmoe_amd: expected a sequence of tensors");
+        break;
+      }
+      sum += (long long)THPVariable_Unpack(items[i])._version();
     }
-    sum += (long long)THPVariable_Unpack(items[i])._version();
+  } catch (const std::exception& e) {  // e.g. an inference tensor, which has no version counter
+    PyErr_SetString(PyExc_ValueError, e.what());
   }
   Py_DECREF(fast);
+  if (PyErr_Occurred()) return nullptr;
   return PyLong_FromLongLong(sum);
 }
 

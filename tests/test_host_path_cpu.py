@@ -513,3 +513,17 @@ def test_host_helper_version_sum_grows_on_in_place_writes():
     assert _host.versions(xs) > v0
     with pytest.raises(TypeError):
         _host.versions([xs[0], 3])
+
+
+def test_host_helper_inference_tensors_raise_instead_of_crashing():
+    """Inference tensors have no version counter, and their accessor throws a C++ exception: both
+    helpers turn it into a ValueError rather than letting it cross the C API."""
+    from fastmoe_amd import _host
+
+    with torch.inference_mode():
+        xs = [torch.randn(3, 4) for _ in range(2)]
+    assert _host.experts(xs)[1] == 6  # no version counter asked for
+    with pytest.raises(ValueError, match="version counter"):
+        _host.experts(xs, True)
+    with pytest.raises(ValueError, match="version counter"):
+        _host.versions(xs)
