@@ -94,7 +94,7 @@ def _backward(ws, N, T, D, x_dtype, weights, grad_output, expert_sizes):
 # ---- end of the binding ----------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_reference_binding_forward_and_backward(dtype):
     """The reference's in-place call (out.zero_() then _launch_grouped_kernel, the harness of
     run_on_cloud.py:66-92) and its backward, through the raw ctypes binding: top-4 routing of 96
