@@ -156,7 +156,8 @@ void oracle_combine_bwd(const void* const* xs, const int64_t* rows, int64_t E, i
       double dot = 0.0;
       for (int64_t d = 0; d < D; ++d) {
         const float go = valid ? load_f32(grad_out, x_dtype, t * D + d) : 0.0f;
-        if (grad_x) store_f32(grad_x, x_dtype, g * D + d, go * w[g]);
+        /* an out-of-range row's gradient is +0, whatever the sign of its gate */
+        if (grad_x) store_f32(grad_x, x_dtype, g * D + d, valid ? go * w[g] : 0.0f);
         if (grad_w && valid) dot += (double)go * (double)load_f32(xs[e], x_dtype, r * D + d);
       }
       if (grad_w) grad_w[g] = dot;

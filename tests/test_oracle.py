@@ -188,6 +188,13 @@ def test_backward_invalid_rows_get_zero():
     gx, gw = cref.combine_bwd([x.numpy()], idx.numpy(), np.ones(3, np.float32), 2, 4, go.numpy())
     assert np.all(gx[1] == 0) and gw[1] == 0
     np.testing.assert_array_equal(gx[0], go[1].numpy())
+    # the zero is +0 whatever the gate's sign (the kernels store zeros; 0 * w would give -0)
+    for code, dtype in ((cref.F32, torch.float32), (cref.BF16, torch.bfloat16)):
+        xs = [to_np(x.to(dtype))]
+        gx, _ = cref.combine_bwd(xs, idx.numpy(), np.array([1, -2, -1], np.float32), 2, 4,
+                                 to_np(go.to(dtype)), code)
+        raw = gx[1].view(np.uint32) if gx.dtype == np.float32 else gx[1]
+        assert not raw.any()
 
 
 def test_plan_is_stable_argsort():

@@ -178,6 +178,46 @@ def test_bwd_grad_w_staged_equals_per_wave(dtype, D, kernel_options):
     assert np.all(np.abs(got["1"].double().cpu().numpy() - want_gw) <= 1e-6 * scale + 1e-30)
 
 
+# (dtype, D): row lengths that are not multiples of the column step, and D % 8 != 0 (element
+# accesses instead of 16-byte vectors).
+_GX_EDGES = [(torch.bfloat16, 16384), (torch.bfloat16, 7000), (torch.float16, 8200),
+             (torch.float32, 4104), (torch.bfloat16, 7001)]
+
+
+@pytest.mark.parametrize("dtype,D", _GX_EDGES)
+def test_bwd_grad_x_negative_gates_and_out_of_range_rows(dtype, D):
+    """grad_X alone through the C ABI, bit for bit against the oracle, with gates of both signs
+    (an out-of-range row's gradient is +0, not 0 * w = -0), out-of-range indices (the plan's last
+    segment), tokens without rows and a grad_out row stride wider than D."""
+    rng = np.random.default_rng(23 + D)
+    T, E = 301, 29
+    per_token = rng.integers(0, 11, T)
+    idx = np.repeat(np.arange(T), per_token)
+    idx[:: 31] = T + 3
+    idx = torch.from_numpy(idx[rng.permutation(idx.size)])
+    N = idx.numel()
+    gen = torch.Generator().manual_seed(24)
+    sizes = np.diff(np.concatenate([[0], np.sort(rng.integers(0, N + 1, E - 1)), [N]])).tolist()
+    experts = [torch.randn(n, D, generator=gen).to(dtype) for n in sizes]
+    w = torch.rand(N, generator=gen) - 0.5
+    go_wide = torch.randn(T, D + 8, generator=gen).to(dtype)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    meta = fastmoe_amd.prepare_grouped_metadata(xd, DEV)
+    plan = fastmoe_amd.build_plan(meta, idd, wd, T)
+    god = go_wide.to(DEV)
+    code = {torch.float32: fastmoe_amd._abi.F32, torch.bfloat16: fastmoe_amd._abi.BF16,
+            torch.float16: fastmoe_amd._abi.F16}[dtype]
+    gx = torch.full((N, D), float("nan"), dtype=dtype, device=DEV)
+    rc = fastmoe_amd._abi.lib().fmoe_combine_bwd(
+        plan.data_ptr(), N, T, D, code, god.data_ptr(), code, D + 8, gx.data_ptr(), None,
+        fastmoe_amd._abi.F32, torch.cuda.current_stream().cuda_stream)
+    fastmoe_amd._abi.check(rc, "fmoe_combine_bwd")
+    torch.cuda.synchronize()
+    want_gx, _ = oracle_bwd(experts, idx, w, T, go_wide[:, :D].contiguous())
+    np.testing.assert_array_equal(bits(gx), want_gx.view(np.uint32) if want_gx.dtype == np.float32
+                                  else want_gx)
+
+
 @pytest.mark.parametrize("fused", ["0", "1"])
 def test_bwd_abi_both_outputs_in_one_call(fused, kernel_options):
     """fmoe_combine_bwd given both outputs (the call a C-ABI binding makes): grad_X and grad_w
