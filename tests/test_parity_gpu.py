@@ -1537,3 +1537,62 @@ def test_packed_atomics_refuse_16bit_output_without_vector_layout():
     scale = abs_sum([xc], idx, w, T)
     assert np.all(within_one_ulp16(out.float().cpu().numpy(), want16, torch.bfloat16, max(k, 2),
                                    scale))
+
+
+def _as_f32(raw: np.ndarray, dtype) -> np.ndarray:
+    """Values of raw storage bits (uint16 for bf16/f16, float32 otherwise) as float32."""
+    if dtype == torch.bfloat16:
+        return (raw.astype(np.uint32) << 16).view(np.float32)
+    if dtype == torch.float16:
+        return raw.view(np.float16).astype(np.float32)
+    return raw.view(np.float32)
+
+
+def _same_non_finite(got_raw, want_raw, dtype):
+    """NaN where the oracle has NaN (any payload), and the same bits everywhere else (+-Inf too)."""
+    g, w = _as_f32(got_raw, dtype), _as_f32(want_raw, dtype)
+    np.testing.assert_array_equal(np.isnan(g), np.isnan(w))
+    keep = ~np.isnan(w)
+    np.testing.assert_array_equal(got_raw[keep], want_raw[keep])
+
+
+@pytest.mark.parametrize("small", [1, 2], ids=["planned", "small"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_non_finite_values_propagate_like_the_oracle(dtype, small, kernel_options):
+    """+-Inf and NaN in the expert rows and in grad_out: the deterministic forward and grad_X have
+    NaN exactly where the oracle does and the oracle's bits elsewhere (infinities included); grad_w
+    is NaN where the oracle's is and within the usual bar where it is finite."""
+    kernel_options(small=small)
+    wl, T, idx, w, experts = _inputs("gigachat", T=32 if small == 2 else 160)
+    gen = torch.Generator().manual_seed(41)
+    experts = [x.clone() for x in experts]
+    for i, x in enumerate(experts):
+        if x.shape[0] and i % 5 == 0:
+            x[0, i % wl.D] = float("inf")
+            x[-1, (3 * i) % wl.D] = float("nan")
+            x[x.shape[0] // 2, (7 * i) % wl.D] = float("-inf")
+    experts = [x.to(dtype) for x in experts]
+    xd, idd, wd = _to_dev(experts, idx, w)
+    xs = [x.requires_grad_(True) for x in xd]
+    wd.requires_grad_(True)
+    grad_out = torch.randn(T, wl.D, generator=gen)
+    grad_out[1, 5], grad_out[2, 6], grad_out[3, 7] = float("inf"), float("nan"), float("-inf")
+    grad_out = grad_out.to(dtype)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, idd, wd, (T, wl.D), mode="det")
+    grads = torch.autograd.grad(out, [wd, *xs], grad_out.to(DEV))
+    torch.cuda.synchronize()
+    want, _, _ = oracle_fwd(experts, idx, w, T, dtype)
+    want = want.view(np.uint32) if want.dtype == np.float32 else want
+    assert np.isnan(_as_f32(want, dtype)).any() and np.isinf(_as_f32(want, dtype)).any()
+    _same_non_finite(bits(out), want, dtype)
+    want_gx, want_gw = oracle_bwd(experts, idx, w, T, grad_out)
+    want_gx = want_gx.view(np.uint32) if want_gx.dtype == np.float32 else want_gx
+    got_gx = np.concatenate([to_np(g) for g in grads[1:]], 0)
+    got_gx = got_gx.view(np.uint32) if got_gx.dtype == np.float32 else got_gx
+    _same_non_finite(got_gx, want_gx, dtype)
+    gw = grads[0].double().cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(gw), np.isnan(want_gw))
+    fin = np.isfinite(want_gw)
+    np.testing.assert_array_equal(gw[~fin & ~np.isnan(want_gw)], want_gw[~fin & ~np.isnan(want_gw)])
+    scale = abs_dot(experts, idx, grad_out, T)
+    assert np.all(np.abs(gw[fin] - want_gw[fin]) <= 1e-6 * scale[fin] + 1e-30)
