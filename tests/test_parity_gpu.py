@@ -1596,3 +1596,30 @@ def test_non_finite_values_propagate_like_the_oracle(dtype, small, kernel_option
     np.testing.assert_array_equal(gw[~fin & ~np.isnan(want_gw)], want_gw[~fin & ~np.isnan(want_gw)])
     scale = abs_dot(experts, idx, grad_out, T)
     assert np.all(np.abs(gw[fin] - want_gw[fin]) <= 1e-6 * scale[fin] + 1e-30)
+
+
+@pytest.mark.parametrize("small", [1, 2], ids=["planned", "small"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_subnormal_values_are_kept_like_the_oracle(dtype, small, kernel_options):
+    """Expert rows, gates and grad_out scaled into the subnormal range: no stage flushes them to
+    zero, so the deterministic forward and grad_X equal the oracle bit for bit."""
+    kernel_options(small=small)
+    wl, T, idx, w, experts = _inputs("gigachat", T=32 if small == 2 else 160)
+    tiny = 2.0 ** -130  # below float32's (and bfloat16's) smallest normal, 2^-126
+    experts = [(x.float() * tiny).to(dtype) for x in experts]
+    assert any(bool((x.float().abs() < 2.0 ** -126).logical_and(x.float() != 0).any())
+               for x in experts)
+    xd, idd, wd = _to_dev(experts, idx, w)
+    xs = [x.requires_grad_(True) for x in xd]
+    grad_out = (torch.randn(T, wl.D, generator=torch.Generator().manual_seed(43)) * tiny).to(dtype)
+    out = fastmoe_amd.grouped_weighted_scatter_add(xs, idd, wd, (T, wl.D), mode="det")
+    gxs = torch.autograd.grad(out, xs, grad_out.to(DEV))
+    torch.cuda.synchronize()
+    want, _, _ = oracle_fwd(experts, idx, w, T, dtype)
+    got = bits(out)
+    np.testing.assert_array_equal(got, want.view(np.uint32) if want.dtype == np.float32 else want)
+    assert np.count_nonzero(got) > got.size // 2  # most sums are subnormal, not flushed
+    want_gx, _ = oracle_bwd(experts, idx, w, T, grad_out)
+    got_gx = np.concatenate([to_np(g) for g in gxs], 0)
+    np.testing.assert_array_equal(got_gx.view(np.uint32) if got_gx.dtype == np.float32 else got_gx,
+                                  want_gx.view(np.uint32) if want_gx.dtype == np.float32 else want_gx)
